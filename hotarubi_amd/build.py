@@ -1,0 +1,55 @@
+"""Build libhotarubi_gpu.so (gfx950 only) in-tree with hipcc.
+
+    python -m hotarubi_amd.build            # compile
+    python -m hotarubi_amd.build --asm      # also dump gfx950 assembly to _build/
+
+Flags: -ffp-contract=off (no FMA contraction: the exact path depends on
+separately rounded adds and multiplies), -fgpu-flush-denormals-to-zero (FP32
+denormal inputs and results flush, the NPU's FTZ rule), and packed-FP32
+instructions disabled.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libhotarubi_gpu.so")
+SOURCES = ["hb_api.hip", "hb_gemm.hip", "hb_vec.hip"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+DEVICE_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-ffp-contract=off",
+    "-fgpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def build(asm: bool = False, verbose: bool = False) -> str:
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    cmd = [HIPCC, *DEVICE_FLAGS, "-fPIC", "-shared", "-I", os.path.join(ROOT, "include"),
+           "-o", LIB + ".tmp", *srcs]
+    if verbose:
+        print(" ".join(cmd))
+    subprocess.run(cmd, check=True)
+    os.replace(LIB + ".tmp", LIB)
+    if asm:
+        out = os.path.join(ROOT, "_build")
+        os.makedirs(out, exist_ok=True)
+        for s in srcs:
+            name = os.path.splitext(os.path.basename(s))[0]
+            subprocess.run([HIPCC, *DEVICE_FLAGS, "-I", os.path.join(ROOT, "include"),
+                            "--cuda-device-only", "-S", "-o", os.path.join(out, name + ".s"), s],
+                           check=True)
+    return LIB
+
+
+if __name__ == "__main__":
+    build(asm="--asm" in sys.argv, verbose=True)

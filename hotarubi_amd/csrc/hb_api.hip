@@ -1,0 +1,633 @@
+// C ABI of the hotarubi GEMM backend (include/hotarubi_gpu.h): contexts,
+// device images of the on-chip memories, command validation and decoding,
+// and the launches.  Everything computed here is bookkeeping on command
+// fields; all arithmetic on operand data runs in the HIP kernels.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "hb_fp32.h"
+#include "hb_internal.h"
+
+struct hb_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  uint32_t* d_flag = nullptr;  // device flag word for hb_encode_mxint8
+};
+
+struct hb_onchip {
+  hb_ctx* ctx = nullptr;
+  uint8_t* abuf = nullptr;
+  uint8_t* wbuf = nullptr;
+  uint32_t* fbuf = nullptr;
+  uint32_t* pbuf = nullptr;
+  uint64_t* tbuf = nullptr;
+  uint32_t* temp = nullptr;  // one VEC pass: up to 511 quads x 255 words x 32 values
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int Fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int HipFail(hipError_t err, const char* what) {
+  return Fail(HB_EDEVICE, "%s: %s", what, hipGetErrorString(err));
+}
+
+#define HB_HIP(call)                                  \
+  do {                                                \
+    hipError_t e_ = (call);                           \
+    if (e_ != hipSuccess) return HipFail(e_, #call);  \
+  } while (0)
+
+constexpr uint32_t kVecTempWords = 511u * 255u;
+
+struct MemInfo {
+  uint32_t depth, word;
+};
+
+MemInfo Info(int mem) {
+  switch (mem) {
+    case HB_MEM_ABUF: return {HB_ABUF_DEPTH, HB_ABUF_WORD_BYTES};
+    case HB_MEM_WBUF: return {HB_WBUF_DEPTH, HB_WBUF_WORD_BYTES};
+    case HB_MEM_FBUF: return {HB_FBUF_DEPTH, HB_FBUF_WORD_BYTES};
+    case HB_MEM_PBUF: return {HB_PBUF_DEPTH, HB_PBUF_WORD_BYTES};
+    case HB_MEM_TBUF: return {HB_TBUF_DEPTH, HB_TBUF_WORD_BYTES};
+  }
+  return {0, 0};
+}
+
+uint8_t* Image(hb_onchip* o, int mem) {
+  switch (mem) {
+    case HB_MEM_ABUF: return o->abuf;
+    case HB_MEM_WBUF: return o->wbuf;
+    case HB_MEM_FBUF: return reinterpret_cast<uint8_t*>(o->fbuf);
+    case HB_MEM_PBUF: return reinterpret_cast<uint8_t*>(o->pbuf);
+    case HB_MEM_TBUF: return reinterpret_cast<uint8_t*>(o->tbuf);
+  }
+  return nullptr;
+}
+
+// Preconditions of ExecuteGemm (tools/iss/gemm_array.cpp:113-119), with the
+// reference's messages.
+int CheckGemm(const hb_gemm_cmd* c) {
+  if (!(c->m >= 32 && c->m <= 992 && c->m % 32 == 0))
+    return Fail(HB_EBADCMD, "GEMM m = %u is not a multiple of 32 from 32 to 992", c->m);
+  if (!(c->kb >= 1 && c->kb <= c->a_stride))
+    return Fail(HB_EBADCMD, "GEMM kb = %u is not in [1, a_stride = %u]", c->kb, c->a_stride);
+  if (c->n8 < 1) return Fail(HB_EBADCMD, "GEMM n8 = 0");
+  return HB_OK;
+}
+
+uint32_t Field(const uint8_t w[16], uint32_t lsb, uint32_t width) {
+  uint64_t lo = 0, hi = 0;
+  for (int i = 7; i >= 0; --i) lo = (lo << 8) | w[i];
+  for (int i = 15; i >= 8; --i) hi = (hi << 8) | w[i];
+  uint64_t v;
+  if (lsb >= 64) v = hi >> (lsb - 64);
+  else if (lsb == 0) v = lo;
+  else v = (lo >> lsb) | (hi << (64 - lsb));
+  return (uint32_t)(v & ((1ull << width) - 1ull));
+}
+
+void SetField(uint8_t w[16], uint32_t lsb, uint32_t width, uint32_t value) {
+  for (uint32_t i = 0; i < width; ++i) {
+    const uint32_t bit = lsb + i;
+    const uint8_t mask = (uint8_t)(1u << (bit & 7));
+    if ((value >> i) & 1u) w[bit >> 3] |= mask;
+    else w[bit >> 3] &= (uint8_t)~mask;
+  }
+}
+
+int Enter(hb_ctx* ctx) {
+  if (!ctx) return Fail(HB_EINVAL, "null context");
+  HB_HIP(hipSetDevice(ctx->device));
+  return HB_OK;
+}
+
+hb::GemmArgs InstrArgs(const hb_gemm_cmd* cmd, hb_onchip* o) {
+  hb::GemmArgs g;
+  std::memset(&g, 0, sizeof g);
+  g.a = o->abuf;
+  g.w[0] = o->wbuf;
+  g.w[1] = o->wbuf;
+  g.c = o->fbuf;
+  g.quads = cmd->m / 4;
+  g.groups = cmd->n8;
+  g.m = cmd->m;
+  g.n = cmd->n8 * 8;
+  g.a_base = cmd->a_base;
+  g.a_stride = cmd->a_stride;
+  g.w_base = cmd->w_base;
+  g.w_stride = cmd->w_stride;
+  g.c_base = cmd->c_base;
+  g.n_pieces = 1;
+  g.piece_off[0] = 0;
+  g.piece_kb[0] = cmd->kb;
+  g.n_planes = 1;
+  g.modes[0] = hb::DecodeMode(cmd->wmode);
+  g.total_steps = cmd->kb;
+  g.acc = cmd->acc ? 1u : 0u;
+  return g;
+}
+
+int GemmExec(hb_ctx* ctx, const hb_gemm_cmd* cmd, hb_onchip* o, bool sync) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!cmd || !o) return Fail(HB_EINVAL, "null argument");
+  if (int rc = CheckGemm(cmd)) return rc;
+  const hb::GemmArgs g = InstrArgs(cmd, o);
+  const uint64_t words = (uint64_t)g.quads * g.groups;
+  hipError_t err = words <= hb::kFbufDepth ? hb::LaunchGemmInstr(g, ctx->stream)
+                                           : hb::LaunchGemmInstrAliased(g, ctx->stream);
+  if (err != hipSuccess) return HipFail(err, "GEMM launch");
+  if (sync) HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+
+// ---- VEC: the passes of library entries 0-9 (tools/compiler/vec_rom.cpp:
+// 63-70 Whole(), 214-237 Activation(), 314-349 Program()) ----
+
+enum { kRSrc = 1, kRSrc2 = 2, kRDst = 3, kRImm = 8 };
+
+struct PassSpec {
+  uint32_t rx, rx2, rd;  // registers
+  uint32_t c0, b, act, po, pv, rowvec, rimm;
+  bool final_;
+};
+
+int LibraryPasses(uint32_t entry, PassSpec* out) {
+  PassSpec p{kRSrc, 0, kRDst, 0, 0, 0, 0, 0, 0, 0, true};
+  switch (entry) {
+    case 0: p.rx2 = kRSrc2; p.c0 = 1; break;               // ADD
+    case 1: p.rx2 = kRSrc2; p.b = 1; break;                // MUL
+    case 2: p.rx2 = kRSrc2; p.po = 1; p.pv = 1; break;     // MAX
+    case 3: p.rowvec = 1; p.c0 = 2; break;                 // ADDP
+    case 4: p.rowvec = 1; p.b = 2; break;                  // MULP
+    case 5: p.rimm = kRImm; p.b = 3; break;                // SCALE
+    case 6: break;                                         // COPY
+    case 7: p.po = 1; break;                               // RELU
+    case 8:
+    case 9: {                                              // ACT, ACT_MUL
+      PassSpec sigma{kRSrc, 0, kRImm, 0, 0, 1, 0, 0, 0, 0, false};
+      PassSpec gate{kRSrc, kRImm, kRDst, 0, 1, 0, 2, 0, 0, 0, true};
+      out[0] = sigma;
+      if (entry == 8) {
+        out[1] = gate;
+        return 2;
+      }
+      gate.rd = kRImm;
+      gate.final_ = false;
+      out[1] = gate;
+      out[2] = PassSpec{kRImm, kRSrc2, kRDst, 0, 1, 0, 0, 0, 0, 0, true};
+      return 3;
+    }
+    default: return 0;
+  }
+  out[0] = p;
+  return 1;
+}
+
+// The failure checks of RunPass/RunQuads/RunWord/Store (vec_engine.cpp:
+// 252-460) in program order, on addresses only.
+int CheckPass(const hb::VecPass& p, const PassSpec& s) {
+  if (p.quads == 0 || p.words == 0)
+    return Fail(HB_EBADCMD, "a PASS has %u quads and %u words", p.quads, p.words);
+  const uint32_t total = p.quads * p.words;
+  if (!p.to_abuf) {
+    std::vector<uint8_t> written(hb::kFbufDepth, 0);
+    for (uint32_t i = 0; i < total; ++i) {
+      const uint32_t xa = (p.src + i) & (hb::kFbufDepth - 1);
+      if (written[xa]) return Fail(HB_EBADCMD, "a PASS reads FBUF word %u after writing it", xa);
+      if (p.x2_en) {
+        const uint32_t x2a = (p.src2 + i) & (hb::kFbufDepth - 1);
+        if (written[x2a])
+          return Fail(HB_EBADCMD, "a PASS reads FBUF word %u after writing it", x2a);
+      }
+      written[(p.d + i) & (hb::kFbufDepth - 1)] = 1;
+    }
+  } else if (p.n8 % 4 != 0) {
+    if (p.quads >= 2) return Fail(HB_EBADCMD, "quantized word 0 arrives out of order");
+    return Fail(HB_EBADCMD, "a PASS ends inside a block of 4 quantized words");
+  }
+  (void)s;
+  return HB_OK;
+}
+
+int VecExec(hb_ctx* ctx, const hb_vec_cmd* cmd, hb_onchip* o) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!cmd || !o) return Fail(HB_EINVAL, "null argument");
+  PassSpec specs[3];
+  const int n = LibraryPasses(cmd->entry, specs);
+  if (n == 0)
+    return Fail(HB_EUNSUPPORTED, "VEC library entry %u is not an epilogue program (0-9)",
+                cmd->entry);
+  // VecEngine::Initialize (vec_engine.cpp:227-239): operand field widths.
+  uint32_t reg[16] = {0};
+  reg[kRSrc] = cmd->src & 0xFFFu;
+  reg[kRSrc2] = cmd->src2 & 0xFFFu;
+  reg[kRDst] = cmd->dst & 0x1FFFu;
+  reg[kRImm] = cmd->imm;
+  const uint32_t rows_q = cmd->rows_q & 0x1FFu, n8 = cmd->n8 & 0xFFu;
+  const uint32_t p_base = cmd->p_base & 0x1FFu;
+  hb::VecPass passes[3];
+  for (int i = 0; i < n; ++i) {
+    const PassSpec& s = specs[i];
+    hb::VecPass& p = passes[i];
+    std::memset(&p, 0, sizeof p);
+    p.src = reg[s.rx] & 0xFFFu;
+    p.src2 = reg[s.rx2] & 0xFFFu;
+    p.x2_en = s.rx2 != 0;
+    p.d = reg[s.rd];
+    p.c0 = s.c0;
+    p.b = s.b;
+    p.act = s.act;
+    p.po = s.po;
+    p.pv = s.pv;
+    p.imm = reg[s.rimm];
+    p.pb = p_base;
+    p.quads = rows_q;
+    p.words = n8;
+    p.n8 = n8;
+    p.to_abuf = s.final_ && cmd->quantize;
+    p.d = p.to_abuf ? (p.d & (hb::kAbufDepth - 1)) : (p.d & (hb::kFbufDepth - 1));
+    if (int rc = CheckPass(p, s)) return rc;
+  }
+  for (int i = 0; i < n; ++i) {
+    hipError_t err =
+        hb::LaunchVecPass(passes[i], o->abuf, o->fbuf, o->pbuf, o->tbuf, o->temp, ctx->stream);
+    if (err != hipSuccess) return HipFail(err, "VEC launch");
+  }
+  HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+
+// ---- linear ----
+
+bool ValidMode(uint32_t m) { return m <= 2; }
+
+int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g) {
+  if (!d) return Fail(HB_EINVAL, "null descriptor");
+  if (d->m < 1 || d->n < 8 || d->n % 8 != 0 || d->kb_total < 1)
+    return Fail(HB_EINVAL, "linear m = %u, n = %u, kb_total = %u: need m >= 1, n %% 8 == 0",
+                d->m, d->n, d->kb_total);
+  if (d->n_planes < 1 || d->n_planes > 2) return Fail(HB_EINVAL, "n_planes = %u", d->n_planes);
+  for (uint32_t l = 0; l < d->n_planes; ++l)
+    if (!ValidMode(d->modes[l]) || !d->w[l])
+      return Fail(HB_EINVAL, "plane %u: mode %u / weights missing", l, d->modes[l]);
+  if (d->n_pieces < 1 || d->n_pieces > HB_MAX_PIECES)
+    return Fail(HB_EINVAL, "n_pieces = %u", d->n_pieces);
+  uint64_t steps = 0;
+  for (uint32_t p = 0; p < d->n_pieces; ++p) {
+    const hb_piece& pc = d->pieces[p];
+    if (pc.kb < 1 || (uint64_t)pc.kb_offset + pc.kb > d->kb_total)
+      return Fail(HB_EINVAL, "piece %u [%u, +%u) is outside %u blocks", p, pc.kb_offset, pc.kb,
+                  d->kb_total);
+    steps += (uint64_t)pc.kb * d->n_planes;
+  }
+  if (steps > 8192) return Fail(HB_EINVAL, "%llu fold steps exceed 8192", (unsigned long long)steps);
+  if (!d->a || !d->c) return Fail(HB_EINVAL, "null A or C");
+  if (d->n_ops > HB_MAX_EP_OPS) return Fail(HB_EINVAL, "n_ops = %u", d->n_ops);
+  if (d->q_out && d->n % 32 != 0) return Fail(HB_EINVAL, "quantized output needs n %% 32 == 0");
+  if (d->flags > HB_LINEAR_FAST) return Fail(HB_EINVAL, "flags = %u", d->flags);
+  std::memset(g, 0, sizeof *g);
+  for (uint32_t o = 0; o < d->n_ops; ++o) {
+    const hb_ep_op& op = d->ops[o];
+    switch (op.op) {
+      case HB_EP_ADDP:
+      case HB_EP_MULP:
+        if (!op.vec) return Fail(HB_EINVAL, "op %u needs a column vector", o);
+        break;
+      case HB_EP_ACT_MUL:
+      case HB_EP_ADD:
+        if (!op.x2) return Fail(HB_EINVAL, "op %u needs x2", o);
+        [[fallthrough]];
+      case HB_EP_ACT:
+        if (op.op != HB_EP_ADD && !d->tbuf) return Fail(HB_EINVAL, "op %u needs TBUF", o);
+        break;
+      case HB_EP_SCALE:
+      case HB_EP_COPY:
+      case HB_EP_RELU:
+        break;
+      default: return Fail(HB_EUNSUPPORTED, "epilogue op %u is not supported", op.op);
+    }
+    g->op_kind[o] = op.op;
+    g->op_imm[o] = op.imm;
+    g->op_vec[o] = reinterpret_cast<const uint32_t*>(op.vec);
+    g->op_x2[o] = reinterpret_cast<const uint32_t*>(op.x2);
+  }
+  g->n_ops = d->n_ops;
+  g->a = static_cast<const uint8_t*>(d->a);
+  g->w[0] = static_cast<const uint8_t*>(d->w[0]);
+  g->w[1] = static_cast<const uint8_t*>(d->n_planes > 1 ? d->w[1] : d->w[0]);
+  g->c = reinterpret_cast<uint32_t*>(d->c);
+  g->quads = (d->m + 3) / 4;
+  g->groups = d->n / 8;
+  g->m = d->m;
+  g->n = d->n;
+  g->kb_total = d->kb_total;
+  g->n_pieces = d->n_pieces;
+  for (uint32_t p = 0; p < d->n_pieces; ++p) {
+    g->piece_off[p] = d->pieces[p].kb_offset;
+    g->piece_kb[p] = d->pieces[p].kb;
+  }
+  g->n_planes = d->n_planes;
+  g->modes[0] = d->modes[0];
+  g->modes[1] = d->n_planes > 1 ? d->modes[1] : d->modes[0];
+  g->total_steps = (uint32_t)steps;
+  g->acc = d->onto ? 1u : 0u;
+  g->tbuf = d->tbuf;
+  g->q_out = static_cast<uint8_t*>(d->q_out);
+  return HB_OK;
+}
+
+template <class T>
+uint64_t Diff(const T* a, const T* b) {
+  return (uint64_t)(reinterpret_cast<const uint8_t*>(b) - reinterpret_cast<const uint8_t*>(a));
+}
+
+}  // namespace
+
+extern "C" {
+
+int hb_abi_version(void) { return HB_ABI_VERSION; }
+
+const char* hb_last_error(void) { return g_error.c_str(); }
+
+int hb_ctx_create(int device, hb_ctx** out) {
+  if (!out) return Fail(HB_EINVAL, "null output");
+  int count = 0;
+  HB_HIP(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count) return Fail(HB_EINVAL, "device %d of %d", device, count);
+  HB_HIP(hipSetDevice(device));
+  hb_ctx* ctx = new (std::nothrow) hb_ctx;
+  if (!ctx) return Fail(HB_ENOMEM, "context");
+  ctx->device = device;
+  hipError_t err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (err == hipSuccess) err = hipMalloc(&ctx->d_flag, sizeof(uint32_t));
+  if (err != hipSuccess) {
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return HipFail(err, "context create");
+  }
+  ctx->own_stream = true;
+  *out = ctx;
+  return HB_OK;
+}
+
+int hb_ctx_destroy(hb_ctx* ctx) {
+  if (!ctx) return HB_OK;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->d_flag) (void)hipFree(ctx->d_flag);
+  if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return HB_OK;
+}
+
+int hb_ctx_set_stream(hb_ctx* ctx, void* hip_stream) {
+  if (int rc = Enter(ctx)) return rc;
+  if (ctx->own_stream && ctx->stream) {
+    HB_HIP(hipStreamSynchronize(ctx->stream));
+    HB_HIP(hipStreamDestroy(ctx->stream));
+  }
+  ctx->stream = static_cast<hipStream_t>(hip_stream);
+  ctx->own_stream = false;
+  return HB_OK;
+}
+
+int hb_ctx_synchronize(hb_ctx* ctx) {
+  if (int rc = Enter(ctx)) return rc;
+  HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+
+int hb_onchip_create(hb_ctx* ctx, hb_onchip** out) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!out) return Fail(HB_EINVAL, "null output");
+  hb_onchip* o = new (std::nothrow) hb_onchip;
+  if (!o) return Fail(HB_ENOMEM, "onchip");
+  o->ctx = ctx;
+  hipError_t err = hipSuccess;
+  const size_t sizes[5] = {(size_t)HB_ABUF_DEPTH * HB_ABUF_WORD_BYTES,
+                           (size_t)HB_WBUF_DEPTH * HB_WBUF_WORD_BYTES,
+                           (size_t)HB_FBUF_DEPTH * HB_FBUF_WORD_BYTES,
+                           (size_t)HB_PBUF_DEPTH * HB_PBUF_WORD_BYTES,
+                           (size_t)HB_TBUF_DEPTH * HB_TBUF_WORD_BYTES};
+  void** ptrs[5] = {(void**)&o->abuf, (void**)&o->wbuf, (void**)&o->fbuf, (void**)&o->pbuf,
+                    (void**)&o->tbuf};
+  for (int i = 0; i < 5 && err == hipSuccess; ++i) {
+    err = hipMalloc(ptrs[i], sizes[i]);
+    if (err == hipSuccess) err = hipMemsetAsync(*ptrs[i], 0, sizes[i], ctx->stream);
+  }
+  if (err == hipSuccess) err = hipMalloc(&o->temp, (size_t)kVecTempWords * 128);
+  if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+  if (err != hipSuccess) {
+    hb_onchip_destroy(o);
+    return HipFail(err, "onchip create");
+  }
+  *out = o;
+  return HB_OK;
+}
+
+int hb_onchip_destroy(hb_onchip* o) {
+  if (!o) return HB_OK;
+  if (o->ctx) {
+    (void)hipSetDevice(o->ctx->device);
+    (void)hipStreamSynchronize(o->ctx->stream);
+  }
+  void* ptrs[6] = {o->abuf, o->wbuf, o->fbuf, o->pbuf, o->tbuf, o->temp};
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  delete o;
+  return HB_OK;
+}
+
+static int Transfer(hb_onchip* o, int mem, uint32_t first, uint32_t count, void* host,
+                    bool upload) {
+  if (!o) return Fail(HB_EINVAL, "null onchip");
+  if (int rc = Enter(o->ctx)) return rc;
+  const MemInfo info = Info(mem);
+  if (info.depth == 0) return Fail(HB_EINVAL, "memory id %d", mem);
+  if ((uint64_t)first + count > info.depth)
+    return Fail(HB_EINVAL, "words [%u, %u) outside depth %u", first, first + count, info.depth);
+  if (count == 0) return HB_OK;
+  if (!host) return Fail(HB_EINVAL, "null host buffer");
+  uint8_t* dev = Image(o, mem) + (size_t)first * info.word;
+  const size_t bytes = (size_t)count * info.word;
+  if (upload)
+    HB_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, o->ctx->stream));
+  else
+    HB_HIP(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, o->ctx->stream));
+  HB_HIP(hipStreamSynchronize(o->ctx->stream));
+  return HB_OK;
+}
+
+int hb_onchip_upload(hb_onchip* o, int mem, uint32_t first, uint32_t count, const void* host) {
+  return Transfer(o, mem, first, count, const_cast<void*>(host), true);
+}
+
+int hb_onchip_download(hb_onchip* o, int mem, uint32_t first, uint32_t count, void* host) {
+  return Transfer(o, mem, first, count, host, false);
+}
+
+int hb_onchip_device_ptr(hb_onchip* o, int mem, void** device) {
+  if (!o || !device) return Fail(HB_EINVAL, "null argument");
+  if (Info(mem).depth == 0) return Fail(HB_EINVAL, "memory id %d", mem);
+  *device = Image(o, mem);
+  return HB_OK;
+}
+
+int hb_gemm_decode(const uint8_t word[16], hb_gemm_cmd* out) {
+  if (!word || !out) return Fail(HB_EINVAL, "null argument");
+  const uint32_t opcode = Field(word, 120, 8);
+  if (opcode != 4) return Fail(HB_EINVAL, "opcode %u is not GEMM (4)", opcode);
+  // isa::gemm field map (include/hotarubi/isa.hpp:75-84)
+  out->a_base = Field(word, 92, 20);
+  out->a_stride = Field(word, 82, 10);
+  out->kb = Field(word, 72, 10);
+  out->m = Field(word, 62, 10);
+  out->w_base = Field(word, 42, 20);
+  out->w_stride = Field(word, 32, 10);
+  out->n8 = Field(word, 24, 8);
+  out->c_base = Field(word, 4, 20);
+  out->wmode = Field(word, 2, 2);
+  out->acc = Field(word, 1, 1);
+  return HB_OK;
+}
+
+int hb_gemm_encode(const hb_gemm_cmd* c, uint8_t word[16]) {
+  if (!c || !word) return Fail(HB_EINVAL, "null argument");
+  std::memset(word, 0, 16);
+  SetField(word, 120, 8, 4);
+  SetField(word, 92, 20, c->a_base);
+  SetField(word, 82, 10, c->a_stride);
+  SetField(word, 72, 10, c->kb);
+  SetField(word, 62, 10, c->m);
+  SetField(word, 42, 20, c->w_base);
+  SetField(word, 32, 10, c->w_stride);
+  SetField(word, 24, 8, c->n8);
+  SetField(word, 4, 20, c->c_base);
+  SetField(word, 2, 2, c->wmode);
+  SetField(word, 1, 1, c->acc ? 1u : 0u);
+  return HB_OK;
+}
+
+int hb_gemm_check(const hb_gemm_cmd* cmd) {
+  if (!cmd) return Fail(HB_EINVAL, "null command");
+  return CheckGemm(cmd);
+}
+
+int hb_gemm_access(const hb_gemm_cmd* cmd, uint8_t* ra, uint8_t* rw, uint8_t* rf, uint8_t* wf) {
+  if (!cmd) return Fail(HB_EINVAL, "null command");
+  if (int rc = CheckGemm(cmd)) return rc;
+  if (ra) std::memset(ra, 0, HB_ABUF_DEPTH);
+  if (rw) std::memset(rw, 0, HB_WBUF_DEPTH);
+  if (rf) std::memset(rf, 0, HB_FBUF_DEPTH);
+  if (wf) std::memset(wf, 0, HB_FBUF_DEPTH);
+  const uint32_t mask = hb::kAddrMask;
+  for (uint32_t g = 0; g < cmd->n8; ++g) {
+    if (rw)
+      for (uint32_t b = 0; b < cmd->kb; ++b)
+        rw[((cmd->w_base + g * cmd->w_stride + b) & mask) % HB_WBUF_DEPTH] = 1;
+    for (uint32_t q = 0; q < cmd->m / 4; ++q) {
+      const uint32_t c = ((cmd->c_base + q * cmd->n8 + g) & mask) % HB_FBUF_DEPTH;
+      if (rf && cmd->acc) rf[c] = 1;
+      if (ra)
+        for (uint32_t b = 0; b < cmd->kb; ++b)
+          ra[((cmd->a_base + q * cmd->a_stride + b) & mask) % HB_ABUF_DEPTH] = 1;
+      if (wf) wf[c] = 1;
+    }
+  }
+  return HB_OK;
+}
+
+int hb_gemm_exec(hb_ctx* ctx, const hb_gemm_cmd* cmd, hb_onchip* o) {
+  return GemmExec(ctx, cmd, o, true);
+}
+
+int hb_gemm_exec_async(hb_ctx* ctx, const hb_gemm_cmd* cmd, hb_onchip* o) {
+  return GemmExec(ctx, cmd, o, false);
+}
+
+uint64_t hb_gemm_cycles(const hb_gemm_cmd* c, uint32_t fixed_cycles) {
+  if (!c) return 0;
+  return (uint64_t)c->n8 * (c->m / 32) * c->kb * 8u + fixed_cycles;
+}
+
+int hb_vec_exec(hb_ctx* ctx, const hb_vec_cmd* cmd, hb_onchip* o) { return VecExec(ctx, cmd, o); }
+
+int hb_linear_async(hb_ctx* ctx, const hb_linear_desc* d) {
+  if (int rc = Enter(ctx)) return rc;
+  hb::GemmArgs g;
+  if (int rc = LinearArgs(d, &g)) return rc;
+  hipError_t err = hb::LaunchLinear(g, 1, d->flags == HB_LINEAR_FAST, ctx->stream);
+  if (err != hipSuccess) return HipFail(err, "linear launch");
+  return HB_OK;
+}
+
+int hb_linear(hb_ctx* ctx, const hb_linear_desc* d) {
+  if (int rc = hb_linear_async(ctx, d)) return rc;
+  HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+
+int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!d || count < 1) return Fail(HB_EINVAL, "no layers");
+  hb::GemmArgs g;
+  if (int rc = LinearArgs(&d[0], &g)) return rc;
+  if (count > 1) {
+    if (d[0].n_ops != 0 || d[0].onto)
+      return Fail(HB_EUNSUPPORTED, "batched layers take no epilogue ops and no onto");
+    g.a_batch = Diff(d[0].a, d[1].a);
+    g.w_batch = Diff(d[0].w[0], d[1].w[0]);
+    g.c_batch = Diff(d[0].c, d[1].c) / 4;
+    g.q_batch = d[0].q_out ? Diff(d[0].q_out, d[1].q_out) : 0;
+    for (uint32_t i = 1; i < count; ++i) {
+      const hb_linear_desc& x = d[i];
+      const bool same = x.m == d[0].m && x.n == d[0].n && x.kb_total == d[0].kb_total &&
+                        x.n_planes == d[0].n_planes && x.flags == d[0].flags &&
+                        x.n_ops == 0 && !x.onto && (x.q_out != nullptr) == (d[0].q_out != nullptr) &&
+                        Diff(d[0].a, x.a) == i * g.a_batch &&
+                        Diff(d[0].w[0], x.w[0]) == i * g.w_batch &&
+                        (x.n_planes < 2 || Diff(d[0].w[1], x.w[1]) == i * g.w_batch) &&
+                        Diff(d[0].c, x.c) == i * g.c_batch * 4 &&
+                        (!x.q_out || Diff(d[0].q_out, x.q_out) == i * g.q_batch);
+      if (!same) return Fail(HB_EINVAL, "layer %u differs in shape or stride", i);
+    }
+  }
+  hipError_t err = hb::LaunchLinear(g, count, d[0].flags == HB_LINEAR_FAST, ctx->stream);
+  if (err != hipSuccess) return HipFail(err, "linear launch");
+  return HB_OK;
+}
+
+int hb_encode_mxint8(hb_ctx* ctx, const float* x, uint32_t rows, uint32_t cols, void* out) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!x || !out || rows < 1 || cols < 1) return Fail(HB_EINVAL, "bad encode arguments");
+  HB_HIP(hipMemsetAsync(ctx->d_flag, 0, sizeof(uint32_t), ctx->stream));
+  hipError_t err = hb::LaunchEncodeMxint8(x, rows, cols, static_cast<uint8_t*>(out),
+                                          ctx->d_flag, ctx->stream);
+  if (err != hipSuccess) return HipFail(err, "encode launch");
+  uint32_t flag = 0;
+  HB_HIP(hipMemcpyAsync(&flag, ctx->d_flag, sizeof flag, hipMemcpyDeviceToHost, ctx->stream));
+  HB_HIP(hipStreamSynchronize(ctx->stream));
+  if (flag) return Fail(HB_EINVAL, "MXINT8 input is infinite or NaN");
+  return HB_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,329 @@
+"""ctypes binding of the CPU oracle (oracle/hb_oracle.c) -- test infrastructure.
+
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg import
+this package, and only as the checker.  The product (hotarubi_amd) never does.
+
+`ref()` returns the reference's own FP32 code compiled from /root/reference
+into oracle/_ref (see oracle/Makefile), or None where it was not built.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libref_fp32.so")
+
+u8p = C.POINTER(C.c_uint8)
+u32p = C.POINTER(C.c_uint32)
+i32p = C.POINTER(C.c_int32)
+i8p = C.POINTER(C.c_int8)
+u64p = C.POINTER(C.c_uint64)
+
+
+class GemmCmd(C.Structure):
+    """Mirrors iss::GemmCommand (tools/iss/gemm_array.hpp:16-27)."""
+
+    _fields_ = [(n, C.c_uint32) for n in
+                ("a_base", "a_stride", "kb", "m", "w_base", "w_stride", "n8",
+                 "c_base", "wmode", "acc")]
+
+
+class VecCmd(C.Structure):
+    """Mirrors iss::VecCommand (tools/iss/vec_engine.hpp:70-81)."""
+
+    _fields_ = [(n, C.c_uint32) for n in
+                ("entry", "quantize", "src", "src2", "dst", "rows_q", "n8",
+                 "p_base", "aux", "imm")]
+
+
+class EpOp(C.Structure):
+    _fields_ = [("op", C.c_uint32), ("imm", C.c_uint32), ("vec", u32p),
+                ("x2", u32p)]
+
+
+class Piece(C.Structure):
+    _fields_ = [("kb_offset", C.c_uint32), ("kb", C.c_uint32)]
+
+
+EP_ADDP, EP_MULP, EP_SCALE, EP_COPY, EP_RELU, EP_ACT, EP_ACT_MUL = 3, 4, 5, 6, 7, 8, 9
+EP_ADD = 0x100
+
+ABUF_DEPTH, WBUF_DEPTH, FBUF_DEPTH, PBUF_DEPTH, TBUF_DEPTH = 8192, 2048, 4096, 512, 1024
+
+_lib = None
+_ref = None
+
+
+def build(quiet: bool = True) -> None:
+    """Compile the oracle (and oracle/_ref when the reference tree exists)."""
+    targets = ["all"]
+    if os.path.isdir("/root/reference"):
+        targets.append("ref")
+    subprocess.run(["make", "-s", "-C", HERE, *targets], check=True,
+                   stdout=subprocess.DEVNULL if quiet else None)
+
+
+def _ptr(arr, typ):
+    return arr.ctypes.data_as(typ)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in [
+            ("hbo_last_error", C.c_char_p, []),
+            ("hbo_fp32_add", C.c_uint32, [C.c_uint32, C.c_uint32]),
+            ("hbo_fp32_mul", C.c_uint32, [C.c_uint32, C.c_uint32]),
+            ("hbo_fp32_mul_fraction", C.c_uint32, [C.c_uint32, C.c_uint32]),
+            ("hbo_decode_weight_mode", C.c_uint32, [C.c_uint32]),
+            ("hbo_weight_value", C.c_int32, [C.c_uint32, C.c_uint32]),
+            ("hbo_block_value", C.c_uint32, [C.c_int32, C.c_uint32, C.c_uint32, C.c_uint32]),
+            ("hbo_gemm_exec", C.c_int, [C.POINTER(GemmCmd), u8p, u8p, u32p]),
+            ("hbo_gemm_access", C.c_int, [C.POINTER(GemmCmd), u8p, u8p, u8p, u8p]),
+            ("hbo_quantize_int8", C.c_int8, [C.c_uint32, C.c_int32]),
+            ("hbo_encode_mxint8", C.c_int, [u32p, C.c_uint32, C.c_uint32, i8p, i32p]),
+            ("hbo_pack_abuf", C.c_int, [i8p, i32p, C.c_uint32, C.c_uint32, u8p]),
+            ("hbo_pack_fbuf", C.c_int, [u32p, C.c_uint32, C.c_uint32, u32p]),
+            ("hbo_unpack_fbuf", C.c_int, [u32p, C.c_uint32, C.c_uint32, u32p]),
+            ("hbo_pack_wbuf", C.c_int, [u8p, i32p, C.c_uint32, C.c_uint32, u8p]),
+            ("hbo_split_w8", None, [i8p, C.c_size_t, u8p, u8p]),
+            ("hbo_canonical_mxfp4", C.c_int, [u8p, i32p, C.c_uint32, C.c_uint32, C.c_int32,
+                                              C.c_uint32, u8p, i32p]),
+            ("hbo_interpolate", C.c_uint32, [C.c_uint64, C.c_uint32]),
+            ("hbo_activation", C.c_uint32, [C.c_uint32, u64p]),
+            ("hbo_post_add", C.c_uint32, [C.c_uint32, C.c_uint32, C.c_uint32]),
+            ("hbo_quantize_element", C.c_uint8, [C.c_uint32, C.c_uint32]),
+            ("hbo_quantize_block", C.c_int, [u32p, u8p]),
+            ("hbo_vec_exec", C.c_int, [C.POINTER(VecCmd), u8p, u32p, u32p, u64p]),
+            ("hbo_linear", C.c_int, [C.c_uint32, C.c_uint32, C.c_uint32, u8p, C.c_uint32,
+                                     C.POINTER(u8p), u32p, C.c_uint32, C.POINTER(Piece),
+                                     C.c_int, u32p, C.c_uint32, C.POINTER(EpOp), u64p, u8p]),
+            ("hbo_gemm_cycles", C.c_uint64, [C.POINTER(GemmCmd), C.c_uint32]),
+            ("hbo_fp32_add_n", None, [u32p, u32p, u32p, C.c_uint64]),
+            ("hbo_fp32_mul_n", None, [u32p, u32p, u32p, C.c_uint64]),
+            ("hbo_fp32_mul_fraction_n", None, [u32p, u32p, u32p, C.c_uint64]),
+            ("hbo_block_value_n", None, [i32p, u32p, u32p, C.c_uint32, u32p, C.c_uint64]),
+        ]:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def ref():
+    """The reference's compiled FP32 code (oracle/_ref), or None."""
+    global _ref
+    if _ref is None and os.path.exists(REF_PATH):
+        R = C.CDLL(REF_PATH)
+        for name in ("ref_iss_fp32_add", "ref_iss_fp32_mul", "ref_iss_fp32_mul_fraction",
+                     "ref_tb_fp32_add", "ref_tb_fp32_mul"):
+            getattr(R, name).restype = C.c_uint32
+            getattr(R, name).argtypes = [C.c_uint32, C.c_uint32]
+        R.ref_tb_fp32_from_int.restype = C.c_uint32
+        R.ref_tb_fp32_from_int.argtypes = [C.c_int64, C.c_int]
+        for name in ("ref_iss_fp32_add_n", "ref_iss_fp32_mul_n",
+                     "ref_iss_fp32_mul_fraction_n", "ref_tb_fp32_add_n"):
+            getattr(R, name).restype = None
+            getattr(R, name).argtypes = [u32p, u32p, u32p, C.c_uint64]
+        R.ref_tb_fp32_from_int_n.restype = None
+        R.ref_tb_fp32_from_int_n.argtypes = [C.POINTER(C.c_int64), i32p, u32p, C.c_uint64]
+        _ref = R
+    return _ref
+
+
+def _batched(fn, *arrays, dtype=np.uint32):
+    arrays = [np.ascontiguousarray(a) for a in arrays]
+    out = np.zeros(arrays[0].shape, np.uint32)
+    fn(*[a.ctypes.data_as(C.c_void_p) for a in arrays], out.ctypes.data_as(C.c_void_p),
+       arrays[0].size)
+    return out
+
+
+def fp32_add_n(a, b):
+    return _batched(_untyped("hbo_fp32_add_n"), np.asarray(a, np.uint32), np.asarray(b, np.uint32))
+
+
+def fp32_mul_n(a, b):
+    return _batched(_untyped("hbo_fp32_mul_n"), np.asarray(a, np.uint32), np.asarray(b, np.uint32))
+
+
+def fp32_mul_fraction_n(s, f):
+    return _batched(_untyped("hbo_fp32_mul_fraction_n"), np.asarray(s, np.uint32),
+                    np.asarray(f, np.uint32))
+
+
+def block_value_n(sums, a_scale, w_scale, mode):
+    s = np.ascontiguousarray(sums, np.int32)
+    a = np.ascontiguousarray(a_scale, np.uint32)
+    w = np.ascontiguousarray(w_scale, np.uint32)
+    out = np.zeros(s.shape, np.uint32)
+    lib().hbo_block_value_n(_ptr(s, i32p), _ptr(a, u32p), _ptr(w, u32p), mode,
+                            _ptr(out, u32p), s.size)
+    return out
+
+
+def ref_batched(name, *arrays):
+    """Call a batched entry of the compiled reference FP32 (oracle/_ref)."""
+    R = ref()
+    fn = getattr(R, name)
+    fn.argtypes = None
+    return _batched(fn, *arrays)
+
+
+def _untyped(name):
+    fn = getattr(lib(), name)
+    fn.argtypes = None
+    return fn
+
+
+def last_error() -> str:
+    return lib().hbo_last_error().decode()
+
+
+# ---------------------------------------------------------------- images --
+
+class Memories:
+    """ISS-layout on-chip images (tools/iss/memories.hpp:86-96)."""
+
+    def __init__(self):
+        self.abuf = np.zeros((ABUF_DEPTH, 132), np.uint8)
+        self.wbuf = np.zeros((WBUF_DEPTH, 144), np.uint8)
+        self.fbuf = np.zeros((FBUF_DEPTH, 32), np.uint32)
+        self.pbuf = np.zeros((PBUF_DEPTH, 32), np.uint32)
+        self.tbuf = np.zeros(TBUF_DEPTH, np.uint64)
+
+    def copy(self) -> "Memories":
+        m = Memories()
+        for k in ("abuf", "wbuf", "fbuf", "pbuf", "tbuf"):
+            getattr(m, k)[...] = getattr(self, k)
+        return m
+
+
+def gemm_exec(cmd: GemmCmd, mem: Memories) -> int:
+    return lib().hbo_gemm_exec(C.byref(cmd), _ptr(mem.abuf, u8p), _ptr(mem.wbuf, u8p),
+                               _ptr(mem.fbuf, u32p))
+
+
+def vec_exec(cmd: VecCmd, mem: Memories) -> int:
+    return lib().hbo_vec_exec(C.byref(cmd), _ptr(mem.abuf, u8p), _ptr(mem.fbuf, u32p),
+                              _ptr(mem.pbuf, u32p), _ptr(mem.tbuf, u64p))
+
+
+def gemm_access(cmd: GemmCmd):
+    ra = np.zeros(ABUF_DEPTH, np.uint8)
+    rw = np.zeros(WBUF_DEPTH, np.uint8)
+    rf = np.zeros(FBUF_DEPTH, np.uint8)
+    wf = np.zeros(FBUF_DEPTH, np.uint8)
+    rc = lib().hbo_gemm_access(C.byref(cmd), _ptr(ra, u8p), _ptr(rw, u8p), _ptr(rf, u8p),
+                               _ptr(wf, u8p))
+    return rc, ra, rw, rf, wf
+
+
+# --------------------------------------------------------------- formats --
+
+def f32_bits(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, np.float32)).view(np.uint32)
+
+
+def bits_f32(b) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(b, np.uint32)).view(np.float32)
+
+
+def encode_mxint8(x_bits: np.ndarray):
+    """EncodeMxint8 (formats.cpp:138-162): returns (q [rows][kpad], e [rows][kpad/32])."""
+    x_bits = np.ascontiguousarray(x_bits, np.uint32)
+    rows, cols = x_bits.shape
+    kp = (cols + 31) // 32 * 32
+    q = np.zeros((rows, kp), np.int8)
+    e = np.zeros((rows, kp // 32), np.int32)
+    rc = lib().hbo_encode_mxint8(_ptr(x_bits, u32p), rows, cols, _ptr(q, i8p), _ptr(e, i32p))
+    if rc:
+        raise ValueError(last_error())
+    return q, e
+
+
+def pack_abuf(q: np.ndarray, e: np.ndarray) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.int8)
+    e = np.ascontiguousarray(e, np.int32)
+    rows, cols = q.shape
+    out = np.zeros(((rows // 4) * (cols // 32), 144), np.uint8)
+    if lib().hbo_pack_abuf(_ptr(q, i8p), _ptr(e, i32p), rows, cols, _ptr(out, u8p)):
+        raise ValueError(last_error())
+    return out
+
+
+def pack_wbuf(code: np.ndarray, e: np.ndarray) -> np.ndarray:
+    code = np.ascontiguousarray(code, np.uint8)
+    e = np.ascontiguousarray(e, np.int32)
+    rows, cols = code.shape
+    out = np.zeros(((rows // 8) * (cols // 32), 144), np.uint8)
+    if lib().hbo_pack_wbuf(_ptr(code, u8p), _ptr(e, i32p), rows, cols, _ptr(out, u8p)):
+        raise ValueError(last_error())
+    return out
+
+
+def split_w8(q: np.ndarray):
+    q = np.ascontiguousarray(q, np.int8)
+    hi = np.zeros(q.shape, np.uint8)
+    lo = np.zeros(q.shape, np.uint8)
+    lib().hbo_split_w8(_ptr(q, i8p), q.size, _ptr(hi, u8p), _ptr(lo, u8p))
+    return hi, lo
+
+
+def canonical_mxfp4(code, e, exponent_shift=0, out_rows=None):
+    code = np.ascontiguousarray(code, np.uint8)
+    e = np.ascontiguousarray(e, np.int32)
+    rows, cols = code.shape
+    out_rows = rows if out_rows is None else out_rows
+    oc = np.zeros((out_rows, cols), np.uint8)
+    oe = np.zeros((out_rows, cols // 32), np.int32)
+    if lib().hbo_canonical_mxfp4(_ptr(code, u8p), _ptr(e, i32p), rows, cols, exponent_shift,
+                                 out_rows, _ptr(oc, u8p), _ptr(oe, i32p)):
+        raise ValueError(last_error())
+    return oc, oe
+
+
+def linear(m, n, kb_total, a_words, planes, modes, pieces=None, c=None, onto=False,
+           ops=(), tbuf=None, quantize=False):
+    """hbo_linear; returns (c bits [m][n], q_out words or None)."""
+    L = lib()
+    a_words = np.ascontiguousarray(a_words, np.uint8)
+    planes = [np.ascontiguousarray(p, np.uint8) for p in planes]
+    wp = (u8p * len(planes))(*[_ptr(p, u8p) for p in planes])
+    md = (C.c_uint32 * len(modes))(*modes)
+    if pieces is None:
+        pieces = [(0, kb_total)]
+    pc = (Piece * len(pieces))(*[Piece(o, k) for o, k in pieces])
+    cc = np.zeros((m, n), np.uint32) if c is None else np.ascontiguousarray(c, np.uint32).copy()
+    keep = []
+    eps = (EpOp * max(1, len(ops)))()
+    for i, op in enumerate(ops):
+        kind = op[0]
+        eps[i].op = kind
+        if kind in (EP_ADDP, EP_MULP):
+            v = np.ascontiguousarray(op[1], np.uint32)
+            keep.append(v)
+            eps[i].vec = _ptr(v, u32p)
+        elif kind == EP_SCALE:
+            eps[i].imm = int(op[1])
+        elif kind in (EP_ACT_MUL, EP_ADD):
+            v = np.ascontiguousarray(op[1], np.uint32)
+            keep.append(v)
+            eps[i].x2 = _ptr(v, u32p)
+    tb = np.zeros(TBUF_DEPTH, np.uint64) if tbuf is None else np.ascontiguousarray(tbuf, np.uint64)
+    q_out = np.zeros(((m // 4) * (n // 32), 144), np.uint8) if quantize else None
+    rc = L.hbo_linear(m, n, kb_total, _ptr(a_words, u8p), len(planes), wp, md, len(pieces), pc,
+                      1 if onto else 0, _ptr(cc, u32p), len(ops), eps, _ptr(tb, u64p),
+                      _ptr(q_out, u8p) if quantize else None)
+    if rc:
+        raise ValueError(last_error())
+    return cc, q_out

@@ -1,0 +1,808 @@
+/*
+ * CPU oracle for the quantized GEMM hot path -- test infrastructure only.
+ * See hb_oracle.h for what it restates and who may load it.
+ *
+ * Built with -O2 -ffp-contract=off (the reference's own flag,
+ * CMakeLists.txt:9); all arithmetic here is on integers anyway.
+ */
+#include "hb_oracle.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static _Thread_local char g_error[256];
+
+static int fail(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof g_error, fmt, ap);
+  va_end(ap);
+  return 1;
+}
+
+const char* hbo_last_error(void) { return g_error; }
+
+static int bit_width32(uint32_t v) { return v ? 32 - __builtin_clz(v) : 0; }
+static int bit_width64(uint64_t v) { return v ? 64 - __builtin_clzll(v) : 0; }
+
+/* ------------------------------------------------------------------ */
+/* FP32: tools/iss/fp32.hpp.  Exponent field 0 reads as zero; results  */
+/* below the normal range become +0; results at exponent 255 or above  */
+/* become +-inf; exponent 255 on input is treated as an ordinary       */
+/* exponent (no NaN/inf semantics).                                    */
+/* ------------------------------------------------------------------ */
+
+static uint32_t exp_field(uint32_t bits) { return (bits >> 23) & 0xFFu; }
+
+static uint32_t significand(uint32_t bits) {
+  return exp_field(bits) ? ((bits & 0x7FFFFFu) | 0x800000u) : 0u;
+}
+
+/* fp32.hpp:24-33 */
+uint32_t hbo_fp32_pack(uint32_t sign, int32_t exponent, uint32_t fraction) {
+  if (exponent <= 0) return 0u;
+  if (exponent >= 255) return (sign << 31) | 0x7F800000u;
+  return (sign << 31) | ((uint32_t)exponent << 23) | fraction;
+}
+
+/* fp32.hpp:35-44: round a 24-bit significand with guard/sticky, RNE. */
+uint32_t hbo_fp32_round(uint32_t sign, int32_t exponent, uint32_t sig24,
+                        int guard, int sticky) {
+  uint32_t r = sig24 + ((guard && (sticky || (sig24 & 1u))) ? 1u : 0u);
+  if (r >> 24) {
+    exponent += 1;
+    r >>= 1;
+  }
+  return hbo_fp32_pack(sign, exponent, r & 0x7FFFFFu);
+}
+
+/* fp32.hpp:46-75: align with 3 extra bits (guard, round, sticky). */
+uint32_t hbo_fp32_add(uint32_t a, uint32_t b) {
+  const uint32_t ea = exp_field(a), eb = exp_field(b);
+  const uint32_t ma = significand(a), mb = significand(b);
+  const int a_larger = ((ea << 24) | ma) >= ((eb << 24) | mb);
+  const uint32_t larger = a_larger ? a : b;
+  const uint32_t e_big = a_larger ? ea : eb;
+  const uint32_t gap = a_larger ? ea - eb : eb - ea;
+  const uint32_t m_big = a_larger ? ma : mb;
+  const uint32_t m_small = a_larger ? mb : ma;
+  uint32_t aligned = 0;
+  if (m_small != 0) {
+    if (gap > 26) {
+      aligned = 1; /* only the sticky bit survives */
+    } else {
+      const uint32_t wide = m_small << 3;
+      aligned = (wide >> gap) | ((wide & ((1u << gap) - 1u)) ? 1u : 0u);
+    }
+  }
+  const int subtract = ((a ^ b) >> 31) != 0;
+  const uint32_t sum = subtract ? (m_big << 3) - aligned : (m_big << 3) + aligned;
+  if (sum == 0) return 0u;
+  const int shift = 28 - bit_width32(sum); /* bring the leading 1 to bit 27 */
+  const uint32_t norm = sum << shift;
+  return hbo_fp32_round(larger >> 31, (int32_t)e_big + 1 - shift, norm >> 4,
+                        (norm >> 3) & 1u, (norm & 7u) != 0);
+}
+
+/* fp32.hpp:77-92 */
+uint32_t hbo_fp32_mul(uint32_t a, uint32_t b) {
+  if (exp_field(a) == 0 || exp_field(b) == 0) return 0u;
+  const uint64_t product = (uint64_t)significand(a) * significand(b);
+  const int carry = (product >> 47) != 0;
+  const int drop = carry ? 23 : 22;
+  const uint64_t kept = product >> drop; /* 24-bit significand + guard */
+  const int sticky = (product & ((1ull << drop) - 1ull)) != 0;
+  const int32_t exponent =
+      (int32_t)(exp_field(a) + exp_field(b)) - (carry ? 126 : 127);
+  return hbo_fp32_round((a ^ b) >> 31, exponent, (uint32_t)(kept >> 1),
+                        (int)(kept & 1u), sticky);
+}
+
+/* fp32.hpp:94-104: s * fraction / 2^16, one rounding. */
+uint32_t hbo_fp32_mul_fraction(uint32_t s, uint32_t fraction) {
+  if (exp_field(s) == 0 || fraction == 0) return 0u;
+  const uint64_t product = (uint64_t)significand(s) * fraction;
+  const int shift = 40 - bit_width64(product);
+  const uint64_t norm = product << shift; /* leading 1 at bit 39 */
+  return hbo_fp32_round(s >> 31, (int32_t)exp_field(s) - shift,
+                        (uint32_t)(norm >> 16), (int)((norm >> 15) & 1u),
+                        (norm & 0x7FFFu) != 0);
+}
+
+/* ------------------------------------------------------------------ */
+/* GEMM array: tools/iss/gemm_array.cpp                                */
+/* ------------------------------------------------------------------ */
+
+enum { MODE_FP4 = 0, MODE_W8_HI = 1, MODE_W8_LO = 2 };
+
+uint32_t hbo_decode_weight_mode(uint32_t wmode) {
+  switch (wmode & 3u) {
+    case 0: return MODE_FP4;
+    case 1: return MODE_W8_HI;
+    default: return MODE_W8_LO;
+  }
+}
+
+int32_t hbo_scale_bias(uint32_t mode) {
+  switch (mode) {
+    case MODE_FP4: return -7;
+    case MODE_W8_HI: return -8;
+    case MODE_W8_LO: return -12;
+  }
+  return 0;
+}
+
+/* E2M1 magnitude times two for codes 0..7: {0,1,2,3,4,6,8,12}. */
+static const int32_t k_fp4_twice[8] = {0, 1, 2, 3, 4, 6, 8, 12};
+
+int32_t hbo_weight_value(uint32_t nibble, uint32_t mode) {
+  const int32_t raw = (int32_t)(nibble & 0xFu);
+  const int negative = (nibble & 0x8u) != 0;
+  switch (mode) {
+    case MODE_FP4: {
+      const int32_t mag = k_fp4_twice[nibble & 7u];
+      return negative ? -mag : mag;
+    }
+    case MODE_W8_HI: return negative ? raw - 16 : raw;
+    case MODE_W8_LO: return raw;
+  }
+  return 0;
+}
+
+/* sum * 2^((a_scale-127) + (w_scale-127) + SBIAS), exact; +0 below range. */
+uint32_t hbo_block_value(int32_t sum, uint32_t a_scale, uint32_t w_scale,
+                         uint32_t mode) {
+  if (sum == 0) return 0u;
+  const uint32_t mag = (uint32_t)(sum < 0 ? -(int64_t)sum : sum);
+  const int msb = bit_width32(mag) - 1;
+  const int32_t exponent = (int32_t)(a_scale + w_scale) - 254 +
+                           hbo_scale_bias(mode) + msb + 127;
+  const uint32_t fraction =
+      msb <= 23 ? (mag << (23 - msb)) & 0x7FFFFFu : (mag >> (msb - 23)) & 0x7FFFFFu;
+  return hbo_fp32_pack(sum < 0 ? 1u : 0u, exponent, fraction);
+}
+
+static int check_gemm(const hbo_gemm_cmd* c) {
+  if (!(c->m >= 32 && c->m <= 992 && c->m % 32 == 0))
+    return fail("GEMM m = %u is not a multiple of 32 from 32 to 992", c->m);
+  if (!(c->kb >= 1 && c->kb <= c->a_stride))
+    return fail("GEMM kb = %u is not in [1, a_stride = %u]", c->kb, c->a_stride);
+  if (c->n8 < 1) return fail("GEMM n8 = 0");
+  return 0;
+}
+
+#define ADDR_MASK ((1u << 20) - 1u)
+
+int hbo_gemm_exec(const hbo_gemm_cmd* cmd, const uint8_t* abuf,
+                  const uint8_t* wbuf, uint32_t* fbuf) {
+  if (check_gemm(cmd)) return 1;
+  g_error[0] = 0;
+  const uint32_t mode = hbo_decode_weight_mode(cmd->wmode);
+  const uint32_t quads = cmd->m / HBO_TOKENS;
+  /* decoded weights of one column group: [kb][8][32] values, [kb][8] scales */
+  int32_t* wv = (int32_t*)malloc(sizeof(int32_t) * cmd->kb * 256u);
+  uint32_t* ws = (uint32_t*)malloc(sizeof(uint32_t) * cmd->kb * 8u);
+  if (!wv || !ws) {
+    free(wv);
+    free(ws);
+    return fail("out of memory");
+  }
+  for (uint32_t g = 0; g < cmd->n8; ++g) {
+    for (uint32_t b = 0; b < cmd->kb; ++b) {
+      const uint32_t addr = ((cmd->w_base + g * cmd->w_stride + b) & ADDR_MASK) %
+                            HBO_WBUF_DEPTH;
+      const uint8_t* word = wbuf + (size_t)addr * HBO_WBUF_WORD;
+      for (uint32_t c = 0; c < 8; ++c) {
+        for (uint32_t k = 0; k < 32; ++k) {
+          const uint32_t idx = c * 32 + k;
+          const uint32_t byte = word[idx / 2];
+          wv[(b * 8 + c) * 32 + k] =
+              hbo_weight_value(idx % 2 == 0 ? (byte & 0xFu) : (byte >> 4), mode);
+        }
+        ws[b * 8 + c] = word[128 + c];
+      }
+    }
+    for (uint32_t q = 0; q < quads; ++q) {
+      const uint32_t c_addr =
+          ((cmd->c_base + q * cmd->n8 + g) & ADDR_MASK) % HBO_FBUF_DEPTH;
+      uint32_t acc[32];
+      if (cmd->acc) memcpy(acc, fbuf + (size_t)c_addr * 32, sizeof acc);
+      else memset(acc, 0, sizeof acc);
+      for (uint32_t b = 0; b < cmd->kb; ++b) {
+        const uint32_t a_addr =
+            ((cmd->a_base + q * cmd->a_stride + b) & ADDR_MASK) % HBO_ABUF_DEPTH;
+        const uint8_t* aw = abuf + (size_t)a_addr * HBO_ABUF_WORD;
+        for (uint32_t t = 0; t < 4; ++t) {
+          for (uint32_t c = 0; c < 8; ++c) {
+            int32_t sum = 0;
+            for (uint32_t k = 0; k < 32; ++k)
+              sum += (int32_t)(int8_t)aw[t * 32 + k] * wv[(b * 8 + c) * 32 + k];
+            acc[t * 8 + c] = hbo_fp32_add(
+                acc[t * 8 + c], hbo_block_value(sum, aw[128 + t], ws[b * 8 + c], mode));
+          }
+        }
+      }
+      memcpy(fbuf + (size_t)c_addr * 32, acc, sizeof acc);
+    }
+  }
+  free(wv);
+  free(ws);
+  return 0;
+}
+
+int hbo_gemm_access(const hbo_gemm_cmd* cmd, uint8_t* reads_abuf,
+                    uint8_t* reads_wbuf, uint8_t* reads_fbuf,
+                    uint8_t* writes_fbuf) {
+  if (check_gemm(cmd)) return 1;
+  memset(reads_abuf, 0, HBO_ABUF_DEPTH);
+  memset(reads_wbuf, 0, HBO_WBUF_DEPTH);
+  memset(reads_fbuf, 0, HBO_FBUF_DEPTH);
+  memset(writes_fbuf, 0, HBO_FBUF_DEPTH);
+  for (uint32_t g = 0; g < cmd->n8; ++g) {
+    for (uint32_t b = 0; b < cmd->kb; ++b)
+      reads_wbuf[((cmd->w_base + g * cmd->w_stride + b) & ADDR_MASK) % HBO_WBUF_DEPTH] = 1;
+    for (uint32_t q = 0; q < cmd->m / 4; ++q) {
+      const uint32_t c_addr = ((cmd->c_base + q * cmd->n8 + g) & ADDR_MASK) % HBO_FBUF_DEPTH;
+      if (cmd->acc) reads_fbuf[c_addr] = 1;
+      for (uint32_t b = 0; b < cmd->kb; ++b)
+        reads_abuf[((cmd->a_base + q * cmd->a_stride + b) & ADDR_MASK) % HBO_ABUF_DEPTH] = 1;
+      writes_fbuf[c_addr] = 1;
+    }
+  }
+  return 0;
+}
+
+uint64_t hbo_gemm_cycles(const hbo_gemm_cmd* cmd, uint32_t fixed_cycles) {
+  return (uint64_t)cmd->n8 * (cmd->m / 32) * cmd->kb * 8u + fixed_cycles;
+}
+
+/* ------------------------------------------------------------------ */
+/* Formats: tools/runtime/formats.cpp                                  */
+/* ------------------------------------------------------------------ */
+
+/* formats.cpp:35-56: RNE(x * 2^(6-e)) saturated to [-128, 127];        */
+/* subnormal inputs keep their value.  Inf/NaN input is an error there; */
+/* here it returns 0 and sets the error text.                           */
+int8_t hbo_quantize_int8(uint32_t bits, int32_t e) {
+  const uint32_t field = exp_field(bits);
+  if (field == 0xFFu) {
+    fail("MXINT8 input is infinite or NaN");
+    return 0;
+  }
+  const uint64_t sig = field == 0 ? (bits & 0x7FFFFFu) : ((bits & 0x7FFFFFu) | 0x800000u);
+  const int64_t shift = (field == 0 ? -149 : (int64_t)field - 150) + 6 - e;
+  int64_t mag = 0;
+  if (shift >= 0) {
+    mag = shift > 8 ? 256 : (int64_t)(sig << shift);
+  } else if (shift > -64) {
+    const uint64_t kept = sig >> (-shift);
+    const uint64_t rest = sig & ((1ull << (-shift)) - 1ull);
+    const uint64_t half = 1ull << (-shift - 1);
+    mag = (int64_t)(kept + ((rest > half || (rest == half && (kept & 1u))) ? 1u : 0u));
+  }
+  int64_t v = (bits >> 31) ? -mag : mag;
+  if (v < -128) v = -128;
+  if (v > 127) v = 127;
+  return (int8_t)v;
+}
+
+static uint32_t pad_to_block(uint32_t k) { return (k + 31u) / 32u * 32u; }
+
+int hbo_encode_mxint8(const uint32_t* x, uint32_t rows, uint32_t cols,
+                      int8_t* q, int32_t* e) {
+  const uint32_t kp = pad_to_block(cols), blocks = kp / 32u;
+  g_error[0] = 0;
+  for (uint32_t r = 0; r < rows; ++r) {
+    for (uint32_t kb = 0; kb < blocks; ++kb) {
+      const uint32_t end = cols < (kb + 1) * 32u ? cols : (kb + 1) * 32u;
+      uint32_t amax = 0;
+      for (uint32_t c = kb * 32u; c < end; ++c) {
+        const uint32_t mag = x[(size_t)r * cols + c] & 0x7FFFFFFFu;
+        if (mag > amax) amax = mag;
+      }
+      const int32_t ex = amax ? (int32_t)exp_field(amax) - 127 : 0;
+      e[(size_t)r * blocks + kb] = ex;
+      for (uint32_t c = kb * 32u; c < (kb + 1) * 32u; ++c) {
+        q[(size_t)r * kp + c] =
+            c < end ? hbo_quantize_int8(x[(size_t)r * cols + c], ex) : 0;
+      }
+    }
+  }
+  return g_error[0] ? 1 : 0;
+}
+
+/* formats.cpp:66-70 */
+static int scale_byte(int32_t e, uint8_t* out) {
+  if (e < -127 || e > 127) return fail("block exponent %d is outside E8M0", e);
+  *out = (uint8_t)(e + 127);
+  return 0;
+}
+
+int hbo_pack_abuf(const int8_t* q, const int32_t* e, uint32_t rows,
+                  uint32_t cols, uint8_t* out) {
+  if (rows % 4 || cols % 32)
+    return fail("ABUF matrix %ux%u is not a multiple of 4x32", rows, cols);
+  const size_t blocks = cols / 32u;
+  memset(out, 0, (size_t)(rows / 4) * blocks * HBO_DDR_WORD);
+  for (size_t qd = 0; qd < rows / 4; ++qd) {
+    for (size_t kb = 0; kb < blocks; ++kb) {
+      uint8_t* word = out + (qd * blocks + kb) * HBO_DDR_WORD;
+      for (size_t j = 0; j < 4; ++j) {
+        const size_t row = 4 * qd + j;
+        for (size_t k = 0; k < 32; ++k)
+          word[j * 32 + k] = (uint8_t)q[row * cols + kb * 32 + k];
+        if (scale_byte(e[row * blocks + kb], &word[128 + j])) return 1;
+      }
+    }
+  }
+  return 0;
+}
+
+int hbo_pack_fbuf(const uint32_t* x, uint32_t rows, uint32_t cols,
+                  uint32_t* out) {
+  if (rows % 4 || cols % 8)
+    return fail("FBUF matrix %ux%u is not a multiple of 4x8", rows, cols);
+  size_t o = 0;
+  for (uint32_t qd = 0; qd < rows / 4; ++qd)
+    for (uint32_t g = 0; g < cols / 8; ++g)
+      for (uint32_t j = 0; j < 4; ++j)
+        for (uint32_t c = 0; c < 8; ++c)
+          out[o++] = x[(size_t)(4 * qd + j) * cols + 8 * g + c];
+  return 0;
+}
+
+int hbo_unpack_fbuf(const uint32_t* words, uint32_t rows, uint32_t cols,
+                    uint32_t* out) {
+  if (rows % 4 || cols % 8)
+    return fail("FBUF matrix %ux%u is not a multiple of 4x8", rows, cols);
+  size_t o = 0;
+  for (uint32_t qd = 0; qd < rows / 4; ++qd)
+    for (uint32_t g = 0; g < cols / 8; ++g)
+      for (uint32_t j = 0; j < 4; ++j)
+        for (uint32_t c = 0; c < 8; ++c)
+          out[(size_t)(4 * qd + j) * cols + 8 * g + c] = words[o++];
+  return 0;
+}
+
+/* tensors.cpp:66-90 */
+int hbo_pack_wbuf(const uint8_t* code, const int32_t* e, uint32_t rows,
+                  uint32_t cols, uint8_t* out) {
+  if (rows % 8 || cols % 32)
+    return fail("WBUF matrix %ux%u is not a multiple of 8x32", rows, cols);
+  const size_t blocks = cols / 32u;
+  memset(out, 0, (size_t)(rows / 8) * blocks * HBO_DDR_WORD);
+  for (size_t g = 0; g < rows / 8; ++g) {
+    for (size_t kb = 0; kb < blocks; ++kb) {
+      uint8_t* word = out + (g * blocks + kb) * HBO_DDR_WORD;
+      for (size_t c = 0; c < 8; ++c) {
+        const size_t row = 8 * g + c;
+        const size_t base = row * cols + kb * 32;
+        for (size_t m = 0; m < 16; ++m)
+          word[c * 16 + m] =
+              (uint8_t)((code[base + 2 * m] & 0xFu) | ((code[base + 2 * m + 1] & 0xFu) << 4));
+        if (scale_byte(e[row * blocks + kb], &word[128 + c])) return 1;
+      }
+    }
+  }
+  return 0;
+}
+
+/* weights.cpp:72-88 */
+void hbo_split_w8(const int8_t* q, size_t count, uint8_t* hi, uint8_t* lo) {
+  for (size_t i = 0; i < count; ++i) {
+    const uint8_t byte = (uint8_t)q[i];
+    hi[i] = (uint8_t)(byte >> 4);
+    lo[i] = (uint8_t)(byte & 0xFu);
+  }
+}
+
+/* weights.cpp:39-70: rescale each block so its largest code has E2M1     */
+/* exponent 2 (code 6 or 7), moving the difference into the block scale. */
+int hbo_canonical_mxfp4(const uint8_t* code, const int32_t* e, uint32_t rows,
+                        uint32_t cols, int32_t exponent_shift,
+                        uint32_t out_rows, uint8_t* out_code, int32_t* out_e) {
+  static const uint32_t half_units[8] = {0, 1, 2, 3, 4, 6, 8, 12};
+  static const int32_t floor_log2[8] = {0, -1, 0, 0, 1, 1, 2, 2};
+  if (out_rows < rows || cols % 32)
+    return fail("cannot pad a %ux%u MXFP4 matrix to %u rows", rows, cols, out_rows);
+  const size_t blocks = cols / 32u;
+  memset(out_code, 0, (size_t)out_rows * cols);
+  memset(out_e, 0, sizeof(int32_t) * out_rows * blocks);
+  for (size_t r = 0; r < rows; ++r) {
+    for (size_t kb = 0; kb < blocks; ++kb) {
+      const size_t first = r * cols + kb * 32;
+      uint8_t top = 0;
+      for (size_t k = 0; k < 32; ++k)
+        if ((code[first + k] & 7u) > top) top = code[first + k] & 7u;
+      if (top == 0) continue;
+      const int32_t shift = 2 - floor_log2[top];
+      out_e[r * blocks + kb] = e[r * blocks + kb] + floor_log2[top] - 2 + exponent_shift;
+      for (size_t k = 0; k < 32; ++k) {
+        const uint8_t c = code[first + k];
+        const uint32_t half = half_units[c & 7u] << shift;
+        int idx = -1;
+        for (int i = 0; i < 8; ++i)
+          if (half_units[i] == half) idx = i;
+        if (idx < 0)
+          return fail("E2M1 code %u scaled by 2^%d is not representable", c, shift);
+        out_code[first + k] = (uint8_t)((idx != 0 && (c & 8u)) ? (idx | 8) : idx);
+      }
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* VEC lane: tools/iss/lane.cpp                                        */
+/* ------------------------------------------------------------------ */
+
+enum { PO_ADD = 0, PO_MAX = 1, PO_SIGNFIX = 2, PO_SUB = 3 };
+
+/* lane.cpp:45-58: sign-magnitude >= with both zeros equal. */
+static int max_greater_equal(uint32_t prod, uint32_t other) {
+  const uint32_t pm = prod & 0x7FFFFFFFu, om = other & 0x7FFFFFFFu;
+  if (pm == 0 && om == 0) return 1;
+  const int pn = (prod >> 31) != 0, on = (other >> 31) != 0;
+  if (pn != on) return !pn;
+  return pn ? pm <= om : pm >= om;
+}
+
+/* lane.cpp:322-335 */
+uint32_t hbo_post_add(uint32_t prod, uint32_t c1, uint32_t op) {
+  switch (op) {
+    case PO_MAX: return hbo_fp32_add(max_greater_equal(prod, c1) ? prod : c1, 0);
+    case PO_SIGNFIX:
+      return (c1 >> 31) ? hbo_fp32_add(prod ^ 0x80000000u, c1) : hbo_fp32_add(prod, 0);
+    case PO_SUB: return hbo_fp32_add(prod, c1 ^ 0x80000000u);
+    default: return hbo_fp32_add(prod, c1);
+  }
+}
+
+/* lane.cpp:337-340: v + RNE(s * frac / 2^16) */
+uint32_t hbo_interpolate(uint64_t entry, uint32_t fraction) {
+  return hbo_fp32_add((uint32_t)entry, hbo_fp32_mul_fraction((uint32_t)(entry >> 32), fraction));
+}
+
+/* lane.cpp:342-355: T(|x|) from the upper half of TBUF, UQ4.21 index. */
+uint32_t hbo_activation(uint32_t prod, const uint64_t* tbuf) {
+  const uint32_t e = exp_field(prod);
+  if (e >= 131) return 0x3F800000u;
+  const uint32_t sig = significand(prod);
+  uint32_t fixed = 0;
+  if (e == 130) fixed = sig << 1;
+  else if (e >= 105) fixed = sig >> (129 - e);
+  return hbo_interpolate(tbuf[512 + (fixed >> 16)], fixed & 0xFFFFu);
+}
+
+/* lane.cpp:384-404 */
+uint8_t hbo_quantize_element(uint32_t value, uint32_t emax) {
+  const uint32_t e = exp_field(value);
+  const uint32_t sig = significand(value);
+  if (sig == 0) return 0;
+  const uint32_t shift = emax - e + 17;
+  uint32_t mag = 0;
+  if (shift < 25) {
+    const uint32_t integer = sig >> shift;
+    const int guard = ((sig >> (shift - 1)) & 1u) != 0;
+    const int sticky = (sig & ((1u << (shift - 1)) - 1u)) != 0;
+    mag = integer + ((guard && (sticky || (integer & 1u))) ? 1u : 0u);
+  }
+  if (value >> 31) return mag >= 128 ? 0x80 : (uint8_t)((256 - mag) & 0xFFu);
+  return mag >= 128 ? 0x7F : (uint8_t)mag;
+}
+
+/* lane.cpp:406-424: words4x32 = 4 FBUF words (32 columns) of one quad. */
+int hbo_quantize_block(const uint32_t* words4x32, uint8_t* out132) {
+  memset(out132, 0, 132);
+  for (uint32_t t = 0; t < 4; ++t) {
+    uint32_t emax = 0;
+    for (uint32_t qw = 0; qw < 4; ++qw)
+      for (uint32_t l = 0; l < 8; ++l) {
+        const uint32_t e = exp_field(words4x32[qw * 32 + t * 8 + l]);
+        if (e > emax) emax = e;
+      }
+    for (uint32_t qw = 0; qw < 4; ++qw)
+      for (uint32_t l = 0; l < 8; ++l)
+        out132[t * 32 + qw * 8 + l] =
+            hbo_quantize_element(words4x32[qw * 32 + t * 8 + l], emax);
+    out132[128 + t] = (uint8_t)(emax == 0 ? 127 : emax);
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* VEC library programs 0-9 as passes (tools/compiler/vec_rom.cpp).    */
+/* ------------------------------------------------------------------ */
+
+enum { R_ZERO = 0, R_SRC = 1, R_SRC2 = 2, R_DST = 3, R_ROWSQ = 4, R_N8 = 5,
+       R_PBASE = 6, R_AUX = 7, R_IMM = 8, R_Q = 9 };
+enum { C0_ZERO, C0_X2, C0_PBUF };
+enum { B_ONE, B_X2, B_PBUF, B_IMM };
+enum { WR_FBUF, WR_FINAL };
+
+typedef struct {
+  uint32_t rx, rx2, rd, rimm; /* register indices */
+  int rowvec;                 /* PBUF row vector operand (Pbuf::kRowVec) */
+  int c0, b, act, po, pv, wr;
+} vpass;
+
+/* Whole(): vec_rom.cpp:63-70 */
+static vpass whole(void) {
+  vpass p;
+  memset(&p, 0, sizeof p);
+  p.rx = R_SRC;
+  p.rd = R_DST;
+  p.wr = WR_FINAL;
+  return p;
+}
+
+/* Program(): vec_rom.cpp:314-372; Activation(): :214-237 */
+static int library_passes(uint32_t entry, vpass* out) {
+  vpass p = whole();
+  switch (entry) {
+    case 0: p.rx2 = R_SRC2; p.c0 = C0_X2; break;                /* ADD */
+    case 1: p.rx2 = R_SRC2; p.b = B_X2; break;                  /* MUL */
+    case 2: p.rx2 = R_SRC2; p.po = PO_MAX; p.pv = 1; break;     /* MAX */
+    case 3: p.rowvec = 1; p.c0 = C0_PBUF; break;                /* ADDP */
+    case 4: p.rowvec = 1; p.b = B_PBUF; break;                  /* MULP */
+    case 5: p.rimm = R_IMM; p.b = B_IMM; break;                 /* SCALE */
+    case 6: break;                                              /* COPY */
+    case 7: p.po = PO_MAX; break;                               /* RELU */
+    case 8:
+    case 9: {                                                   /* ACT, ACT_MUL */
+      vpass sigma = whole();
+      sigma.rd = R_IMM;
+      sigma.act = 1;
+      sigma.wr = WR_FBUF;
+      vpass gate = whole();
+      gate.rx2 = R_IMM;
+      gate.b = B_X2;
+      gate.po = PO_SIGNFIX;
+      out[0] = sigma;
+      if (entry == 8) {
+        out[1] = gate;
+        return 2;
+      }
+      gate.rd = R_IMM;
+      gate.wr = WR_FBUF;
+      out[1] = gate;
+      vpass product = whole();
+      product.rx = R_IMM;
+      product.rx2 = R_SRC2;
+      product.b = B_X2;
+      out[2] = product;
+      return 3;
+    }
+    default: return 0;
+  }
+  out[0] = p;
+  return 1;
+}
+
+/* LaneOutput + FloatResult (lane.cpp:163-179, 305-320) for the subset. */
+static uint32_t lane(const vpass* p, uint32_t x, uint32_t x2, uint32_t pb,
+                     uint32_t imm, const uint64_t* tbuf) {
+  uint32_t c1 = p->pv ? x2 : 0u;
+  if (p->po == PO_SIGNFIX) c1 = x;
+  const uint32_t c0 = p->c0 == C0_X2 ? x2 : p->c0 == C0_PBUF ? pb : 0u;
+  const uint32_t pre = hbo_fp32_add(x, c0);
+  const uint32_t bv = p->b == B_X2 ? x2 : p->b == B_PBUF ? pb : p->b == B_IMM ? imm : 0x3F800000u;
+  const uint32_t prod = hbo_fp32_mul(pre, bv);
+  if (p->act) return hbo_activation(prod, tbuf);
+  return hbo_post_add(prod, c1, (uint32_t)p->po);
+}
+
+/* VecEngine::RunPass/RunQuads/RunWord/Store (vec_engine.cpp:252-460)  */
+/* without the timing model.                                           */
+static int run_pass(const vpass* p, const uint32_t* reg, int quantize,
+                    uint8_t* abuf, uint32_t* fbuf, const uint32_t* pbuf,
+                    const uint64_t* tbuf, uint8_t* written) {
+  const uint32_t quads = reg[R_ROWSQ] & 0x1FFu;
+  const uint32_t words = reg[R_N8] & 0x3FFu;
+  if (quads == 0 || words == 0)
+    return fail("a PASS has %u quads and %u words", quads, words);
+  const uint32_t n8 = reg[R_N8] & 0xFFu;
+  const uint32_t d = reg[p->rd];
+  uint32_t src = reg[p->rx] & 4095u, src2 = reg[p->rx2] & 4095u;
+  uint32_t dst = d & 4095u, abuf_at = d & 8191u;
+  const uint32_t pb = reg[R_PBASE] & 511u;
+  const uint32_t imm = reg[p->rimm];
+  const int x2_en = p->rx2 != R_ZERO;
+  const int to_abuf = p->wr == WR_FINAL && quantize;
+  uint32_t block[4][32];
+  uint32_t next_quarter = 0;
+  memset(written, 0, HBO_FBUF_DEPTH);
+  for (uint32_t q = 0; q < quads; ++q) {
+    for (uint32_t w = 0; w < words; ++w) {
+      const uint32_t xa = (src + w) & 4095u;
+      if (written[xa]) return fail("a PASS reads FBUF word %u after writing it", xa);
+      uint32_t xw[32], x2w[32], out[32];
+      memcpy(xw, fbuf + (size_t)xa * 32, sizeof xw);
+      if (x2_en) {
+        const uint32_t x2a = (src2 + w) & 4095u;
+        if (written[x2a]) return fail("a PASS reads FBUF word %u after writing it", x2a);
+        memcpy(x2w, fbuf + (size_t)x2a * 32, sizeof x2w);
+      } else {
+        memcpy(x2w, xw, sizeof x2w);
+      }
+      const uint32_t* pw = pbuf + (size_t)((pb + (w >> 2)) & 511u) * 32;
+      const uint32_t slice = w & 3u;
+      for (uint32_t t = 0; t < 4; ++t)
+        for (uint32_t l = 0; l < 8; ++l)
+          out[t * 8 + l] = lane(p, xw[t * 8 + l], x2w[t * 8 + l],
+                                p->rowvec ? pw[slice * 8 + l] : 0u, imm, tbuf);
+      if (!to_abuf) {
+        const uint32_t da = (dst + w) & 4095u;
+        memcpy(fbuf + (size_t)da * 32, out, sizeof out);
+        written[da] = 1;
+      } else {
+        const uint32_t quarter = w & 3u;
+        if (quarter != next_quarter)
+          return fail("quantized word %u arrives out of order", quarter);
+        memcpy(block[quarter], out, sizeof out);
+        next_quarter = (quarter + 1u) & 3u;
+        if (quarter == 3) {
+          const uint32_t aa = (abuf_at + (w >> 2)) & 8191u;
+          hbo_quantize_block(&block[0][0], abuf + (size_t)aa * HBO_ABUF_WORD);
+        }
+      }
+    }
+    src = (src + n8) & 4095u;
+    src2 = (src2 + n8) & 4095u;
+    dst = (dst + n8) & 4095u;
+    abuf_at = (abuf_at + (n8 >> 2)) & 8191u;
+  }
+  if (next_quarter != 0) return fail("a PASS ends inside a block of 4 quantized words");
+  return 0;
+}
+
+int hbo_vec_exec(const hbo_vec_cmd* cmd, uint8_t* abuf, uint32_t* fbuf,
+                 const uint32_t* pbuf, const uint64_t* tbuf) {
+  vpass passes[3];
+  const int n = library_passes(cmd->entry, passes);
+  if (n == 0) {
+    fail("library entry %u is not an epilogue program", cmd->entry);
+    return 2;
+  }
+  /* VecEngine::Initialize (vec_engine.cpp:227-239): operand widths */
+  uint32_t reg[32];
+  memset(reg, 0, sizeof reg);
+  reg[R_SRC] = cmd->src & 0xFFFu;
+  reg[R_SRC2] = cmd->src2 & 0xFFFu;
+  reg[R_DST] = cmd->dst & 0x1FFFu;
+  reg[R_ROWSQ] = cmd->rows_q & 0x1FFu;
+  reg[R_N8] = cmd->n8 & 0xFFu;
+  reg[R_PBASE] = cmd->p_base & 0x1FFu;
+  reg[R_AUX] = cmd->aux & 0x7FFu;
+  reg[R_IMM] = cmd->imm;
+  reg[R_Q] = cmd->quantize ? 1u : 0u;
+  uint8_t written[HBO_FBUF_DEPTH];
+  g_error[0] = 0;
+  for (int i = 0; i < n; ++i)
+    if (run_pass(&passes[i], reg, cmd->quantize != 0, abuf, fbuf, pbuf, tbuf, written))
+      return 1;
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Linear layer: the fold order of LinearEmitter::Emit                 */
+/* (tools/compiler/kernels.cpp:361-392) plus the epilogue ops.         */
+/* ------------------------------------------------------------------ */
+
+static uint32_t epilogue(const hbo_ep_op* op, uint32_t y, size_t r, uint32_t n,
+                         uint32_t col, const uint64_t* tbuf) {
+  vpass p = whole();
+  switch (op->op) {
+    case HBO_EP_ADDP: {
+      p.c0 = C0_PBUF;
+      return lane(&p, y, y, op->vec[col], 0, tbuf);
+    }
+    case HBO_EP_MULP: {
+      p.b = B_PBUF;
+      return lane(&p, y, y, op->vec[col], 0, tbuf);
+    }
+    case HBO_EP_SCALE: {
+      p.b = B_IMM;
+      return lane(&p, y, y, 0, op->imm, tbuf);
+    }
+    case HBO_EP_COPY: return lane(&p, y, y, 0, 0, tbuf);
+    case HBO_EP_RELU: {
+      p.po = PO_MAX;
+      return lane(&p, y, y, 0, 0, tbuf);
+    }
+    case HBO_EP_ADD: {
+      p.c0 = C0_X2;
+      return lane(&p, y, op->x2[r * n + col], 0, 0, tbuf);
+    }
+    case HBO_EP_ACT:
+    case HBO_EP_ACT_MUL: {
+      vpass sigma = whole();
+      sigma.act = 1;
+      const uint32_t t = lane(&sigma, y, y, 0, 0, tbuf);
+      vpass gate = whole();
+      gate.b = B_X2;
+      gate.po = PO_SIGNFIX;
+      const uint32_t g = lane(&gate, y, t, 0, 0, tbuf);
+      if (op->op == HBO_EP_ACT) return g;
+      vpass product = whole();
+      product.b = B_X2;
+      return lane(&product, g, op->x2[r * n + col], 0, 0, tbuf);
+    }
+    default: return y;
+  }
+}
+
+int hbo_linear(uint32_t m, uint32_t n, uint32_t kb_total, const uint8_t* a,
+               uint32_t n_planes, const uint8_t* const* w,
+               const uint32_t* modes, uint32_t n_pieces,
+               const hbo_piece* pieces, int onto, uint32_t* c,
+               uint32_t n_ops, const hbo_ep_op* ops, const uint64_t* tbuf,
+               uint8_t* q_out) {
+  if (m % 4 || n % 8) return fail("linear %ux%u is not a multiple of 4x8", m, n);
+  if (q_out && n % 32) return fail("quantized output needs n %% 32 == 0, n = %u", n);
+  if (n_planes < 1 || n_planes > 2 || n_pieces < 1) return fail("bad planes/pieces");
+  for (uint32_t p = 0; p < n_pieces; ++p)
+    if (pieces[p].kb < 1 || pieces[p].kb_offset + pieces[p].kb > kb_total)
+      return fail("piece %u [%u, +%u) outside %u blocks", p, pieces[p].kb_offset,
+                  pieces[p].kb, kb_total);
+  for (uint32_t r = 0; r < m; ++r) {
+    const uint32_t qd = r / 4, t = r % 4;
+    for (uint32_t col = 0; col < n; ++col) {
+      const uint32_t g = col / 8, cl = col % 8;
+      uint32_t acc = onto ? c[(size_t)r * n + col] : 0u;
+      for (uint32_t p = 0; p < n_pieces; ++p) {
+        for (uint32_t l = 0; l < n_planes; ++l) {
+          const uint32_t mode = modes[l];
+          for (uint32_t b = pieces[p].kb_offset; b < pieces[p].kb_offset + pieces[p].kb; ++b) {
+            const uint8_t* aw = a + ((size_t)qd * kb_total + b) * HBO_DDR_WORD;
+            const uint8_t* ww = w[l] + ((size_t)g * kb_total + b) * HBO_DDR_WORD;
+            int32_t sum = 0;
+            for (uint32_t k = 0; k < 32; ++k) {
+              const uint32_t idx = cl * 32 + k;
+              const uint32_t byte = ww[idx / 2];
+              sum += (int32_t)(int8_t)aw[t * 32 + k] *
+                     hbo_weight_value(idx % 2 == 0 ? (byte & 0xFu) : (byte >> 4), mode);
+            }
+            acc = hbo_fp32_add(acc, hbo_block_value(sum, aw[128 + t], ww[128 + cl], mode));
+          }
+        }
+      }
+      for (uint32_t o = 0; o < n_ops; ++o) acc = epilogue(&ops[o], acc, r, n, col, tbuf);
+      c[(size_t)r * n + col] = acc;
+    }
+  }
+  if (q_out) {
+    const uint32_t nb = n / 32;
+    memset(q_out, 0, (size_t)(m / 4) * nb * HBO_DDR_WORD);
+    for (uint32_t qd = 0; qd < m / 4; ++qd) {
+      for (uint32_t b = 0; b < nb; ++b) {
+        uint32_t words[4][32];
+        for (uint32_t qw = 0; qw < 4; ++qw)
+          for (uint32_t t = 0; t < 4; ++t)
+            for (uint32_t l = 0; l < 8; ++l)
+              words[qw][t * 8 + l] = c[(size_t)(4 * qd + t) * n + b * 32 + qw * 8 + l];
+        hbo_quantize_block(&words[0][0], q_out + ((size_t)qd * nb + b) * HBO_DDR_WORD);
+      }
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Batched forms for the tests (no semantics of their own).            */
+/* ------------------------------------------------------------------ */
+void hbo_fp32_add_n(const uint32_t* a, const uint32_t* b, uint32_t* out, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) out[i] = hbo_fp32_add(a[i], b[i]);
+}
+void hbo_fp32_mul_n(const uint32_t* a, const uint32_t* b, uint32_t* out, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) out[i] = hbo_fp32_mul(a[i], b[i]);
+}
+void hbo_fp32_mul_fraction_n(const uint32_t* s, const uint32_t* f, uint32_t* out, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) out[i] = hbo_fp32_mul_fraction(s[i], f[i]);
+}
+void hbo_block_value_n(const int32_t* sum, const uint32_t* as, const uint32_t* ws,
+                       uint32_t mode, uint32_t* out, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) out[i] = hbo_block_value(sum[i], as[i], ws[i], mode);
+}

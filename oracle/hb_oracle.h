@@ -1,0 +1,181 @@
+/*
+ * CPU oracle for the quantized GEMM hot path (test infrastructure only).
+ *
+ * This is a plain-C restatement of the reference CPU path: the ISS GEMM
+ * instruction (tools/iss/gemm_array.cpp), its FP32 arithmetic
+ * (tools/iss/fp32.hpp), the operand formats and packers
+ * (tools/runtime/formats.cpp, tools/compiler/tensors.cpp,
+ * tools/compiler/weights.cpp), the VEC epilogue subset
+ * (tools/iss/lane.cpp, tools/iss/vec_engine.cpp, tools/compiler/vec_rom.cpp)
+ * and the fold order of an emitted linear layer
+ * (tools/compiler/kernels.cpp:343-395).
+ *
+ * Only the tests, the smoke check and the CPU-baseline leg of the benchmark
+ * load this library, and only as the checker.  The product library
+ * (libhotarubi_gpu.so) never links or calls it.
+ *
+ * Every function here is pinned by at least one of: the reference's own
+ * known-answer tests (tests/golden/), the reference FP32 sources compiled
+ * from /root/reference into oracle/_ref, closed-form checks in
+ * tests/test_oracle_*.py (exact rational arithmetic, brute force on tiny
+ * inputs, invariants).  No function is "parity unpinned".
+ */
+#ifndef HB_ORACLE_H_
+#define HB_ORACLE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* On-chip memory geometry (tools/iss/memories.hpp:16-34). */
+enum {
+  HBO_TOKENS = 4,
+  HBO_LANES = 8,
+  HBO_BLOCK = 32,
+  HBO_ABUF_WORD = 132, /* in-ISS word: 128 int8 + 4 scales */
+  HBO_WBUF_WORD = 144, /* 128 nibble bytes + 8 scales + 8 pad */
+  HBO_DDR_WORD = 144,  /* ABUF/WBUF word in DDR (docs/design.md:402-406) */
+  HBO_ABUF_DEPTH = 8192,
+  HBO_WBUF_DEPTH = 2048,
+  HBO_FBUF_DEPTH = 4096,
+  HBO_PBUF_DEPTH = 512,
+  HBO_TBUF_DEPTH = 1024
+};
+
+/* Mirrors iss::GemmCommand (tools/iss/gemm_array.hpp:16-27). */
+typedef struct {
+  uint32_t a_base, a_stride, kb, m, w_base, w_stride, n8, c_base, wmode, acc;
+} hbo_gemm_cmd;
+
+/* Mirrors iss::VecCommand (tools/iss/vec_engine.hpp:70-81). */
+typedef struct {
+  uint32_t entry, quantize, src, src2, dst, rows_q, n8, p_base, aux, imm;
+} hbo_vec_cmd;
+
+/* Last error message of the calling thread ("" if none). */
+const char* hbo_last_error(void);
+
+/* ---- FP32 semantics: tools/iss/fp32.hpp:24-104 ---- */
+uint32_t hbo_fp32_pack(uint32_t sign, int32_t exponent, uint32_t fraction);
+uint32_t hbo_fp32_round(uint32_t sign, int32_t exponent, uint32_t significand,
+                        int guard, int sticky);
+uint32_t hbo_fp32_add(uint32_t a, uint32_t b);
+uint32_t hbo_fp32_mul(uint32_t a, uint32_t b);
+uint32_t hbo_fp32_mul_fraction(uint32_t s, uint32_t fraction);
+
+/* ---- GEMM array: tools/iss/gemm_array.cpp ---- */
+uint32_t hbo_decode_weight_mode(uint32_t wmode);          /* :73-82 */
+int32_t hbo_weight_value(uint32_t nibble, uint32_t mode); /* :84-97 */
+int32_t hbo_scale_bias(uint32_t mode);                    /* :25-35 */
+uint32_t hbo_block_value(int32_t sum, uint32_t a_scale, uint32_t w_scale,
+                         uint32_t mode); /* :99-110 */
+/* ExecuteGemm (:112-149) on ISS-layout images:
+ * abuf[8192][132], wbuf[2048][144], fbuf[4096][32].  Returns 0 on success,
+ * nonzero (message in hbo_last_error) when the preconditions of :113-119
+ * fail; the images are then untouched. */
+int hbo_gemm_exec(const hbo_gemm_cmd* cmd, const uint8_t* abuf,
+                  const uint8_t* wbuf, uint32_t* fbuf);
+/* Access sets of ExecuteGemm (memories.log reads/writes at :127,135,141,145)
+ * as one byte per word: reads_abuf[8192], reads_wbuf[2048], reads_fbuf[4096],
+ * writes_fbuf[4096] (1 = accessed). */
+int hbo_gemm_access(const hbo_gemm_cmd* cmd, uint8_t* reads_abuf,
+                    uint8_t* reads_wbuf, uint8_t* reads_fbuf,
+                    uint8_t* writes_fbuf);
+
+/* ---- formats: tools/runtime/formats.cpp ---- */
+int8_t hbo_quantize_int8(uint32_t bits, int32_t e); /* :35-56 */
+/* EncodeMxint8 (:138-162): x row-major [rows][cols] fp32 bits ->
+ * q [rows][kpad] int8, e [rows][kpad/32] int32, kpad = PadToBlock(cols). */
+int hbo_encode_mxint8(const uint32_t* x, uint32_t rows, uint32_t cols,
+                      int8_t* q, int32_t* e);
+/* PackAbuf (:114-136): q [rows][cols], e [rows][cols/32] -> DDR words
+ * [(rows/4) * (cols/32)][144]. */
+int hbo_pack_abuf(const int8_t* q, const int32_t* e, uint32_t rows,
+                  uint32_t cols, uint8_t* out);
+/* PackFbuf / UnpackFbuf (:72-112): row-major [rows][cols] <-> words. */
+int hbo_pack_fbuf(const uint32_t* x, uint32_t rows, uint32_t cols,
+                  uint32_t* out);
+int hbo_unpack_fbuf(const uint32_t* words, uint32_t rows, uint32_t cols,
+                    uint32_t* out);
+
+/* ---- weights: tools/compiler/tensors.cpp:66-90, weights.cpp:39-88 ---- */
+/* PackWbuf: code [rows][cols] (low 4 bits used), e [rows][cols/32] ->
+ * DDR words [(rows/8) * (cols/32)][144]. */
+int hbo_pack_wbuf(const uint8_t* code, const int32_t* e, uint32_t rows,
+                  uint32_t cols, uint8_t* out);
+/* SplitW8: q -> hi = byte >> 4, lo = byte & 15 (scales shared). */
+void hbo_split_w8(const int8_t* q, size_t count, uint8_t* hi, uint8_t* lo);
+/* CanonicalMxfp4 (weights.cpp:39-70), out has out_rows >= rows rows. */
+int hbo_canonical_mxfp4(const uint8_t* code, const int32_t* e, uint32_t rows,
+                        uint32_t cols, int32_t exponent_shift,
+                        uint32_t out_rows, uint8_t* out_code, int32_t* out_e);
+
+/* ---- VEC lane: tools/iss/lane.cpp ---- */
+uint32_t hbo_interpolate(uint64_t entry, uint32_t fraction);       /* :337 */
+uint32_t hbo_activation(uint32_t prod, const uint64_t* tbuf);       /* :342 */
+uint32_t hbo_post_add(uint32_t prod, uint32_t c1, uint32_t op);     /* :322 */
+uint8_t hbo_quantize_element(uint32_t value, uint32_t emax);        /* :384 */
+int hbo_quantize_block(const uint32_t* words4x32, uint8_t* out132); /* :406 */
+
+/* VecEngine::Execute for library entries 0-9 (ADD, MUL, MAX, ADDP, MULP,
+ * SCALE, COPY, RELU, ACT, ACT_MUL), with and without quantize.  Images in ISS
+ * layout: abuf[8192][132], fbuf[4096][32], pbuf[512][32], tbuf[1024].
+ * Returns nonzero (and leaves the images in an unspecified state) where the
+ * reference calls Fail; 2 for entries outside 0-9. */
+int hbo_vec_exec(const hbo_vec_cmd* cmd, uint8_t* abuf, uint32_t* fbuf,
+                 const uint32_t* pbuf, const uint64_t* tbuf);
+
+/* ---- linear layer: tools/compiler/kernels.cpp:343-395 ---- */
+enum { HBO_EP_NONE = 0, HBO_EP_ADDP = 3, HBO_EP_MULP = 4, HBO_EP_SCALE = 5,
+       HBO_EP_COPY = 6, HBO_EP_RELU = 7, HBO_EP_ACT = 8, HBO_EP_ACT_MUL = 9,
+       HBO_EP_ADD = 0x100 };
+
+typedef struct {
+  uint32_t op;          /* HBO_EP_* (library entry numbers) */
+  uint32_t imm;         /* SCALE factor bits */
+  const uint32_t* vec;  /* ADDP/MULP: n fp32 bits, one per column */
+  const uint32_t* x2;   /* ACT_MUL (up) / ADD (residual): [m][n] fp32 bits */
+} hbo_ep_op;
+
+typedef struct {
+  uint32_t kb_offset, kb;
+} hbo_piece;
+
+/* One linear layer as the emitted GEMM sequence computes it: per output,
+ *   acc = onto ? c[r][n] : +0
+ *   for piece p: for plane l: for block b: acc = Add(acc, BlockValue(...))
+ * then the epilogue ops in order (each with the VEC lane formula), then
+ * optionally QuantizeBlock per 4 tokens x 32 columns.
+ *   a      : A DDR words [(m/4)][kb_total][144] (PackAbuf layout)
+ *   w[l]   : plane l DDR words [(n/8)][kb_total][144] (PackWbuf layout)
+ *   modes[l]: 0 FP4, 1 W8_HI, 2 W8_LO
+ *   c      : fp32 bits row-major [m][n] (input if onto, output always)
+ *   q_out  : if non-NULL, MXINT8 DDR words [(m/4)][(n/32)][144]
+ * m must be a multiple of 4, n of 8 (of 32 with q_out). */
+int hbo_linear(uint32_t m, uint32_t n, uint32_t kb_total, const uint8_t* a,
+               uint32_t n_planes, const uint8_t* const* w,
+               const uint32_t* modes, uint32_t n_pieces,
+               const hbo_piece* pieces, int onto, uint32_t* c,
+               uint32_t n_ops, const hbo_ep_op* ops, const uint64_t* tbuf,
+               uint8_t* q_out);
+
+/* Batched forms for the tests. */
+void hbo_fp32_add_n(const uint32_t* a, const uint32_t* b, uint32_t* out, uint64_t n);
+void hbo_fp32_mul_n(const uint32_t* a, const uint32_t* b, uint32_t* out, uint64_t n);
+void hbo_fp32_mul_fraction_n(const uint32_t* s, const uint32_t* f, uint32_t* out,
+                             uint64_t n);
+void hbo_block_value_n(const int32_t* sum, const uint32_t* a_scale,
+                       const uint32_t* w_scale, uint32_t mode, uint32_t* out,
+                       uint64_t n);
+
+/* GEMM cost model (tools/iss/timing.cpp:65-67,89-93), cycles at 250 MHz. */
+uint64_t hbo_gemm_cycles(const hbo_gemm_cmd* cmd, uint32_t fixed_cycles);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HB_ORACLE_H_ */

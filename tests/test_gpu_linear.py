@@ -1,0 +1,261 @@
+"""hb_linear (the linear layer over DDR words, fused epilogue, requantize)
+and hb_encode_mxint8 on an MI355X against the oracle.
+
+Exact mode: bitwise.  Fast mode: the block products are exact and only the
+FP32 accumulation order differs; tolerance per output row r:
+    max_n |gpu[r][n] - ref[r][n]| <= 1e-5 * max_n |ref[r][n]|   (normwise)
+and, per element, |gpu - ref| <= 2^-20 * sum_b |block value b|."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import helpers
+import hotarubi_amd as hb
+import oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def make_layer(rng, m, n, k, w8, exp_lo=-10, exp_hi=-2):
+    kb = (k + 31) // 32
+    x, a = helpers.activations(rng, m, kb * 32)
+    if w8:
+        planes = list(helpers.w8_planes_from_int8(rng.integers(-127, 128, (n, kb * 32))))
+        modes = [1, 2]
+    else:
+        code, e = helpers.mxfp4_weights(rng, n, kb * 32, exp_lo, exp_hi)
+        planes, modes = [oracle.pack_wbuf(code, e)], [0]
+    return kb, a, planes, modes
+
+
+def run_linear(gpu, m, n, kb, a, planes, modes, ops=(), pieces=None, onto=None, tbuf=None,
+               quantize=False, mode=hb.EXACT):
+    say("linear", dict(m=m, n=n, kb=kb, planes=len(planes), ops=[o[0] for o in ops], pieces=pieces,
+                       onto=onto is not None, quantize=quantize, mode=mode))
+    a_d = dev(a)
+    w_d = [dev(p) for p in planes]
+    c_d = dev(onto.view(np.float32)) if onto is not None else torch.zeros((m, n), dtype=torch.float32, device=DEV)
+    dev_ops = []
+    for kind, arg in ops:
+        if kind in (hb.EP_ADDP, hb.EP_MULP):
+            dev_ops.append((kind, dev(arg.view(np.float32))))
+        elif kind in (hb.EP_ACT_MUL, hb.EP_ADD):
+            dev_ops.append((kind, dev(arg.view(np.float32))))
+        else:
+            dev_ops.append((kind, arg))
+    tb = dev(tbuf.view(np.int64)) if tbuf is not None else None
+    q_d = torch.zeros((((m + 3) // 4) * (n // 32), 144), dtype=torch.uint8, device=DEV) if quantize else None
+    torch.cuda.synchronize()
+    hb.linear(gpu, a=a_d, planes=w_d, modes=modes, c=c_d, m=m, n=n, kb_total=kb, pieces=pieces,
+              onto=onto is not None, ops=dev_ops, tbuf=tb, q_out=q_d, mode=mode)
+    return host(c_d).view(np.uint32), (host(q_d) if quantize else None)
+
+
+def oracle_linear(m, n, kb, a, planes, modes, ops=(), pieces=None, onto=None, tbuf=None,
+                  quantize=False):
+    mp = (m + 3) // 4 * 4
+    c0 = None
+    if onto is not None:
+        c0 = np.zeros((mp, n), np.uint32)
+        c0[:m] = onto
+    oops = []
+    for kind, arg in ops:
+        if kind in (hb.EP_ACT_MUL, hb.EP_ADD):
+            pad = np.zeros((mp, n), np.uint32)
+            pad[:m] = arg
+            oops.append((kind, pad))
+        else:
+            oops.append((kind, arg))
+    c, q = oracle.linear(mp, n, kb, a, planes, modes, pieces=pieces, c=c0, onto=onto is not None,
+                         ops=oops, tbuf=tbuf, quantize=quantize)
+    return c[:m], q
+
+
+def assert_bits(got, want):
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} differ; first {bad[0]}: {got[tuple(bad[0])]:#x} vs {want[tuple(bad[0])]:#x}"
+
+
+# ---- the workloads: W8 M=64 K=960 N=2560 + MULP + ADDP; MXFP4 K=2560 N=960 ----
+
+def test_w8_layer_with_scale_and_bias(gpu):
+    rng = np.random.default_rng(1)
+    m, n, k = 64, 2560, 960
+    kb, a, planes, modes = make_layer(rng, m, n, k, True)
+    scale = np.asarray(rng.uniform(0.001, 0.02, n), np.float32).view(np.uint32)
+    bias = np.asarray(rng.normal(0, 0.1, n), np.float32).view(np.uint32)
+    ops = [(hb.EP_MULP, scale), (hb.EP_ADDP, bias)]
+    got, _ = run_linear(gpu, m, n, kb, a, planes, modes, ops)
+    want, _ = oracle_linear(m, n, kb, a, planes, modes, ops)
+    assert_bits(got, want)
+
+
+@pytest.mark.parametrize("m", [1, 16, 128])
+def test_mxfp4_layer(gpu, m):
+    rng = np.random.default_rng(2 + m)
+    n, k = 960, 2560
+    kb, a, planes, modes = make_layer(rng, m, n, k, False)
+    got, _ = run_linear(gpu, m, n, kb, a, planes, modes)
+    want, _ = oracle_linear(m, n, kb, a, planes, modes)
+    assert_bits(got, want)
+
+
+def block_abs_sums(m, n, kb, a, planes, modes):
+    """sum_b |block value| per output (the fast-mode error scale)."""
+    qa = a.reshape(-1, kb, 144)
+    tot = np.zeros((qa.shape[0] * 4, n))
+    for plane, mode in zip(planes, modes):
+        w = plane.reshape(n // 8, kb, 144)
+        nib = np.empty((n // 8, kb, 8, 32), np.int64)
+        nib[..., 0::2] = (w[:, :, :128] & 15).reshape(n // 8, kb, 8, 16)
+        nib[..., 1::2] = (w[:, :, :128] >> 4).reshape(n // 8, kb, 8, 16)
+        mag = np.array([0, 1, 2, 3, 4, 6, 8, 12])
+        if mode == 0:
+            v = np.where(nib & 8, -mag[nib & 7], mag[nib & 7])
+        elif mode == 1:
+            v = np.where(nib & 8, nib - 16, nib)
+        else:
+            v = nib
+        bias = {0: -7, 1: -8, 2: -12}[mode]
+        aq = qa[:, :, :128].view(np.int8).reshape(-1, kb, 4, 32).astype(np.int64)
+        ea = qa[:, :, 128:132].astype(np.int64)
+        ew = w[:, :, 128:136].astype(np.int64)
+        for b in range(kb):
+            s = np.einsum("qtk,gck->qtgc", aq[:, b], v[:, b]).reshape(-1, n)
+            sc = (ea[:, b, :].reshape(-1, 1) - 127) + (ew[:, b, :].reshape(1, -1) - 127) + bias
+            tot += np.abs(s) * np.exp2(sc.astype(np.float64))
+    return tot[:m]
+
+
+@pytest.mark.parametrize("m,w8", [(128, False), (1024, False), (64, True), (2048, True)])
+def test_fast_mode_tolerance(gpu, m, w8):
+    rng = np.random.default_rng(10 + m)
+    n, k = (960, 2560) if not w8 else (768, 768)
+    kb, a, planes, modes = make_layer(rng, m, n, k, w8)
+    got, _ = run_linear(gpu, m, n, kb, a, planes, modes, mode=hb.FAST)
+    want, _ = oracle_linear(m, n, kb, a, planes, modes)
+    g, w = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
+    err = np.abs(g - w)
+    row_scale = np.abs(w).max(axis=1, keepdims=True)
+    assert (err <= 1e-5 * row_scale).all(), float((err / row_scale).max())
+    if m <= 128:
+        assert (err <= 2.0 ** -20 * block_abs_sums(m, n, kb, a, planes, modes) + 1e-30).all()
+
+
+@pytest.mark.parametrize("w8", [False, True])
+def test_pieces_and_onto(gpu, w8):
+    rng = np.random.default_rng(20 + w8)
+    m, n, k = 96, 256, 640
+    kb, a, planes, modes = make_layer(rng, m, n, k, w8)
+    onto = helpers.random_fp32_words(rng, (m, n), 120, 130)
+    pieces = [(12, 8), (0, 5), (5, 7)]
+    got, _ = run_linear(gpu, m, n, kb, a, planes, modes, pieces=pieces, onto=onto)
+    want, _ = oracle_linear(m, n, kb, a, planes, modes, pieces=pieces, onto=onto)
+    assert_bits(got, want)
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+def test_epilogue_ops_and_requantize(gpu, act):
+    rng = np.random.default_rng(30)
+    m, n, k = 64, 512, 256
+    kb, a, planes, modes = make_layer(rng, m, n, k, False, -6, 0)
+    tbuf = helpers.activation_table(act)
+    up = helpers.random_fp32_words(rng, (m, n), 120, 130)
+    res = helpers.random_fp32_words(rng, (m, n), 118, 128)
+    vec = helpers.random_fp32_words(rng, (n,), 120, 128)
+    imm = int(helpers.random_fp32_words(rng, (1,), 124, 128)[0])
+    for ops in ([(hb.EP_ACT, None)], [(hb.EP_ACT_MUL, up)], [(hb.EP_RELU, None), (hb.EP_SCALE, imm)],
+                [(hb.EP_MULP, vec), (hb.EP_ADD, res), (hb.EP_COPY, None)],
+                [(hb.EP_ADDP, vec), (hb.EP_ACT, None), (hb.EP_MULP, vec)]):
+        for quantize in (False, True):
+            got, gq = run_linear(gpu, m, n, kb, a, planes, modes, ops, tbuf=tbuf, quantize=quantize)
+            want, wq = oracle_linear(m, n, kb, a, planes, modes, ops, tbuf=tbuf, quantize=quantize)
+            assert_bits(got, want)
+            if quantize:
+                assert np.array_equal(gq, wq)
+
+
+@pytest.mark.parametrize("m", [1, 3, 5, 30, 37])
+def test_rows_not_a_multiple_of_four(gpu, m):
+    rng = np.random.default_rng(40 + m)
+    n, k = 320, 384
+    kb, a, planes, modes = make_layer(rng, m, n, k, m % 2 == 0)
+    res = helpers.random_fp32_words(rng, (m, n), 118, 128)
+    ops = [(hb.EP_ADD, res)]
+    got, _ = run_linear(gpu, m, n, kb, a, planes, modes, ops)
+    want, _ = oracle_linear(m, n, kb, a, planes, modes, ops)
+    assert_bits(got, want)
+
+
+def test_extreme_scales_exact(gpu):
+    rng = np.random.default_rng(50)
+    m, n, k = 64, 128, 256
+    kb, a, planes, modes = make_layer(rng, m, n, k, False, -127, 127)
+    a = a.copy()
+    a.reshape(-1, 144)[::7, 128] = 1      # tiny activation scales in some words
+    got, _ = run_linear(gpu, m, n, kb, a, planes, modes)
+    want, _ = oracle_linear(m, n, kb, a, planes, modes)
+    assert_bits(got, want)
+
+
+def test_batched_layers(gpu):
+    rng = np.random.default_rng(60)
+    layers, m, n, k = 5, 128, 192, 512
+    kb = k // 32
+    data = [make_layer(rng, m, n, k, False) for _ in range(layers)]
+    a_all = dev(np.stack([d[1] for d in data]))
+    w_all = dev(np.stack([d[2][0] for d in data]))
+    c_all = torch.zeros((layers, m, n), dtype=torch.float32, device=DEV)
+    descs = [hb.linear_desc(m, n, kb, a_all[i], [w_all[i]], [0], c_all[i]) for i in range(layers)]
+    torch.cuda.synchronize()
+    say("batched", layers)
+    hb.linear_batched(descs, gpu)
+    got = host(c_all).view(np.uint32)
+    for i, d in enumerate(data):
+        want, _ = oracle_linear(m, n, kb, d[1], d[2], d[3])
+        assert_bits(got[i], want)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 32), (4, 960), (7, 100), (64, 2560)])
+def test_encode_mxint8(gpu, rows, cols):
+    rng = np.random.default_rng(rows * cols)
+    x = (rng.standard_normal((rows, cols)) * np.exp2(rng.integers(-20, 20, (rows, cols)))).astype(np.float32)
+    x[0, :5] = [0.0, -0.0, 1e-40, -1e-39, 3.0]
+    say("encode", rows, cols)
+    x_d = dev(x)
+    quads, blocks = (rows + 3) // 4, (cols + 31) // 32
+    out = torch.full((quads * blocks, 144), 0xAB, dtype=torch.uint8, device=DEV)
+    torch.cuda.synchronize()
+    hb.encode_mxint8(x_d, rows, cols, out, gpu)
+    got = host(out)
+    xp = np.zeros((quads * 4, cols), np.float32)
+    xp[:rows] = x
+    q, e = oracle.encode_mxint8(oracle.f32_bits(xp))
+    assert np.array_equal(got, oracle.pack_abuf(q, e))
+
+
+def test_encode_rejects_non_finite(gpu):
+    x_d = dev(np.array([[1.0, np.inf, 2.0]], np.float32))
+    out = torch.zeros((1, 144), dtype=torch.uint8, device=DEV)
+    torch.cuda.synchronize()
+    with pytest.raises(hb.HbError):
+        hb.encode_mxint8(x_d, 1, 3, out, gpu)

@@ -1,0 +1,97 @@
+"""hb_vec_exec (VEC library entries 0-9) on an MI355X against the oracle."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import helpers
+import hotarubi_amd as hb
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def filled(seed, lo=100, hi=140):
+    rng = np.random.default_rng(seed)
+    m = oracle.Memories()
+    m.fbuf[...] = helpers.random_fp32_words(rng, m.fbuf.shape, lo, hi)
+    m.pbuf[...] = helpers.random_fp32_words(rng, m.pbuf.shape, lo, hi)
+    m.tbuf[...] = helpers.activation_table("silu" if seed % 2 else "gelu")
+    return m
+
+
+def run_both(mem, fields, gpu):
+    say("vec case", fields)
+    dm = hb.DeviceMemories(gpu)
+    dm.upload_all(mem.abuf, mem.wbuf, mem.fbuf, mem.pbuf, mem.tbuf)
+    hb.vec_execute(hb.VecCommand(**fields), dm)
+    got_f, got_a = dm.download(hb.FBUF), dm.download(hb.ABUF)
+    dm.close()
+    want = mem.copy()
+    vc = oracle.VecCmd()
+    for k, v in fields.items():
+        setattr(vc, k, int(v))
+    assert oracle.vec_exec(vc, want) == 0, oracle.last_error()
+    assert np.array_equal(got_f, want.fbuf), np.argwhere(got_f != want.fbuf)[:3]
+    assert np.array_equal(got_a, want.abuf), np.argwhere(got_a != want.abuf)[:3]
+
+
+@pytest.mark.parametrize("entry", range(10))
+@pytest.mark.parametrize("quantize", [0, 1])
+def test_entries(gpu, entry, quantize):
+    mem = filled(entry * 2 + quantize)
+    run_both(mem, dict(entry=entry, quantize=quantize, src=100, src2=900, dst=2000 if not quantize else 7000,
+                       rows_q=5, n8=12, p_base=20, imm=int(helpers.random_fp32_words(
+                           np.random.default_rng(entry), (1,), 120, 130)[0]) if entry == 5 else 3000), gpu)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_special_values(gpu, seed):
+    """Zeros, -0, subnormals, inf/NaN encodings and values near the bottom of
+    the normal range: the integer fallbacks of the lane arithmetic."""
+    mem = filled(50 + seed, 0, 255)
+    rng = np.random.default_rng(seed)
+    special = np.array([0, 0x80000000, 1, 0x807FFFFF, 0x7F800000, 0xFF800000, 0x7FC00000,
+                        0x00800000, 0x00FFFFFF, 0x41800000, 0xC1800001], np.uint32)
+    mem.fbuf.flat[rng.integers(0, mem.fbuf.size, 20000)] = special[rng.integers(0, len(special), 20000)]
+    for entry in range(10):
+        run_both(mem, dict(entry=entry, quantize=entry % 2, src=0, src2=1500, dst=3000 if entry % 2 == 0 else 100,
+                           rows_q=7, n8=16, p_base=0, imm=0x00C00000 if entry == 5 else 2400), gpu)
+
+
+def test_in_place_and_trailing_overlap(gpu):
+    mem = filled(70)
+    run_both(mem, dict(entry=4, src=100, dst=100, rows_q=3, n8=10, p_base=3), gpu)       # in place
+    run_both(mem, dict(entry=6, src=100, dst=95, rows_q=3, n8=10), gpu)                   # dst trails src
+    run_both(mem, dict(entry=8, src=200, dst=200, rows_q=2, n8=8, imm=200), gpu)          # scratch == dst
+
+
+def test_wrap_and_repeated_writes(gpu):
+    mem = filled(71)
+    run_both(mem, dict(entry=6, src=100, dst=4090, rows_q=4, n8=24), gpu)                 # dst wraps FBUF
+    run_both(mem, dict(entry=7, quantize=1, src=0, dst=8000, rows_q=300, n8=128), gpu)    # wraps ABUF
+
+
+@pytest.mark.parametrize("fields,text", [
+    (dict(entry=6, src=10, dst=12, rows_q=1, n8=5), "a PASS reads FBUF word 12 after writing it"),
+    (dict(entry=6, src=0, dst=0, rows_q=0, n8=5), "a PASS has 0 quads and 5 words"),
+    (dict(entry=6, quantize=1, rows_q=2, n8=6), "quantized word 0 arrives out of order"),
+    (dict(entry=6, quantize=1, rows_q=1, n8=6), "a PASS ends inside a block of 4 quantized words"),
+])
+def test_failures(gpu, fields, text):
+    say("vec reject", fields)
+    dm = hb.DeviceMemories(gpu)
+    with pytest.raises(hb.HbBadCommand) as err:
+        hb.vec_execute(hb.VecCommand(**fields), dm)
+    assert err.value.message == text
+    with pytest.raises(hb.HbError) as err:
+        hb.vec_execute(hb.VecCommand(entry=12, rows_q=1, n8=4), dm)
+    assert err.value.code == hb.HB_EUNSUPPORTED
+    dm.close()

@@ -347,8 +347,9 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
   const uint8_t* w1 = g.w[1];
   uint32_t* c = g.c;
   uint8_t* q_out = g.q_out;
+  const TileId tile = LogicalTile(g.gx, g.gy, g.gz);
   if (kLinear) {
-    const uint32_t z = blockIdx.z;
+    const uint32_t z = tile.z;
     a += z * g.a_batch;
     w0 += z * g.w_batch;
     w1 += z * g.w_batch;
@@ -359,7 +360,7 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t wm = wave / T::kWaveN, wn = wave % T::kWaveN;
   const uint32_t row16 = lane & 15, kq = lane >> 4;
-  const uint32_t q0 = blockIdx.y * (kBM / 4), g0 = blockIdx.x * (kBN / 8);
+  const uint32_t q0 = tile.y * (kBM / 4), g0 = tile.x * (kBN / 8);
   const uint32_t row0 = q0 * 4, col0 = g0 * 8;
 
   const Lane<T> ln;
@@ -588,13 +589,19 @@ __global__ __launch_bounds__(32) void GemmAliasKernel(GemmArgs g) {
 }  // namespace
 
 template <bool kLinear>
-hipError_t LaunchTiles(const GemmArgs& args, uint32_t batch, hipStream_t stream) {
+hipError_t LaunchTiles(const GemmArgs& in, uint32_t batch, hipStream_t stream) {
+  GemmArgs args = in;
+  args.gz = batch;
   if (args.quads * 4 <= 32) {
-    const dim3 grid((args.groups + 31) / 32, (args.quads + 7) / 8, batch);
-    hipLaunchKernelGGL((GemmTileKernel<kLinear, 32, 256>), grid, dim3(kThreads), 0, stream, args);
+    args.gx = (args.groups + 31) / 32;
+    args.gy = (args.quads + 7) / 8;
+    hipLaunchKernelGGL((GemmTileKernel<kLinear, 32, 256>), dim3(args.gx * args.gy * batch),
+                       dim3(kThreads), 0, stream, args);
   } else {
-    const dim3 grid((args.groups + 15) / 16, (args.quads + 31) / 32, batch);
-    hipLaunchKernelGGL((GemmTileKernel<kLinear, 128, 128>), grid, dim3(kThreads), 0, stream, args);
+    args.gx = (args.groups + 15) / 16;
+    args.gy = (args.quads + 31) / 32;
+    hipLaunchKernelGGL((GemmTileKernel<kLinear, 128, 128>), dim3(args.gx * args.gy * batch),
+                       dim3(kThreads), 0, stream, args);
   }
   return hipGetLastError();
 }
@@ -611,7 +618,9 @@ hipError_t LaunchGemmInstrAliased(const GemmArgs& args, hipStream_t stream) {
 }
 
 hipError_t LaunchLinear(const GemmArgs& args, uint32_t batch, bool fast, hipStream_t stream) {
-  (void)fast;  // the exact kernel meets the fast-mode tolerance
+  if (fast && args.n_planes == 1 && args.modes[0] == kModeFp4)
+    return LaunchLinearFastFp4(args, batch, stream);
+  // every other layer runs exactly (which meets the fast-mode tolerance)
   return LaunchTiles<true>(args, batch, stream);
 }
 

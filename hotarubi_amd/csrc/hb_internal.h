@@ -49,12 +49,36 @@ struct GemmArgs {
   uint8_t* q_out;     // MXINT8 DDR words [quads][n/32] or null
   // batched linear: per-layer strides (bytes / elements), 0 for one layer
   uint64_t a_batch, w_batch, c_batch, q_batch;
+  // tile grid (x: column tiles, y: row tiles, z: layers), launched 1-D
+  uint32_t gx, gy, gz;
 };
+
+// Workgroup -> tile mapping.  The hardware deals workgroups round-robin over
+// the 8 XCDs, each with its own L2; remapping puts consecutive logical tiles
+// (x fastest, then y, then layer z) on one XCD, so the workgroups that share
+// a layer's weights and activations share an L2.
+constexpr uint32_t kXcds = 8;
+struct TileId {
+  uint32_t x, y, z;
+};
+__device__ __forceinline__ TileId LogicalTile(uint32_t gx, uint32_t gy, uint32_t gz) {
+  const uint32_t b = blockIdx.x;
+  const uint32_t total = gx * gy * gz;
+  uint32_t l = b;
+  if (total % kXcds == 0) l = (b % kXcds) * (total / kXcds) + b / kXcds;
+  TileId t;
+  t.x = l % gx;
+  t.y = (l / gx) % gy;
+  t.z = l / (gx * gy);
+  return t;
+}
 
 // Launchers (hb_gemm.hip).
 hipError_t LaunchGemmInstr(const GemmArgs& args, hipStream_t stream);
 hipError_t LaunchGemmInstrAliased(const GemmArgs& args, hipStream_t stream);
 hipError_t LaunchLinear(const GemmArgs& args, uint32_t batch, bool fast, hipStream_t stream);
+// Fast MXFP4 path (hb_fast.hip): one FP4 plane, block-scaled f8f6f4 MFMA.
+hipError_t LaunchLinearFastFp4(const GemmArgs& args, uint32_t batch, hipStream_t stream);
 
 // VEC (hb_vec.hip).
 struct VecPass {

@@ -279,7 +279,10 @@ __global__ __launch_bounds__(kBM * 4) void FastFp4Kernel(GemmArgs g) {
       acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(alo, b, acc[j], 2, 4, 0, sa_lo, 0, sw);
     }
     // Keep the step's matrix work inside the step: sinking it past later
-    // steps' barriers only lengthens the operands' live ranges.
+    // steps' barriers only lengthens the operands' live ranges.  The empty
+    // asm emits no instruction.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(acc[j]));
     __builtin_amdgcn_sched_barrier(0);
   };
   // Loads issue in program order (the fences stop the scheduler from

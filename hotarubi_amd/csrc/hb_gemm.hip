@@ -33,6 +33,8 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -65,14 +67,16 @@ struct Step {
   uint32_t p, l, b;  // piece, plane, block within the piece
 };
 
-__device__ __forceinline__ void Advance(Step& s, const GemmArgs& g) {
-  if (++s.b == g.piece_kb[s.p]) {
-    s.b = 0;
-    if (++s.l == g.n_planes) {
-      s.l = 0;
-      ++s.p;
-    }
-  }
+// The step after s in fold order (pieces, planes, blocks), by selects only:
+// the step loop stays one basic block.
+__device__ __forceinline__ Step Next(const Step& s, const GemmArgs& g) {
+  Step n;
+  const bool wrap_b = s.b + 1 == g.piece_kb[s.p];
+  const bool wrap_l = wrap_b && s.l + 1 == g.n_planes;
+  n.b = wrap_b ? 0u : s.b + 1;
+  n.l = wrap_l ? 0u : (wrap_b ? s.l + 1 : s.l);
+  n.p = wrap_l ? s.p + 1 : s.p;
+  return n;
 }
 
 template <bool kLinear>
@@ -137,6 +141,7 @@ struct Staged {
   uint32_t a[kA4];
   uint32_t w[kW4];
   uint32_t sa, sw, plane;
+  bool zero_a;  // a surplus step past the end: A stages as zeros
 };
 
 // Per-thread byte offsets of the staged bytes within a block's words
@@ -252,6 +257,8 @@ __device__ __forceinline__ bool StoreBlock(const S& st, const Lane<T>& ln, uint3
   uint32_t ab[2 * T::kA4];
 #pragma unroll
   for (int i = 0; i < T::kA4; ++i) ConvertA4(st.a[i], fa, fc, ab + 2 * i);
+#pragma unroll
+  for (int i = 0; i < 2 * T::kA4; ++i) ab[i] = st.zero_a ? 0u : ab[i];
   uint32_t* da = reinterpret_cast<uint32_t*>(lds_a + ln.r * kLdsRow + ln.aofs);
   if (T::kA4 == 4) {
     reinterpret_cast<u32x4*>(da)[0] = u32x4{ab[0], ab[1], ab[2], ab[3]};
@@ -273,7 +280,7 @@ __device__ __forceinline__ bool StoreBlock(const S& st, const Lane<T>& ln, uint3
   u32x4* dw = reinterpret_cast<u32x4*>(lds_w + ln.col * kLdsRow + ln.wofs * 2);
 #pragma unroll
   for (int i = 0; i < T::kW4; ++i) dw[i] = u32x4{wb[4 * i], wb[4 * i + 1], wb[4 * i + 2], wb[4 * i + 3]};
-  if (ln.wofs == 0) lds_ws[ln.col] = (uint8_t)st.sw;
+  lds_ws[ln.col] = (uint8_t)st.sw;  // both threads of a column store the same byte
   return st.sa < kSafeLo || st.sa > kSafeHi || st.sw < kSafeLo || st.sw > kSafeHi;
 }
 
@@ -372,6 +379,7 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
     lut[l * 256 + tid] = Bf16OfInt(WeightValue(tid & 15u, mode)) |
                          (Bf16OfInt(WeightValue(tid >> 4, mode)) << 16);
   }
+  __syncthreads();  // the table and the cleared flag are visible to every wave
 
   // Output (i, j, v) of this lane: tile row wm*kTM + i*16 + kq*4 + v,
   // tile column wn*kTN + j*16 + row16 (16x16 MFMA accumulator layout).
@@ -393,32 +401,38 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
         acc[i][j][v] = __uint_as_float(init);
       }
 
+  // The step loop is one basic block: every wave runs every step (surplus
+  // steps of the last iteration repeat the last block with A zeroed, adding
+  // +0), the load cursor advances by selects, and scale bytes outside the
+  // safe window are collected per thread and acted on once, after the loop.
   const uint32_t total = g.total_steps;
   Step ls{0, 0, 0};  // load cursor; stays on the last step once there
   uint32_t loaded = 0;
+  // Loads issue in program order (the fences stop the scheduler from mixing
+  // the two register sets), so the in-order load counter lets each compute
+  // wait for exactly its own set.
   auto load_chunk = [&](S* set) {
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int b = 0; b < kChunk; ++b) {
       LoadBlock<kLinear, T>(g, a, w0, w1, offs, ls, set[b]);
-      if (loaded + 1 < total) Advance(ls, g);
+      set[b].zero_a = loaded >= total;
+      const Step nx = Next(ls, g);
+      const bool adv = loaded + 1 < total;
+      ls.p = adv ? nx.p : ls.p;
+      ls.l = adv ? nx.l : ls.l;
+      ls.b = adv ? nx.b : ls.b;
       ++loaded;
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
-  bool slow = false;
   auto compute_chunk = [&](const S* set, uint32_t base) {
 #pragma unroll
     for (int b = 0; b < kChunk; ++b) {
-      const uint32_t step = base + b;
-      if (step >= total || slow) break;
-      const uint32_t buf = step & 1;
+      const uint32_t buf = (base + b) & 1;
       unsafe |= StoreBlock<T>(set[b], ln, g.modes[set[b].plane], lds_a[buf], lds_w[buf],
                               lds_ws[buf], lut);
-      if (unsafe) lds_unsafe = 1;
       __syncthreads();
-      if (lds_unsafe) {
-        slow = true;
-        break;
-      }
       const int32_t wbias = ScaleBias(g.modes[set[b].plane]);
       bf16x8 af[T::kTI], bfr[T::kTJ];
       float fw[T::kTJ];
@@ -441,74 +455,82 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(bv[v], fw[j], acc[i][j][v]);
         }
+      // Anchor the fold here: left free, the compiler sinks every step's
+      // (pure) folds to the end of the iteration, keeping all the steps'
+      // block values live at once.  The empty asm emits no instruction.
+#pragma unroll
+      for (int i = 0; i < T::kTI; ++i)
+#pragma unroll
+        for (int j = 0; j < T::kTJ; ++j) asm volatile("" : "+v"(acc[i][j]));
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // Ping-pong over two register sets: every iteration issues the same
-  // number of loads (past the end they repeat the last block), so the wait
-  // before consuming one set is exactly "the other set's loads".
+  // Ping-pong over two register sets: each compute consumes one set while
+  // the other set's loads are in flight.
   S set0[kChunk], set1[kChunk];
   load_chunk(set0);
-  for (uint32_t base = 0; base < total && !slow; base += 2 * kChunk) {
+  for (uint32_t base = 0; base < total; base += 2 * kChunk) {
     load_chunk(set1);
     compute_chunk(set0, base);
     load_chunk(set0);
     compute_chunk(set1, base + kChunk);
   }
+  if (unsafe) lds_unsafe = 1;
+  __syncthreads();
+  const bool slow = lds_unsafe != 0;
 
-  // Results as FP32 bits; the slow path recomputes the whole tile exactly.
-  uint32_t out[T::kTI][T::kTJ][4];
+  // Results as FP32 bits in one 16-value register vector per row tile i
+  // (element e = 4 * j + v).  i is unrolled and e, where a loop over it is
+  // not, is a wave-uniform index into the vector, so nothing goes through
+  // scratch memory.  The slow path recomputes the whole tile exactly.
+  static_assert(T::kTJ == 4, "four 16-column tiles per wave");
+  f32x16 res[T::kTI];
 #pragma unroll
-  for (int i = 0; i < T::kTI; ++i)
+  for (int i = 0; i < T::kTI; ++i) {
+    const f32x8 lo = __builtin_shufflevector(acc[i][0], acc[i][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    const f32x8 hi = __builtin_shufflevector(acc[i][2], acc[i][3], 0, 1, 2, 3, 4, 5, 6, 7);
+    res[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
 #pragma unroll
-    for (int j = 0; j < T::kTJ; ++j)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const uint32_t bits = __float_as_uint(acc[i][j][v]);
-        out[i][j][v] = bits == kSign ? 0u : bits;
-      }
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t bits = __float_as_uint(res[i][e]);
+      res[i][e] = __uint_as_float(bits == kSign ? 0u : bits);
+    }
+  }
+  const uint32_t row_l = row0 + wm * T::kTM + kq * 4;
+  const uint32_t col_l = col0 + wn * T::kTN + row16;
   if (slow) {
 #pragma unroll
     for (int i = 0; i < T::kTI; ++i)
-#pragma unroll
-      for (int j = 0; j < T::kTJ; ++j)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const uint32_t row = row0 + wm * T::kTM + i * 16 + kq * 4 + v;
-          const uint32_t col = col0 + wn * T::kTN + j * 16 + row16;
-          if ((row >> 2) >= g.quads || (col >> 3) >= g.groups) continue;
-          uint32_t init = 0;
-          if (g.acc && (!kLinear || row < g.m)) init = *CElem<kLinear>(g, c, row, col);
-          out[i][j][v] = SlowOutput<kLinear>(g, a, w0, w1, init, row, col);
-        }
+      for (uint32_t e = 0; e < 16; ++e) {
+        const uint32_t row = row_l + i * 16 + (e & 3), col = col_l + (e >> 2) * 16;
+        if ((row >> 2) >= g.quads || (col >> 3) >= g.groups) continue;
+        uint32_t init = 0;
+        if (g.acc && (!kLinear || row < g.m)) init = *CElem<kLinear>(g, c, row, col);
+        res[i][e] = __uint_as_float(SlowOutput<kLinear>(g, a, w0, w1, init, row, col));
+      }
   }
 
-  // Epilogue ops (op-major so each op's element loop unrolls), then stores.
+  // Epilogue ops, then stores.
   if (kLinear) {
     for (uint32_t o = 0; o < g.n_ops; ++o) {
 #pragma unroll
       for (int i = 0; i < T::kTI; ++i)
-#pragma unroll
-        for (int j = 0; j < T::kTJ; ++j)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const uint32_t row = row0 + wm * T::kTM + i * 16 + kq * 4 + v;
-            const uint32_t col = col0 + wn * T::kTN + j * 16 + row16;
-            if ((row >> 2) < g.quads && (col >> 3) < g.groups)
-              out[i][j][v] = EpOp(g, o, out[i][j][v], row, col, row < g.m);
-          }
+        for (uint32_t e = 0; e < 16; ++e) {
+          const uint32_t row = row_l + i * 16 + (e & 3), col = col_l + (e >> 2) * 16;
+          if ((row >> 2) < g.quads && (col >> 3) < g.groups)
+            res[i][e] = __uint_as_float(EpOp(g, o, __float_as_uint(res[i][e]), row, col, row < g.m));
+        }
     }
   }
 #pragma unroll
   for (int i = 0; i < T::kTI; ++i)
 #pragma unroll
-    for (int j = 0; j < T::kTJ; ++j)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const uint32_t row = row0 + wm * T::kTM + i * 16 + kq * 4 + v;
-        const uint32_t col = col0 + wn * T::kTN + j * 16 + row16;
-        const bool in_tile = (row >> 2) < g.quads && (col >> 3) < g.groups;
-        if (in_tile && (!kLinear || row < g.m)) *CElem<kLinear>(g, c, row, col) = out[i][j][v];
-      }
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t row = row_l + i * 16 + (e & 3), col = col_l + (e >> 2) * 16;
+      const bool in_tile = (row >> 2) < g.quads && (col >> 3) < g.groups;
+      if (in_tile && (!kLinear || row < g.m))
+        *CElem<kLinear>(g, c, row, col) = __float_as_uint(res[i][e]);
+    }
 
   // MXINT8 requantize: one ABUF word per quad and 32 columns.  A quad is the
   // 4 accumulator rows (v) of one lane group (kq); a 32-column block is two
@@ -524,7 +546,8 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
         uint32_t emax[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          uint32_t e = max(ExpField(out[i][jb][v]), ExpField(out[i][jb + 1][v]));
+          uint32_t e = max(ExpField(__float_as_uint(res[i][4 * jb + v])),
+                           ExpField(__float_as_uint(res[i][4 * jb + 4 + v])));
           e = max(e, (uint32_t)__shfl_xor((int)e, 1));
           e = max(e, (uint32_t)__shfl_xor((int)e, 2));
           e = max(e, (uint32_t)__shfl_xor((int)e, 4));
@@ -537,7 +560,8 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
           for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-              word[v * 32 + jj * 16 + row16] = QuantizeElement(out[i][jb + jj][v], emax[v]);
+              word[v * 32 + jj * 16 + row16] =
+                  QuantizeElement(__float_as_uint(res[i][4 * (jb + jj) + v]), emax[v]);
           const uint32_t e_own =
               row16 == 0 ? emax[0] : row16 == 1 ? emax[1] : row16 == 2 ? emax[2] : emax[3];
           if (row16 < 4) word[128 + row16] = (uint8_t)ScaleByteOf(e_own);

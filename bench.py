@@ -1,22 +1,31 @@
 """Benchmark: quantized GEMM TOPS and roofline fraction on one MI355X.
 
-Workload (the metric's configuration): an MXFP4 linear layer, weights
-E2M1 [N=960][K=2560] with E8M0 block-32 scales (exponents -10..-2), MXINT8
-activations [M=128][K=2560] from N(0,1), FP32 output.  One step = one pass
-over a batch of L independent layers of that shape (distinct weights and
-activations, L * 2.24 MB > the 256 MB last-level cache), launched as one
-batched kernel; the inputs are resident in HBM before timing starts.
+Headline workload: an MXFP4 linear layer, weights E2M1 [N=960][K=2560] with
+E8M0 block-32 scales (exponents -10..-2), MXINT8 activations [M=128][K=2560]
+from N(0,1), FP32 output, fast mode (block-scaled FP6 x FP4 matrix cores,
+FP32 accumulation order differs from the NPU's; max relative error <= 1e-5).
+One step = one pass over L independent layers of that shape (distinct weights
+and activations, L * 2.1 MB > the 256 MB last-level cache) in one batched
+launch; inputs are resident in HBM before timing starts.
+
+Extra fields (skipped with --quick): the same workload in exact mode (bitwise
+equal to the NPU), the M sweep {1, 16, 1024} in fast mode, and the W8 layer
+M=64 K=960 N=2560 with per-channel scale (MULP) and bias (ADDP).
 
     python bench.py [--steps K] [--warmup W] [--mode exact|fast] [--layers L]
+                    [--quick] [--no-cpu] [--copy-probe MIB]
 
 Prints one JSON line.  The CPU baseline times the oracle (a C restatement of
 the reference's CPU path, single thread) on one layer of the same shape.
+--copy-probe copies MIB MiB on the device three times first (a plain copy of
+known size, to calibrate HBM byte counters under a profiler).
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -25,22 +34,26 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
-MFMA_PEAK_TOPS = {"int8": 5000.0, "fp8": 5000.0, "bf16": 2500.0, "fp4": 10100.0}
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+# Dense MFMA peaks (TFLOP/s or TOPS) of the instruction class each kernel uses.
+MFMA_PEAK = {"bf16": 2500.0, "fp6_fp4": 10100.0, "int8": 5000.0}
+METRIC = "quantized GEMM TOPS & % MFMA/HBM roofline (W8, MXFP4); SmolVLA step ms"
+PROFILES = os.path.join(ROOT, "profiles")
 
 
-def layer_bytes(m, n, kb, w_bits=4):
-    """Algorithmic bytes: A MXINT8 + W (4- or 8-bit + E8M0) + C fp32."""
+def layer_bytes(m, n, kb, w_bits, n_vectors=0):
+    """Algorithmic bytes of one layer: A MXINT8 + W (E8M0 per 32) + C fp32
+    + fp32 epilogue vectors."""
     k = kb * 32
-    a = m * k * (1 + 1 / 32)
-    w = n * k * (w_bits / 8 + 1 / 32)
-    c = 4 * m * n
-    return a + w + c
+    return m * k * (1 + 1 / 32) + n * k * (w_bits / 8 + 1 / 32) + 4 * m * n + 4 * n * n_vectors
 
 
-def make_inputs(rng, m, n, kb):
-    """Synthetic MXINT8 activations and MXFP4 weights in DDR word layout,
-    generated directly (no oracle): A words [m/4][kb][144], W words [n/8][kb][144]."""
+def make_inputs(rng, m, n, kb, w8=False):
+    """Synthetic operands in DDR word layout, generated directly (no oracle):
+    A words [m/4][kb][144] (MXINT8 of N(0,1) rows), W words [n/8][kb][144]
+    per plane.  MXFP4: random E2M1 codes, E8M0 exponents -10..-2.  W8: int8
+    weights U{-127..127} encoded MXINT8 (lossless, scale byte 133) and split
+    into the hi (signed) and lo (unsigned) nibble planes."""
     quads = (m + 3) // 4
     a = np.zeros((quads, kb, 144), np.uint8)
     x = rng.standard_normal((quads * 4, kb, 32)).astype(np.float32)
@@ -49,10 +62,20 @@ def make_inputs(rng, m, n, kb):
     q = np.clip(np.rint(x * np.exp2(6 - e)[..., None]), -128, 127).astype(np.int8)
     a[:, :, :128] = q.reshape(quads, 4, kb, 32).transpose(0, 2, 1, 3).reshape(quads, kb, 128).view(np.uint8)
     a[:, :, 128:132] = (e + 127).reshape(quads, 4, kb).transpose(0, 2, 1).astype(np.uint8)
-    w = np.zeros((n // 8, kb, 144), np.uint8)
-    w[:, :, :128] = rng.integers(0, 256, (n // 8, kb, 128), dtype=np.uint8)
-    w[:, :, 128:136] = (127 + rng.integers(-10, -1, (n // 8, kb, 8))).astype(np.uint8)
-    return a.reshape(-1, 144), w.reshape(-1, 144)
+    if not w8:
+        w = np.zeros((n // 8, kb, 144), np.uint8)
+        w[:, :, :128] = rng.integers(0, 256, (n // 8, kb, 128), dtype=np.uint8)
+        w[:, :, 128:136] = (127 + rng.integers(-10, -1, (n // 8, kb, 8))).astype(np.uint8)
+        return a.reshape(-1, 144), [w.reshape(-1, 144)]
+    qw = rng.integers(-127, 128, (n, kb * 32)).astype(np.int8).view(np.uint8)
+    planes = []
+    for nib in (qw >> 4, qw & 15):  # hi plane code, lo plane code
+        w = np.zeros((n // 8, kb, 144), np.uint8)
+        v = nib.reshape(n // 8, 8, kb, 16, 2)
+        w[:, :, :128] = (v[..., 0] | (v[..., 1] << 4)).transpose(0, 2, 1, 3).reshape(n // 8, kb, 128)
+        w[:, :, 128:136] = 133
+        planes.append(w.reshape(-1, 144))
+    return a.reshape(-1, 144), planes
 
 
 def cpu_baseline(m, n, kb, budget_s=15.0):
@@ -65,13 +88,104 @@ def cpu_baseline(m, n, kb, budget_s=15.0):
     t_end = time.perf_counter() + budget_s
     while True:
         t0 = time.perf_counter()
-        oracle.linear(m, n, kb, a, [w], [0])
+        oracle.linear(m, n, kb, a, w, [0])
         times.append(time.perf_counter() - t0)
         if time.perf_counter() + times[-1] > t_end or len(times) >= 5:
             break
     t = float(np.median(times))
-    return {"value": 2.0 * m * n * kb * 32 / t / 1e12, "unit": "TOPS", "cores": 1, "kind": "port",
-            "sample": f"{len(times)} run(s) of one {m}x{kb * 32}x{n} MXFP4 layer, median {t:.3f} s"}
+    return {"value": round(2.0 * m * n * kb * 32 / t / 1e12, 6), "unit": "TOPS", "cores": 1,
+            "kind": "port",
+            "sample": f"{len(times)} run(s) of one {m}x{kb * 32}x{n} MXFP4 layer (exact fold), "
+                      f"median {t:.3f} s"}
+
+
+def counted_traffic(kernel_tag):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE, calibrated against
+    a device copy of known size), or None when no summary covers it."""
+    path = os.path.join(PROFILES, "hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        m = re.match(r"\|\s*" + re.escape(kernel_tag) + r"\s*\|.*\|\s*([0-9]+)\s*\|\s*$", line)
+        if m:
+            return int(m.group(1))
+    return None
+
+
+class Workload:
+    """L layers of one shape on the device, with their descriptors."""
+
+    def __init__(self, hb, torch, m, n, kb, w8, layers, mode, epilogue=False, seed=1):
+        dev = "cuda:0"
+        self.m, self.n, self.kb, self.w8, self.layers = m, n, kb, w8, layers
+        self.n_vectors = 2 if epilogue else 0
+        a1, w1 = make_inputs(np.random.default_rng(seed), m, n, kb, w8)
+        L = layers
+        self.a = torch.empty((L,) + a1.shape, dtype=torch.uint8, device=dev)
+        self.w = [torch.empty((L,) + p.shape, dtype=torch.uint8, device=dev) for p in w1]
+        for i in range(min(L, 4)):  # four layers from the host generator
+            ai, wi = make_inputs(np.random.default_rng(seed * 100 + i), m, n, kb, w8)
+            self.a[i].copy_(torch.from_numpy(ai))
+            for p in range(len(wi)):
+                self.w[p][i].copy_(torch.from_numpy(wi[p]))
+        if L > 4:  # the rest: same scales, fresh codes drawn on the device
+            g = torch.Generator(device=dev).manual_seed(seed + 5)
+            self.a[4:] = self.a[:1]
+            for p in range(len(self.w)):
+                self.w[p][4:] = self.w[p][:1]
+                self.w[p][4:, :, :128] = torch.randint(0, 256, self.w[p][4:, :, :128].shape,
+                                                       generator=g, device=dev, dtype=torch.uint8)
+            self.a[4:, :, :128] = torch.randint(0, 256, self.a[4:, :, :128].shape, generator=g,
+                                                device=dev, dtype=torch.uint8)
+        self.c = torch.zeros((L, m, n), dtype=torch.float32, device=dev)
+        ops_t = []
+        if epilogue:  # per-channel scale ~ U(0.001, 0.02), bias ~ N(0, 0.1)
+            self.scale = torch.rand((L, n), device=dev) * 0.019 + 0.001
+            self.bias = torch.randn((L, n), device=dev) * 0.1
+            ops_t = [(hb.EP_MULP, self.scale), (hb.EP_ADDP, self.bias)]
+        modes = [1, 2] if w8 else [0]
+        self.descs = [hb.linear_desc(m, n, kb, self.a[i], [p[i] for p in self.w], modes,
+                                     self.c[i], ops=[(k, t[i]) for k, t in ops_t], mode=mode)
+                      for i in range(L)]
+        torch.cuda.synchronize()
+
+    def ops(self):
+        return 2.0 * self.m * self.n * self.kb * 32 * self.layers
+
+    def bytes(self):
+        return layer_bytes(self.m, self.n, self.kb, 8 if self.w8 else 4, self.n_vectors) * self.layers
+
+
+def time_steps(hb, torch, ctx, stream, work, steps, warmup):
+    """Average ms per step over `steps` back-to-back batched launches, timed
+    with events on the stream the kernels run on."""
+    for _ in range(warmup):
+        hb.linear_batched(work.descs, ctx)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        hb.linear_batched(work.descs, ctx)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def summarize(work, ms, mfma_class, kernel_tag=None):
+    ops, nbytes = work.ops(), work.bytes()
+    tops = ops / (ms * 1e-3) / 1e12
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    peak = MFMA_PEAK[mfma_class]
+    hbm_bound = ops / nbytes * HBM_PEAK_GBS / 1e3 < peak
+    if hbm_bound:
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(tops, 1), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(tops / peak, 4)}
+    roof["traffic"] = counted_traffic(kernel_tag) if kernel_tag else None
+    return tops, roof
 
 
 def main():
@@ -79,10 +193,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--mode", choices=["exact", "fast"], default="exact")
+    ap.add_argument("--mode", choices=["exact", "fast"], default="fast")
     ap.add_argument("--layers", type=int, default=256)
     ap.add_argument("--m", type=int, default=128)
+    ap.add_argument("--quick", action="store_true", help="headline only, no extra fields")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}); nothing in this build "
@@ -92,63 +208,31 @@ def main():
     import torch
     import hotarubi_amd as hb
 
-    m, n, kb, L = args.m, 960, 80, args.layers
-    rng = np.random.default_rng(1)
-    a1, w1 = make_inputs(rng, m, n, kb)
-    dev = "cuda:0"
-    # distinct layers: random weights/activations per layer, built on device
-    a_all = torch.empty((L,) + a1.shape, dtype=torch.uint8, device=dev)
-    w_all = torch.empty((L,) + w1.shape, dtype=torch.uint8, device=dev)
-    for i in range(L):
-        ai, wi = make_inputs(np.random.default_rng(100 + i), m, n, kb) if i < 4 else (a1, w1)
-        a_all[i].copy_(torch.from_numpy(ai))
-        w_all[i].copy_(torch.from_numpy(wi))
-    if L > 4:  # decorrelate the rest cheaply on device: permute words, keep scales sane
-        g = torch.Generator(device=dev).manual_seed(5)
-        for i in range(4, L):
-            w_all[i, :, :128] = torch.randint(0, 256, w_all[i, :, :128].shape, generator=g,
-                                              device=dev, dtype=torch.uint8)
-            a_all[i, :, :128] = torch.randint(0, 256, a_all[i, :, :128].shape, generator=g,
-                                              device=dev, dtype=torch.uint8)
-    c_all = torch.zeros((L, m, n), dtype=torch.float32, device=dev)
-    torch.cuda.synchronize()
+    if args.copy_probe:
+        x = torch.ones(args.copy_probe << 20, dtype=torch.uint8, device="cuda:0")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        del x, y
 
     ctx = hb.Context(0)
     stream = torch.cuda.current_stream()
     ctx.set_stream(stream.cuda_stream)
-    mode = hb.FAST if args.mode == "fast" else hb.EXACT
-    descs = [hb.linear_desc(m, n, kb, a_all[i], [w_all[i]], [0], c_all[i], mode=mode) for i in range(L)]
+    fast = args.mode == "fast"
+    mode = hb.FAST if fast else hb.EXACT
+    n, kb = 960, 80
 
-    def step():
-        hb.linear_batched(descs, ctx)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for _ in range(args.steps):
-        step()
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / args.steps
-
-    ops = 2.0 * m * n * kb * 32 * L
-    tops = ops / (ms * 1e-3) / 1e12
-    bytes_step = layer_bytes(m, n, kb) * L
-    gbs = bytes_step / (ms * 1e-3) / 1e9
-    ai = ops / bytes_step
-    peak_mfma = MFMA_PEAK_TOPS["int8"]
-    bound = "hbm" if ai * HBM_PEAK_GBS / 1e3 < peak_mfma else "mfma"
-    if bound == "hbm":
-        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
-    else:
-        roof = {"bound": "mfma", "achieved": round(tops, 1), "peak": peak_mfma, "unit": "TFLOP/s",
-                "frac": round(tops / peak_mfma, 4), "traffic": None}
+    work = Workload(hb, torch, args.m, n, kb, False, args.layers, mode)
+    ms = time_steps(hb, torch, ctx, stream, work, args.steps, args.warmup)
+    tag = ("FastFp4Kernel<128>" if args.m > 64 else "FastFp4Kernel<64>") if fast else \
+        "GemmTileKernel<linear,128,128>"
+    tops, roof = summarize(work, ms, "fp6_fp4" if fast else "bf16",
+                           tag if (args.m == 128 and args.layers == 256) else None)
+    del work
 
     out = {
-        "metric": "quantized GEMM TOPS & % MFMA/HBM roofline (W8, MXFP4); SmolVLA step ms",
+        "metric": METRIC,
         "value": round(tops, 3),
         "unit": "TOPS",
         "n_gpus": 1,
@@ -159,13 +243,49 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "mxint8 x mxfp4 -> fp32",
-        "data": "synthetic (seeded MXINT8 activations, random E2M1 codes, E8M0 exponents -10..-2)",
-        "config": {"workload": f"MXFP4 linear M={m} K={kb * 32} N={n}, {L} distinct layers per step",
-                   "mode": args.mode, "layers_per_step": L, "m": m, "k": kb * 32, "n": n},
+        "data": "synthetic (seeded MXINT8 activations of N(0,1), random E2M1 codes, "
+                "E8M0 exponents -10..-2)",
+        "config": {"workload": f"MXFP4 linear M={args.m} K={kb * 32} N={n}, "
+                               f"{args.layers} distinct layers per step",
+                   "mode": args.mode, "layers_per_step": args.layers, "m": args.m,
+                   "k": kb * 32, "n": n},
         "roofline": roof,
     }
+
+    if not args.quick:
+        extra_steps, extra_warm = 5, 1
+        # the same workload in the other mode
+        other = hb.EXACT if fast else hb.FAST
+        w2 = Workload(hb, torch, args.m, n, kb, False, args.layers, other)
+        ms2 = time_steps(hb, torch, ctx, stream, w2, extra_steps, extra_warm)
+        t2, r2 = summarize(w2, ms2, "bf16" if fast else "fp6_fp4")
+        out["exact" if fast else "fast"] = {"value": round(t2, 3), "unit": "TOPS",
+                                            "ms_per_step": round(ms2, 4), "roofline": r2}
+        del w2
+        # M sweep (fast MXFP4), enough layers per step to exceed the caches
+        sweep = {}
+        for m, L in ((1, 256), (16, 256), (1024, 64)):
+            ws = Workload(hb, torch, m, n, kb, False, L, hb.FAST, seed=3)
+            mss = time_steps(hb, torch, ctx, stream, ws, extra_steps, extra_warm)
+            ts, rs = summarize(ws, mss, "fp6_fp4")
+            sweep[f"M={m}"] = {"value": round(ts, 3), "unit": "TOPS", "layers": L,
+                               "ms_per_step": round(mss, 4), "roofline": rs}
+            del ws
+        sweep["M=128"] = {"value": out["value"], "unit": "TOPS", "layers": args.layers,
+                          "ms_per_step": out["ms_per_step"], "roofline": roof}
+        out["mxfp4_fast_m_sweep"] = sweep
+        # W8 layer with per-channel scale and bias (exact)
+        L8 = 128
+        w8 = Workload(hb, torch, 64, 2560, 30, True, L8, hb.EXACT, epilogue=True, seed=4)
+        ms8 = time_steps(hb, torch, ctx, stream, w8, extra_steps, extra_warm)
+        t8, r8 = summarize(w8, ms8, "bf16")
+        out["w8_exact"] = {"workload": f"W8 linear M=64 K=960 N=2560 + MULP + ADDP, {L8} layers "
+                                       "per step", "value": round(t8, 3), "unit": "TOPS",
+                           "ms_per_step": round(ms8, 4), "roofline": r8}
+        del w8
+
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(m, n, kb)
+        out["cpu_baseline"] = cpu_baseline(args.m, n, kb)
     print(json.dumps(out), flush=True)
     ctx.close()
 

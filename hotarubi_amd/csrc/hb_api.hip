@@ -592,23 +592,36 @@ int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count
   hb::GemmArgs g;
   if (int rc = LinearArgs(&d[0], &g)) return rc;
   if (count > 1) {
-    if (d[0].n_ops != 0 || d[0].onto)
-      return Fail(HB_EUNSUPPORTED, "batched layers take no epilogue ops and no onto");
-    g.a_batch = Diff(d[0].a, d[1].a);
-    g.w_batch = Diff(d[0].w[0], d[1].w[0]);
-    g.c_batch = Diff(d[0].c, d[1].c) / 4;
-    g.q_batch = d[0].q_out ? Diff(d[0].q_out, d[1].q_out) : 0;
+    const hb_linear_desc& d0 = d[0];
+    g.a_batch = Diff(d0.a, d[1].a);
+    g.w_batch = Diff(d0.w[0], d[1].w[0]);
+    g.c_batch = Diff(d0.c, d[1].c) / 4;
+    g.q_batch = d0.q_out ? Diff(d0.q_out, d[1].q_out) : 0;
+    for (uint32_t o = 0; o < d0.n_ops; ++o) {
+      g.op_vec_batch[o] = d0.ops[o].vec ? Diff(d0.ops[o].vec, d[1].ops[o].vec) / 4 : 0;
+      g.op_x2_batch[o] = d0.ops[o].x2 ? Diff(d0.ops[o].x2, d[1].ops[o].x2) / 4 : 0;
+    }
     for (uint32_t i = 1; i < count; ++i) {
       const hb_linear_desc& x = d[i];
-      const bool same = x.m == d[0].m && x.n == d[0].n && x.kb_total == d[0].kb_total &&
-                        x.n_planes == d[0].n_planes && x.flags == d[0].flags &&
-                        x.n_ops == 0 && !x.onto && (x.q_out != nullptr) == (d[0].q_out != nullptr) &&
-                        Diff(d[0].a, x.a) == i * g.a_batch &&
-                        Diff(d[0].w[0], x.w[0]) == i * g.w_batch &&
-                        (x.n_planes < 2 || Diff(d[0].w[1], x.w[1]) == i * g.w_batch) &&
-                        Diff(d[0].c, x.c) == i * g.c_batch * 4 &&
-                        (!x.q_out || Diff(d[0].q_out, x.q_out) == i * g.q_batch);
-      if (!same) return Fail(HB_EINVAL, "layer %u differs in shape or stride", i);
+      bool same = x.m == d0.m && x.n == d0.n && x.kb_total == d0.kb_total &&
+                  x.n_planes == d0.n_planes && x.flags == d0.flags && x.onto == d0.onto &&
+                  x.n_pieces == d0.n_pieces && x.n_ops == d0.n_ops && x.tbuf == d0.tbuf &&
+                  (x.q_out != nullptr) == (d0.q_out != nullptr) &&
+                  Diff(d0.a, x.a) == i * g.a_batch && Diff(d0.w[0], x.w[0]) == i * g.w_batch &&
+                  (x.n_planes < 2 || Diff(d0.w[1], x.w[1]) == i * g.w_batch) &&
+                  Diff(d0.c, x.c) == i * g.c_batch * 4 &&
+                  (!x.q_out || Diff(d0.q_out, x.q_out) == i * g.q_batch);
+      for (uint32_t l = 0; same && l < d0.n_planes; ++l) same = x.modes[l] == d0.modes[l];
+      for (uint32_t p = 0; same && p < d0.n_pieces; ++p)
+        same = x.pieces[p].kb_offset == d0.pieces[p].kb_offset && x.pieces[p].kb == d0.pieces[p].kb;
+      for (uint32_t o = 0; same && o < d0.n_ops; ++o) {
+        const hb_ep_op &a = d0.ops[o], &b = x.ops[o];
+        same = a.op == b.op && a.imm == b.imm && (a.vec != nullptr) == (b.vec != nullptr) &&
+               (a.x2 != nullptr) == (b.x2 != nullptr) &&
+               (!a.vec || Diff(a.vec, b.vec) == i * g.op_vec_batch[o] * 4) &&
+               (!a.x2 || Diff(a.x2, b.x2) == i * g.op_x2_batch[o] * 4);
+      }
+      if (!same) return Fail(HB_EINVAL, "layer %u differs in shape, schedule, ops or stride", i);
     }
   }
   hipError_t err = hb::LaunchLinear(g, count, d[0].flags == HB_LINEAR_FAST, ctx->stream);

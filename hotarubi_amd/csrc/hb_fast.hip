@@ -182,21 +182,27 @@ __device__ __forceinline__ uint32_t SlowLinear(const GemmArgs& g, const uint8_t*
   return acc;
 }
 
-__device__ __forceinline__ uint32_t FastEp(const GemmArgs& g, uint32_t o, uint32_t y, uint32_t row,
-                                           uint32_t col, bool row_ok) {
+// z: layer of a batched launch (op vectors advance by their per-layer stride).
+__device__ __forceinline__ uint32_t FastEp(const GemmArgs& g, uint32_t o, uint32_t z, uint32_t y,
+                                           uint32_t row, uint32_t col, bool row_ok) {
   switch (g.op_kind[o]) {
-    case kEpAddP: return LaneAddMul(y, g.op_vec[o][col], kOne, 0u);
-    case kEpMulP: return LaneAddMul(y, 0u, g.op_vec[o][col], 0u);
+    case kEpAddP: return LaneAddMul(y, g.op_vec[o][z * g.op_vec_batch[o] + col], kOne, 0u);
+    case kEpMulP: return LaneAddMul(y, 0u, g.op_vec[o][z * g.op_vec_batch[o] + col], 0u);
     case kEpScale: return LaneAddMul(y, 0u, g.op_imm[o], 0u);
     case kEpCopy: return LaneAddMul(y, 0u, kOne, 0u);
     case kEpRelu: {
       const uint32_t prod = FMul(FAdd(y, 0u), kOne);
       return FAdd(MaxGreaterEqual(prod, 0u) ? prod : 0u, 0u);
     }
-    case kEpAdd: return LaneAddMul(y, row_ok ? g.op_x2[o][(size_t)row * g.n + col] : 0u, kOne, 0u);
+    case kEpAdd: {
+      const uint32_t x2 = row_ok ? g.op_x2[o][z * g.op_x2_batch[o] + (size_t)row * g.n + col] : 0u;
+      return LaneAddMul(y, x2, kOne, 0u);
+    }
     case kEpAct: return ActGate(y, g.tbuf);
-    case kEpActMul:
-      return LaneAddMul(ActGate(y, g.tbuf), 0u, row_ok ? g.op_x2[o][(size_t)row * g.n + col] : 0u, 0u);
+    case kEpActMul: {
+      const uint32_t x2 = row_ok ? g.op_x2[o][z * g.op_x2_batch[o] + (size_t)row * g.n + col] : 0u;
+      return LaneAddMul(ActGate(y, g.tbuf), 0u, x2, 0u);
+    }
     default: return y;
   }
 }
@@ -337,7 +343,8 @@ __global__ __launch_bounds__(kBM * 4) void FastFp4Kernel(GemmArgs g) {
       for (uint32_t r = 0; r < 16; ++r) {
         const uint32_t row = row_l + 8 * (r / 4) + (r & 3), col = col_l + j * 32;
         if ((row >> 2) < g.quads && col < g.n)
-          acc[j][r] = __uint_as_float(FastEp(g, o, __float_as_uint(acc[j][r]), row, col, row < g.m));
+          acc[j][r] =
+              __uint_as_float(FastEp(g, o, z, __float_as_uint(acc[j][r]), row, col, row < g.m));
       }
   }
 #pragma unroll

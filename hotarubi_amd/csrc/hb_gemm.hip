@@ -310,11 +310,12 @@ __device__ __forceinline__ uint32_t SlowOutput(const GemmArgs& g, const uint8_t*
 }
 
 // One epilogue op on one element (lane formulas of the VEC library entries).
-__device__ __forceinline__ uint32_t EpOp(const GemmArgs& g, uint32_t o, uint32_t y, uint32_t row,
-                                         uint32_t col, bool row_ok) {
+// z: layer of a batched launch (op vectors advance by their per-layer stride).
+__device__ __forceinline__ uint32_t EpOp(const GemmArgs& g, uint32_t o, uint32_t z, uint32_t y,
+                                         uint32_t row, uint32_t col, bool row_ok) {
   switch (g.op_kind[o]) {
-    case kEpAddP: return LaneAddMul(y, g.op_vec[o][col], kOne, 0u);
-    case kEpMulP: return LaneAddMul(y, 0u, g.op_vec[o][col], 0u);
+    case kEpAddP: return LaneAddMul(y, g.op_vec[o][z * g.op_vec_batch[o] + col], kOne, 0u);
+    case kEpMulP: return LaneAddMul(y, 0u, g.op_vec[o][z * g.op_vec_batch[o] + col], 0u);
     case kEpScale: return LaneAddMul(y, 0u, g.op_imm[o], 0u);
     case kEpCopy: return LaneAddMul(y, 0u, kOne, 0u);
     case kEpRelu: {
@@ -322,12 +323,12 @@ __device__ __forceinline__ uint32_t EpOp(const GemmArgs& g, uint32_t o, uint32_t
       return FAdd(MaxGreaterEqual(prod, 0u) ? prod : 0u, 0u);
     }
     case kEpAdd: {
-      const uint32_t x2 = row_ok ? g.op_x2[o][(size_t)row * g.n + col] : 0u;
+      const uint32_t x2 = row_ok ? g.op_x2[o][z * g.op_x2_batch[o] + (size_t)row * g.n + col] : 0u;
       return LaneAddMul(y, x2, kOne, 0u);
     }
     case kEpAct: return ActGate(y, g.tbuf);
     case kEpActMul: {
-      const uint32_t x2 = row_ok ? g.op_x2[o][(size_t)row * g.n + col] : 0u;
+      const uint32_t x2 = row_ok ? g.op_x2[o][z * g.op_x2_batch[o] + (size_t)row * g.n + col] : 0u;
       return LaneAddMul(ActGate(y, g.tbuf), 0u, x2, 0u);
     }
     default: return y;
@@ -355,8 +356,8 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
   uint32_t* c = g.c;
   uint8_t* q_out = g.q_out;
   const TileId tile = LogicalTile(g.gx, g.gy, g.gz);
+  const uint32_t z = kLinear ? tile.z : 0u;  // layer of a batched linear launch
   if (kLinear) {
-    const uint32_t z = tile.z;
     a += z * g.a_batch;
     w0 += z * g.w_batch;
     w1 += z * g.w_batch;
@@ -518,7 +519,8 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
         for (uint32_t e = 0; e < 16; ++e) {
           const uint32_t row = row_l + i * 16 + (e & 3), col = col_l + (e >> 2) * 16;
           if ((row >> 2) < g.quads && (col >> 3) < g.groups)
-            res[i][e] = __uint_as_float(EpOp(g, o, __float_as_uint(res[i][e]), row, col, row < g.m));
+            res[i][e] =
+                __uint_as_float(EpOp(g, o, z, __float_as_uint(res[i][e]), row, col, row < g.m));
         }
     }
   }

@@ -49,6 +49,7 @@ struct GemmArgs {
   uint8_t* q_out;     // MXINT8 DDR words [quads][n/32] or null
   // batched linear: per-layer strides (bytes / elements), 0 for one layer
   uint64_t a_batch, w_batch, c_batch, q_batch;
+  uint64_t op_vec_batch[kMaxOps], op_x2_batch[kMaxOps];  // elements
   // tile grid (x: column tiles, y: row tiles, z: layers), launched 1-D
   uint32_t gx, gy, gz;
 };

@@ -220,8 +220,11 @@ typedef struct hb_linear_desc {
 
 int hb_linear(hb_ctx* ctx, const hb_linear_desc* desc);
 int hb_linear_async(hb_ctx* ctx, const hb_linear_desc* desc);
-/* `count` independent layers of identical shape, flags and op kinds in one
- * launch (e.g. the same projection of many layers or requests). */
+/* `count` independent layers in one launch (e.g. the same projection of
+ * many layers or requests).  Every descriptor must match descs[0] in shape,
+ * planes, modes, pieces, onto, flags, TBUF and op kinds/immediates, and each
+ * pointer (A, W planes, C, q_out, op vectors) must advance by the same byte
+ * stride from one layer to the next; otherwise HB_EINVAL. */
 int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* descs,
                             uint32_t count);
 

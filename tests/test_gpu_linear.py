@@ -235,6 +235,75 @@ def test_batched_layers(gpu):
         assert_bits(got[i], want)
 
 
+@pytest.mark.parametrize("w8,mode,quantize", [(True, hb.EXACT, False), (False, hb.EXACT, True),
+                                              (False, hb.FAST, False)])
+def test_batched_layers_with_epilogue(gpu, w8, mode, quantize):
+    """Per-layer MULP scale and ADDP bias vectors at a uniform stride, as in
+    the W8 workload (per-channel scale and bias), batched into one launch."""
+    rng = np.random.default_rng(61 + w8)
+    layers, m, n, k = 4, 64, 256, 320
+    data = [make_layer(rng, m, n, k, w8) for _ in range(layers)]
+    kb, modes = data[0][0], data[0][3]
+    scale = np.stack([helpers.random_fp32_words(rng, (n,), 117, 122) for _ in range(layers)])
+    bias = np.stack([helpers.random_fp32_words(rng, (n,), 118, 124) for _ in range(layers)])
+    a_all = dev(np.stack([d[1] for d in data]))
+    w_all = [dev(np.stack([d[2][p] for d in data])) for p in range(len(modes))]
+    s_all, b_all = dev(scale.view(np.float32)), dev(bias.view(np.float32))
+    c_all = torch.zeros((layers, m, n), dtype=torch.float32, device=DEV)
+    nb = n // 32
+    q_all = (torch.zeros((layers, m // 4 * nb, 144), dtype=torch.uint8, device=DEV)
+             if quantize else None)
+    descs = [hb.linear_desc(m, n, kb, a_all[i], [w[i] for w in w_all], modes, c_all[i],
+                            ops=[(hb.EP_MULP, s_all[i]), (hb.EP_ADDP, b_all[i])],
+                            q_out=q_all[i] if quantize else None, mode=mode)
+             for i in range(layers)]
+    torch.cuda.synchronize()
+    say("batched with epilogue", dict(layers=layers, w8=w8, mode=mode, quantize=quantize))
+    hb.linear_batched(descs, gpu)
+    got = host(c_all).view(np.uint32)
+    gq = host(q_all) if quantize else None
+    for i, d in enumerate(data):
+        ops = [(hb.EP_MULP, scale[i]), (hb.EP_ADDP, bias[i])]
+        want, wq = oracle_linear(m, n, kb, d[1], d[2], d[3], ops, quantize=quantize)
+        if mode == hb.EXACT:
+            assert_bits(got[i], want)
+            if quantize:
+                assert np.array_equal(gq[i], wq)
+        else:
+            g = got[i].view(np.float32).astype(np.float64)
+            w = want.view(np.float32).astype(np.float64)
+            row_scale = np.abs(w).max(axis=1, keepdims=True)
+            assert (np.abs(g - w) <= 1e-5 * row_scale).all()
+
+
+def test_batched_rejects_mismatched_layers(gpu):
+    rng = np.random.default_rng(62)
+    m, n, k = 32, 64, 64
+    kb, a, planes, modes = make_layer(rng, m, n, k, False)
+    a_all = dev(np.stack([a] * 3))
+    w_all = dev(np.stack([planes[0]] * 3))
+    c_all = torch.zeros((3, m, n), dtype=torch.float32, device=DEV)
+    vec = torch.zeros((3, n), dtype=torch.float32, device=DEV)
+    good = [hb.linear_desc(m, n, kb, a_all[i], [w_all[i]], modes, c_all[i],
+                           ops=[(hb.EP_MULP, vec[i])]) for i in range(3)]
+    cases = {
+        "op vector stride": [good[0], good[1],
+                             hb.linear_desc(m, n, kb, a_all[2], [w_all[2]], modes, c_all[2],
+                                            ops=[(hb.EP_MULP, vec[0])])],
+        "op kind": [good[0], good[1],
+                    hb.linear_desc(m, n, kb, a_all[2], [w_all[2]], modes, c_all[2],
+                                   ops=[(hb.EP_ADDP, vec[2])])],
+        "pieces": [good[0], good[1],
+                   hb.linear_desc(m, n, kb, a_all[2], [w_all[2]], modes, c_all[2],
+                                  pieces=[(1, 1)], ops=[(hb.EP_MULP, vec[2])])],
+    }
+    for name, descs in cases.items():
+        say("batched mismatch", name)
+        with pytest.raises(hb.HbError):
+            hb.linear_batched(descs, gpu)
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 32), (4, 960), (7, 100), (64, 2560)])
 def test_encode_mxint8(gpu, rows, cols):
     rng = np.random.default_rng(rows * cols)

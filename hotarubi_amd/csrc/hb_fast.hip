@@ -38,30 +38,46 @@ constexpr int kBN = 256;  // 8 MFMA column tiles of 32
 constexpr int kRing = HB_FAST_RING;  // register sets (prefetch distance kRing - 1 steps)
 constexpr uint32_t kSafeLo = 70, kSafeHi = 179;
 
-// LDS layout of one step (two K blocks), kMT = kBM / 32 row tiles:
-//   A planes: [plane 2][m-tile][lane 64][6 dwords]  (32 E2M3 codes per lane)
-//   A scales: [plane 2][m-tile][lane 64] bytes      (E8M0 of the lane's block)
-//   W:        [n-tile 8][lane 64][4 dwords]         (32 E2M1 codes per lane)
-//   W scales: [n-tile 8][lane 64] bytes
+// LDS layout of one step (two K blocks), kMT = kBM / 32 row tiles.  Every
+// array is lane-major, so a wave's store or load of one operand touches 64
+// consecutive slots (no bank conflicts):
+//   A planes: [plane 2][m-tile][part 3][lane 64] 8-byte slots (32 E2M3 codes)
+//   A scales: [plane 2][m-tile][lane 64] dwords (E8M0 of the lane's block)
+//   W:        [n-tile 8][lane 64] 16-byte slots (32 E2M1 codes per lane)
+//   W scales: [n-tile 8][lane 64] dwords
+// Lane l of an m-tile holds row l % 32 of the tile and block l / 32 of the
+// step; lane l of an n-tile holds column l % 32 and block l / 32.
 template <int kMT>
 struct StepLds {
-  uint32_t a[2][kMT][64][6];
-  uint32_t w[8][64][4];
-  uint8_t sa[2][kMT][64];
-  uint8_t sw[8][64];
+  uint2 a[2][kMT][3][64];
+  uint4 w[8][64];
+  uint32_t sa[2][kMT][64];
+  uint32_t sw[8][64];
 };
 
-// One step's raw bytes per thread (kBM * 4 threads):
-//   A: row r = tid >> 2, block half h = (tid >> 1) & 1, plane p = tid & 1;
-//      all 32 bytes of the row's block (both plane threads load them).
-//   W: column tid % 256, block half tid / 256 (128-row tile) or both halves
-//      (64-row tile): 16 bytes per block.
+// Work split of the raw bytes of one step (kBM * 4 threads, kBM / 16 waves):
+//   A: wave v converts plane v % 2 (0: hi, 1: lo) of m-tile v / 2; its lane
+//      l takes row l % 32 of the tile, block l / 32 (32 bytes + scale byte).
+//   W: thread t takes column t % 256, block t / 256 (128-row tile) or both
+//      blocks (64-row tile): 16 bytes + scale byte per block.
+// Scale bytes travel as the aligned dword that holds them (bytes 128..131 of
+// an A word, 128..131 or 132..135 of a W word) and are extracted where they
+// are stored: a byte load's zero-extension would be placed at the load and
+// make the compiler wait for it there.
 template <int kWBlocks>
 struct Raw {
   uint32_t a[8];
   uint32_t w[kWBlocks][4];
   uint32_t sa, sw[kWBlocks];
   bool zero_a;  // the lane's block is past the end: its codes become 0
+};
+
+// Per-thread byte offsets within a layer's A and W arrays (fixed for the
+// whole K loop; a step adds the uniform offset of its block).  32 bits: one
+// layer's operands are far below 4 GiB.
+template <int kWBlocks>
+struct Offsets {
+  uint32_t a, a_scale, w, w_scale;
 };
 
 // The blocks of the fold, paired into steps: step s covers list entries 2s
@@ -82,21 +98,38 @@ __device__ __forceinline__ uint32_t BlockOf(const GemmArgs& g, uint32_t idx) {
   return base + idx;
 }
 
+template <int kBM, int kWBlocks>
+__device__ __forceinline__ Offsets<kWBlocks> ThreadOffsets(const GemmArgs& g, uint32_t q0,
+                                                           uint32_t g0) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t mt = (tid >> 6) >> 1;
+  const uint32_t r = mt * 32 + (lane & 31);
+  const uint32_t quad = min(q0 + (r >> 2), g.quads - 1), t = r & 3;
+  const uint32_t col = tid % 256;
+  const uint32_t grp = min(g0 + (col >> 3), g.groups - 1), cl = col & 7;
+  const uint32_t word_row = g.kb_total * kDdrWord;
+  Offsets<kWBlocks> o;
+  o.a = quad * word_row + t * 32;
+  o.a_scale = quad * word_row + 128;
+  o.w = grp * word_row + cl * 16;
+  o.w_scale = grp * word_row + 128 + (cl & 4);
+  return o;
+}
+
 // Steps at or past `steps` reload the last step's words (cache hits) with the
-// activations zeroed, so they add nothing.
+// activations zeroed, so they add nothing.  The block offsets are uniform;
+// each load is one instruction on (uniform base, 32-bit lane offset).
 template <int kBM, int kWBlocks, bool kMulti>
 __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, const uint8_t* w,
-                                        uint32_t q0, uint32_t g0, uint32_t live_step, uint32_t steps,
-                                        uint32_t nblocks, Raw<kWBlocks>& rw) {
-  const uint32_t tid = threadIdx.x;
+                                        const Offsets<kWBlocks>& o, uint32_t live_step,
+                                        uint32_t steps, uint32_t nblocks, Raw<kWBlocks>& rw) {
+  const uint32_t tid = threadIdx.x, h = (tid & 63) >> 5;
   const uint32_t step = min(live_step, steps - 1);
-  const uint32_t b0 = BlockOf<kMulti>(g, 2 * step);
-  const uint32_t b1 = BlockOf<kMulti>(g, min(2 * step + 1, nblocks - 1));
-  const uint32_t r = tid >> 2, h = (tid >> 1) & 1;
-  const uint32_t quad = min(q0 + (r >> 2), g.quads - 1), t = r & 3;
-  const uint8_t* aw = a + ((size_t)quad * g.kb_total + (h ? b1 : b0)) * kDdrWord;
-  const u32x4 v0 = *reinterpret_cast<const u32x4*>(aw + t * 32);
-  const u32x4 v1 = *reinterpret_cast<const u32x4*>(aw + t * 32 + 16);
+  const uint32_t ub0 = BlockOf<kMulti>(g, 2 * step) * kDdrWord;
+  const uint32_t ub1 = BlockOf<kMulti>(g, min(2 * step + 1, nblocks - 1)) * kDdrWord;
+  const uint32_t ua = h ? ub1 : ub0;
+  const u32x4 v0 = *reinterpret_cast<const u32x4*>(a + (o.a + ua));
+  const u32x4 v1 = *reinterpret_cast<const u32x4*>(a + (o.a + ua + 16));
   // Zeroed where the codes are stored, not here: a select on the loaded
   // registers would make the compiler wait for the load right away.
   rw.zero_a = live_step >= steps || (h && 2 * step + 1 >= nblocks);
@@ -105,17 +138,14 @@ __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, con
     rw.a[i] = v0[i];
     rw.a[4 + i] = v1[i];
   }
-  rw.sa = aw[128 + t];
-  const uint32_t col = tid % kBN;
-  const uint32_t grp = min(g0 + (col >> 3), g.groups - 1), cl = col & 7;
+  rw.sa = *reinterpret_cast<const uint32_t*>(a + (o.a_scale + ua));
 #pragma unroll
   for (int hb = 0; hb < kWBlocks; ++hb) {
-    const uint32_t half = kWBlocks == 2 ? hb : tid / kBN;
-    const uint8_t* wp = w + ((size_t)grp * g.kb_total + (half ? b1 : b0)) * kDdrWord;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(wp + cl * 16);
+    const uint32_t uw = (kWBlocks == 2 ? hb : tid / 256) ? ub1 : ub0;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(w + (o.w + uw));
 #pragma unroll
     for (int i = 0; i < 4; ++i) rw.w[hb][i] = v[i];
-    rw.sw[hb] = wp[128 + cl];
+    rw.sw[hb] = *reinterpret_cast<const uint32_t*>(w + (o.w_scale + uw));
   }
 }
 
@@ -123,12 +153,15 @@ __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, con
 // nibble n placed under the f16 exponent byte 0x60 is exactly 512 + n/2, so
 // one v_perm and one packed f16 subtract give n/2 (hi: (n^8)/2 - 4 = signed
 // hi/2); v_cvt_scalef32_pk32_fp6_f16 packs the 32 values (scale 1, exact).
+// `lo` is wave-uniform: the plane choice costs no per-lane selects.
 __device__ __forceinline__ u32x6 Plane32(const uint32_t* x, bool lo) {
-  const f16x2 bias = lo ? f16x2{(_Float16)512.0f, (_Float16)512.0f} : f16x2{(_Float16)516.0f, (_Float16)516.0f};
+  const uint32_t shift = lo ? 0u : 4u, flip = lo ? 0u : 0x08080808u;
+  const _Float16 b = lo ? (_Float16)512.0f : (_Float16)516.0f;
+  const f16x2 bias = {b, b};
   f16x32 v;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const uint32_t nb = lo ? (x[i] & 0x0F0F0F0Fu) : (((x[i] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u);
+    const uint32_t nb = ((x[i] >> shift) & 0x0F0F0F0Fu) ^ flip;
     const f16x2 d0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x60606060u, nb, 0x04010400u)) - bias;
     const f16x2 d1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x60606060u, nb, 0x04030402u)) - bias;
     v[4 * i] = d0[0];
@@ -141,23 +174,24 @@ __device__ __forceinline__ u32x6 Plane32(const uint32_t* x, bool lo) {
 
 template <int kBM, int kWBlocks>
 __device__ __forceinline__ bool StoreRaw(const Raw<kWBlocks>& rw, StepLds<kBM / 32>& s) {
-  const uint32_t tid = threadIdx.x;
-  const uint32_t r = tid >> 2, h = (tid >> 1) & 1, p = tid & 1;
-  const uint32_t mt = r >> 5, lane = (r & 31) + 32 * h;
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t p = wave & 1, mt = wave >> 1;
   const u32x6 codes = Plane32(rw.a, p != 0);
-  uint32_t* dst = s.a[p][mt][lane];
 #pragma unroll
-  for (int i = 0; i < 6; ++i) dst[i] = rw.zero_a ? 0u : codes[i];
-  s.sa[p][mt][lane] = (uint8_t)(rw.sa - (p ? 5u : 1u));
-  const uint32_t col = tid % kBN, nt = col >> 5, wl = col & 31;
-  bool bad = rw.sa < kSafeLo || rw.sa > kSafeHi;
+  for (int i = 0; i < 3; ++i)
+    s.a[p][mt][i][lane] = rw.zero_a ? uint2{0u, 0u} : uint2{codes[2 * i], codes[2 * i + 1]};
+  const uint32_t ea = __builtin_amdgcn_ubfe(rw.sa, 8 * (lane & 3), 8);  // row t = lane % 4
+  s.sa[p][mt][lane] = ea - (p ? 5u : 1u);
+  const uint32_t col = tid % 256, nt = col >> 5, wl = col & 31;
+  bool bad = ea - kSafeLo > kSafeHi - kSafeLo;
 #pragma unroll
   for (int hb = 0; hb < kWBlocks; ++hb) {
-    const uint32_t half = kWBlocks == 2 ? hb : tid / kBN;
-    *reinterpret_cast<u32x4*>(s.w[nt][wl + 32 * half]) =
-        u32x4{rw.w[hb][0], rw.w[hb][1], rw.w[hb][2], rw.w[hb][3]};
-    s.sw[nt][wl + 32 * half] = (uint8_t)rw.sw[hb];
-    bad |= rw.sw[hb] < kSafeLo || rw.sw[hb] > kSafeHi;
+    const uint32_t half = kWBlocks == 2 ? hb : tid / 256;
+    const uint32_t ew = __builtin_amdgcn_ubfe(rw.sw[hb], 8 * (col & 3), 8);  // column cl % 4
+    s.w[nt][wl + 32 * half] = uint4{rw.w[hb][0], rw.w[hb][1], rw.w[hb][2], rw.w[hb][3]};
+    s.sw[nt][wl + 32 * half] = ew;
+    bad |= ew - kSafeLo > kSafeHi - kSafeLo;
   }
   return bad;
 }
@@ -261,26 +295,27 @@ __global__ __launch_bounds__(kBM * 4) void FastFp4Kernel(GemmArgs g) {
     unsafe |= StoreRaw<kBM, kWBlocks>(rw, s);
     __syncthreads();
     i32x8 ahi, alo;
-    const uint32_t* ph = s.a[0][wm][lane];
-    const uint32_t* pl = s.a[1][wm][lane];
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      ahi[i] = (int)ph[i];
-      alo[i] = (int)pl[i];
+    for (int i = 0; i < 3; ++i) {
+      const uint2 h2 = s.a[0][wm][i][lane], l2 = s.a[1][wm][i][lane];
+      ahi[2 * i] = (int)h2.x;
+      ahi[2 * i + 1] = (int)h2.y;
+      alo[2 * i] = (int)l2.x;
+      alo[2 * i + 1] = (int)l2.y;
     }
     ahi[6] = ahi[7] = alo[6] = alo[7] = 0;
-    const int sa_hi = s.sa[0][wm][lane], sa_lo = s.sa[1][wm][lane];
+    const int sa_hi = (int)s.sa[0][wm][lane], sa_lo = (int)s.sa[1][wm][lane];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t nt = wn * 4 + j;
-      const u32x4 wv = *reinterpret_cast<const u32x4*>(s.w[nt][lane]);
+      const uint4 wv = s.w[nt][lane];
       i32x8 b;
-      b[0] = (int)wv[0];
-      b[1] = (int)wv[1];
-      b[2] = (int)wv[2];
-      b[3] = (int)wv[3];
+      b[0] = (int)wv.x;
+      b[1] = (int)wv.y;
+      b[2] = (int)wv.z;
+      b[3] = (int)wv.w;
       b[4] = b[5] = b[6] = b[7] = 0;
-      const int sw = s.sw[nt][lane];
+      const int sw = (int)s.sw[nt][lane];
       acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ahi, b, acc[j], 2, 4, 0, sa_hi, 0, sw);
       acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(alo, b, acc[j], 2, 4, 0, sa_lo, 0, sw);
     }
@@ -294,9 +329,10 @@ __global__ __launch_bounds__(kBM * 4) void FastFp4Kernel(GemmArgs g) {
   // Loads issue in program order (the fences stop the scheduler from
   // reordering ring sets), so the in-order load counter lets each compute
   // wait for exactly its own set.
+  const Offsets<kWBlocks> offs = ThreadOffsets<kBM, kWBlocks>(g, q0, g0);
   auto load = [&](Raw<kWBlocks>& rw, uint32_t step) {
     __builtin_amdgcn_sched_barrier(0);
-    LoadRaw<kBM, kWBlocks, kMulti>(g, a, w, q0, g0, step, steps, nblocks, rw);
+    LoadRaw<kBM, kWBlocks, kMulti>(g, a, w, offs, step, steps, nblocks, rw);
     __builtin_amdgcn_sched_barrier(0);
   };
   // Ring of kRing register sets: each compute consumes the set loaded

@@ -35,7 +35,7 @@ constexpr int kBN = 256;  // 8 MFMA column tiles of 32
 #ifndef HB_FAST_RING
 #define HB_FAST_RING 4
 #endif
-constexpr int kRing = HB_FAST_RING;  // register sets (prefetch distance kRing - 1 steps)
+constexpr int kRing = HB_FAST_RING;  // raw register sets (steps) per producer thread
 constexpr uint32_t kSafeLo = 70, kSafeHi = 179;
 
 // LDS layout of one step (two K blocks), kMT = kBM / 32 row tiles.  Every
@@ -55,29 +55,31 @@ struct StepLds {
   uint32_t sw[8][64];
 };
 
-// Work split of the raw bytes of one step (kBM * 4 threads, kBM / 16 waves):
+// Work split of the raw bytes of one step over the kP = kBM * 4 producer
+// threads (kBM / 16 waves; t below is the producer-local index):
 //   A: wave v converts plane v % 2 (0: hi, 1: lo) of m-tile v / 2; its lane
-//      l takes row l % 32 of the tile, block l / 32 (32 bytes + scale byte).
-//   W: thread t takes column t % 256, block t / 256 (128-row tile) or both
-//      blocks (64-row tile): 16 bytes + scale byte per block.
+//      l takes row l % 32 of the tile and block l / 32 (32 bytes + scale).
+//   W: the step's 256 columns x 2 blocks are 512 column-blocks of 16 bytes;
+//      thread t loads column-blocks t + kP*k, k < kWLoads = 512 / kP
+//      (column u % 256, block u / 256; the block is wave-uniform).
 // Scale bytes travel as the aligned dword that holds them (bytes 128..131 of
 // an A word, 128..131 or 132..135 of a W word) and are extracted where they
 // are stored: a byte load's zero-extension would be placed at the load and
 // make the compiler wait for it there.
-template <int kWBlocks>
+template <int kWLoads>
 struct Raw {
   uint32_t a[8];
-  uint32_t w[kWBlocks][4];
-  uint32_t sa, sw[kWBlocks];
-  bool zero_a;  // the lane's block is past the end: its codes become 0
+  uint32_t w[kWLoads][4];
+  uint32_t sa, sw[kWLoads];
+  uint32_t nib;  // 0x0F0F0F0F, or 0 where the lane's block is past the end
 };
 
 // Per-thread byte offsets within a layer's A and W arrays (fixed for the
 // whole K loop; a step adds the uniform offset of its block).  32 bits: one
 // layer's operands are far below 4 GiB.
-template <int kWBlocks>
+template <int kWLoads>
 struct Offsets {
-  uint32_t a, a_scale, w, w_scale;
+  uint32_t a, a_scale, w[kWLoads], w_scale[kWLoads];
 };
 
 // The blocks of the fold, paired into steps: step s covers list entries 2s
@@ -98,54 +100,59 @@ __device__ __forceinline__ uint32_t BlockOf(const GemmArgs& g, uint32_t idx) {
   return base + idx;
 }
 
-template <int kBM, int kWBlocks>
-__device__ __forceinline__ Offsets<kWBlocks> ThreadOffsets(const GemmArgs& g, uint32_t q0,
-                                                           uint32_t g0) {
-  const uint32_t tid = threadIdx.x, lane = tid & 63;
-  const uint32_t mt = (tid >> 6) >> 1;
+template <int kP, int kWLoads>
+__device__ __forceinline__ Offsets<kWLoads> ThreadOffsets(const GemmArgs& g, uint32_t q0,
+                                                          uint32_t g0, uint32_t t) {
+  const uint32_t lane = t & 63, mt = (t >> 6) >> 1;
   const uint32_t r = mt * 32 + (lane & 31);
-  const uint32_t quad = min(q0 + (r >> 2), g.quads - 1), t = r & 3;
-  const uint32_t col = tid % 256;
-  const uint32_t grp = min(g0 + (col >> 3), g.groups - 1), cl = col & 7;
+  const uint32_t quad = min(q0 + (r >> 2), g.quads - 1);
   const uint32_t word_row = g.kb_total * kDdrWord;
-  Offsets<kWBlocks> o;
-  o.a = quad * word_row + t * 32;
+  Offsets<kWLoads> o;
+  o.a = quad * word_row + (r & 3) * 32;
   o.a_scale = quad * word_row + 128;
-  o.w = grp * word_row + cl * 16;
-  o.w_scale = grp * word_row + 128 + (cl & 4);
+#pragma unroll
+  for (int k = 0; k < kWLoads; ++k) {
+    const uint32_t col = (t + kP * k) % 256;
+    const uint32_t grp = min(g0 + (col >> 3), g.groups - 1), cl = col & 7;
+    o.w[k] = grp * word_row + cl * 16;
+    o.w_scale[k] = grp * word_row + 128 + (cl & 4);
+  }
   return o;
 }
 
 // Steps at or past `steps` reload the last step's words (cache hits) with the
-// activations zeroed, so they add nothing.  The block offsets are uniform;
-// each load is one instruction on (uniform base, 32-bit lane offset).
-template <int kBM, int kWBlocks, bool kMulti>
+// activations masked to zero, so they add nothing.  Block offsets are uniform
+// and folded into the scalar base pointer; each load is one instruction on
+// (uniform base, 32-bit lane offset).
+template <int kP, int kWLoads, bool kMulti>
 __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, const uint8_t* w,
-                                        const Offsets<kWBlocks>& o, uint32_t live_step,
-                                        uint32_t steps, uint32_t nblocks, Raw<kWBlocks>& rw) {
-  const uint32_t tid = threadIdx.x, h = (tid & 63) >> 5;
+                                        const Offsets<kWLoads>& o, uint32_t t,
+                                        uint32_t live_step, uint32_t steps, uint32_t nblocks,
+                                        Raw<kWLoads>& rw) {
+  const uint32_t h = (t & 63) >> 5;
   const uint32_t step = min(live_step, steps - 1);
   const uint32_t ub0 = BlockOf<kMulti>(g, 2 * step) * kDdrWord;
   const uint32_t ub1 = BlockOf<kMulti>(g, min(2 * step + 1, nblocks - 1)) * kDdrWord;
-  const uint32_t ua = h ? ub1 : ub0;
-  const u32x4 v0 = *reinterpret_cast<const u32x4*>(a + (o.a + ua));
-  const u32x4 v1 = *reinterpret_cast<const u32x4*>(a + (o.a + ua + 16));
-  // Zeroed where the codes are stored, not here: a select on the loaded
-  // registers would make the compiler wait for the load right away.
-  rw.zero_a = live_step >= steps || (h && 2 * step + 1 >= nblocks);
+  const uint8_t* ab = a + ub0;                 // uniform
+  const uint32_t ao = o.a + (h ? ub1 - ub0 : 0u);  // ub1 - ub0 is uniform
+  const u32x4 v0 = *reinterpret_cast<const u32x4*>(ab + ao);
+  const u32x4 v1 = *reinterpret_cast<const u32x4*>(ab + ao + 16);
+  // Applied at conversion time, not here: a select on the loaded registers
+  // would make the compiler wait for the load right away.
+  rw.nib = (live_step >= steps || (h && 2 * step + 1 >= nblocks)) ? 0u : 0x0F0F0F0Fu;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     rw.a[i] = v0[i];
     rw.a[4 + i] = v1[i];
   }
-  rw.sa = *reinterpret_cast<const uint32_t*>(a + (o.a_scale + ua));
+  rw.sa = *reinterpret_cast<const uint32_t*>(ab + (o.a_scale + (h ? ub1 - ub0 : 0u)));
 #pragma unroll
-  for (int hb = 0; hb < kWBlocks; ++hb) {
-    const uint32_t uw = (kWBlocks == 2 ? hb : tid / 256) ? ub1 : ub0;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(w + (o.w + uw));
+  for (int k = 0; k < kWLoads; ++k) {
+    const uint8_t* wb = w + ((t + kP * k) / 256 ? ub1 : ub0);  // wave-uniform block
+    const u32x4 v = *reinterpret_cast<const u32x4*>(wb + o.w[k]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rw.w[hb][i] = v[i];
-    rw.sw[hb] = *reinterpret_cast<const uint32_t*>(w + (o.w_scale + uw));
+    for (int i = 0; i < 4; ++i) rw.w[k][i] = v[i];
+    rw.sw[k] = *reinterpret_cast<const uint32_t*>(wb + o.w_scale[k]);
   }
 }
 
@@ -153,15 +160,16 @@ __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, con
 // nibble n placed under the f16 exponent byte 0x60 is exactly 512 + n/2, so
 // one v_perm and one packed f16 subtract give n/2 (hi: (n^8)/2 - 4 = signed
 // hi/2); v_cvt_scalef32_pk32_fp6_f16 packs the 32 values (scale 1, exact).
-// `lo` is wave-uniform: the plane choice costs no per-lane selects.
-__device__ __forceinline__ u32x6 Plane32(const uint32_t* x, bool lo) {
+// `nib` = 0 masks the block to zero (lo: n = 0; hi: n ^ 8 = 8 -> 0).  `lo` is
+// wave-uniform.
+__device__ __forceinline__ u32x6 Plane32(const uint32_t* x, uint32_t nib, bool lo) {
   const uint32_t shift = lo ? 0u : 4u, flip = lo ? 0u : 0x08080808u;
   const _Float16 b = lo ? (_Float16)512.0f : (_Float16)516.0f;
   const f16x2 bias = {b, b};
   f16x32 v;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const uint32_t nb = ((x[i] >> shift) & 0x0F0F0F0Fu) ^ flip;
+    const uint32_t nb = ((x[i] >> shift) & nib) ^ flip;
     const f16x2 d0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x60606060u, nb, 0x04010400u)) - bias;
     const f16x2 d1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x60606060u, nb, 0x04030402u)) - bias;
     v[4 * i] = d0[0];
@@ -172,24 +180,23 @@ __device__ __forceinline__ u32x6 Plane32(const uint32_t* x, bool lo) {
   return __builtin_amdgcn_cvt_scalef32_pk32_fp6_f16(v, 1.0f);
 }
 
-template <int kBM, int kWBlocks>
-__device__ __forceinline__ bool StoreRaw(const Raw<kWBlocks>& rw, StepLds<kBM / 32>& s) {
-  const uint32_t tid = threadIdx.x, lane = tid & 63;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+template <int kMT, int kP, int kWLoads>
+__device__ __forceinline__ bool StoreRaw(const Raw<kWLoads>& rw, StepLds<kMT>& s, uint32_t t) {
+  const uint32_t lane = t & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const uint32_t p = wave & 1, mt = wave >> 1;
-  const u32x6 codes = Plane32(rw.a, p != 0);
+  const u32x6 codes = Plane32(rw.a, rw.nib, p != 0);
 #pragma unroll
-  for (int i = 0; i < 3; ++i)
-    s.a[p][mt][i][lane] = rw.zero_a ? uint2{0u, 0u} : uint2{codes[2 * i], codes[2 * i + 1]};
+  for (int i = 0; i < 3; ++i) s.a[p][mt][i][lane] = uint2{codes[2 * i], codes[2 * i + 1]};
   const uint32_t ea = __builtin_amdgcn_ubfe(rw.sa, 8 * (lane & 3), 8);  // row t = lane % 4
   s.sa[p][mt][lane] = ea - (p ? 5u : 1u);
-  const uint32_t col = tid % 256, nt = col >> 5, wl = col & 31;
   bool bad = ea - kSafeLo > kSafeHi - kSafeLo;
 #pragma unroll
-  for (int hb = 0; hb < kWBlocks; ++hb) {
-    const uint32_t half = kWBlocks == 2 ? hb : tid / 256;
-    const uint32_t ew = __builtin_amdgcn_ubfe(rw.sw[hb], 8 * (col & 3), 8);  // column cl % 4
-    s.w[nt][wl + 32 * half] = uint4{rw.w[hb][0], rw.w[hb][1], rw.w[hb][2], rw.w[hb][3]};
+  for (int k = 0; k < kWLoads; ++k) {
+    const uint32_t u = t + kP * k, col = u % 256, half = u / 256;
+    const uint32_t nt = col >> 5, wl = col & 31;
+    const uint32_t ew = __builtin_amdgcn_ubfe(rw.sw[k], 8 * (col & 3), 8);  // column cl % 4
+    s.w[nt][wl + 32 * half] = uint4{rw.w[k][0], rw.w[k][1], rw.w[k][2], rw.w[k][3]};
     s.sw[nt][wl + 32 * half] = ew;
     bad |= ew - kSafeLo > kSafeHi - kSafeLo;
   }
@@ -241,12 +248,25 @@ __device__ __forceinline__ uint32_t FastEp(const GemmArgs& g, uint32_t o, uint32
   }
 }
 
+// Producer/consumer split.  Threads [0, kBM*4) are producers: they stream
+// the raw A and W bytes through a ring of register sets, convert A into its
+// two FP6 planes and stage both operands in LDS.  Threads [kBM*4, kBM*8)
+// are consumers: they run the matrix cores and alone hold the accumulators.
+// Neither role needs more than 128 registers, so 16 waves share a CU, two
+// of each role per SIMD.  In iteration s the producers convert step s + 2;
+// the consumers issue step s's matrix work and then read step s + 1's
+// operands, whose latency hides under the matrix work.  One barrier per
+// iteration; with kStages = 4 LDS buffers, the buffer a producer writes was
+// last read two iterations earlier.
 template <int kBM, bool kMulti>
-__global__ __launch_bounds__(kBM * 4) void FastFp4Kernel(GemmArgs g) {
+__global__ __launch_bounds__(kBM * 8) void FastFp4Kernel(GemmArgs g) {
   constexpr int kMT = kBM / 32;
-  constexpr int kWaveM = kMT;  // waves: kMT (rows) x 2 (columns), wave tile 32 x 128
-  constexpr int kWBlocks = kBM * 4 >= 2 * kBN ? 1 : 2;
-  __shared__ __attribute__((aligned(16))) StepLds<kMT> lds[2];
+  constexpr int kWaveM = kMT;  // consumer waves: kMT (rows) x 2 (columns), tile 32 x 128
+  constexpr int kP = kBM * 4;  // producer threads
+  constexpr int kWLoads = 512 / kP;
+  constexpr int kStages = 4;
+  static_assert(kRing == 4 && kStages == 4, "the loop is unrolled by 4");
+  __shared__ __attribute__((aligned(16))) StepLds<kMT> lds[kStages];
   __shared__ uint32_t lds_unsafe;
 
   const TileId tile = LogicalTile(g.gx, g.gy, g.gz);
@@ -256,13 +276,55 @@ __global__ __launch_bounds__(kBM * 4) void FastFp4Kernel(GemmArgs g) {
   uint32_t* c = g.c + z * g.c_batch;
   uint8_t* q_out = g.q_out ? g.q_out + z * g.q_batch : nullptr;
 
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t wm = wave % kWaveM, wn = wave / kWaveM;
+  const bool consumer = __builtin_amdgcn_readfirstlane(threadIdx.x >= kP);  // wave-uniform
   const uint32_t q0 = tile.y * (kBM / 4), g0 = tile.x * (kBN / 8);
   const uint32_t row0 = q0 * 4, col0 = g0 * 8;
-  if (tid == 0) lds_unsafe = 0;
+  if (threadIdx.x == 0) lds_unsafe = 0;
   __syncthreads();  // the flag is clear before any wave can raise it
 
+  uint32_t nblocks = 0;
+  for (uint32_t p = 0; p < g.n_pieces; ++p) nblocks += g.piece_kb[p];
+  const uint32_t steps = (nblocks + 1) / 2;
+
+  if (!consumer) {
+    // Ring of kRing raw register sets (slot t % kRing holds step t): the
+    // set of step s + 2 is converted in iteration s and its slot refilled
+    // with step s + 2 + kRing at once.  Loads issue in program order (the
+    // fences stop the scheduler from mixing sets), so the in-order load
+    // counter gives exact waits.  Surplus steps past the end convert to
+    // zeros, so the loop is branch-free.
+    const uint32_t t = threadIdx.x;
+    Raw<kWLoads> ring[kRing];
+    const Offsets<kWLoads> offs = ThreadOffsets<kP, kWLoads>(g, q0, g0, t);
+    auto load = [&](Raw<kWLoads>& rw, uint32_t step) {
+      __builtin_amdgcn_sched_barrier(0);
+      LoadRaw<kP, kWLoads, kMulti>(g, a, w, offs, t, step, steps, nblocks, rw);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    bool unsafe = false;
+#pragma unroll
+    for (int i = 0; i < kRing; ++i) load(ring[i], i);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      unsafe |= StoreRaw<kMT, kP, kWLoads>(ring[i], lds[i], t);
+      load(ring[i], i + kRing);
+    }
+    __syncthreads();
+    for (uint32_t step = 0; step < steps; step += 4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {  // iteration step + i converts step + i + 2
+        unsafe |= StoreRaw<kMT, kP, kWLoads>(ring[(i + 2) % 4], lds[(i + 2) % 4], t);
+        load(ring[(i + 2) % 4], step + i + 2 + kRing);
+        __syncthreads();
+      }
+    }
+    if (unsafe) lds_unsafe = 1;
+    __syncthreads();
+    return;
+  }
+
+  const uint32_t tid = threadIdx.x - kP, lane = tid & 63, wave = tid >> 6;
+  const uint32_t wm = wave % kWaveM, wn = wave / kWaveM;
   // Output (j, r) of this lane: row row0 + wm*32 + 8*(r/4) + 4*(lane/32) + r%4,
   // column col0 + wn*128 + j*32 + lane%32 (32x32 MFMA accumulator layout).
   f32x16 acc[4];
@@ -280,75 +342,65 @@ __global__ __launch_bounds__(kBM * 4) void FastFp4Kernel(GemmArgs g) {
       }
       acc[j][r] = __uint_as_float(init);
     }
+  if (unsafe) lds_unsafe = 1;
 
-  uint32_t nblocks = 0;
-  for (uint32_t p = 0; p < g.n_pieces; ++p) nblocks += g.piece_kb[p];
-  const uint32_t steps = (nblocks + 1) / 2;
-
-  // The loop body is branch-free (every wave runs every step, the last
-  // iteration's surplus steps add zeros), so the compiler waits for each
-  // register set only where it is consumed.  Scale bytes outside the safe
-  // window are collected per thread and acted on once, after the loop.
-  Raw<kWBlocks> ring[kRing];
-  auto compute = [&](const Raw<kWBlocks>& rw, uint32_t step) {
-    StepLds<kMT>& s = lds[step & 1];
-    unsafe |= StoreRaw<kBM, kWBlocks>(rw, s);
-    __syncthreads();
-    i32x8 ahi, alo;
+  // One step's operands in registers: both A planes with their scales, the
+  // four n-tiles of W with theirs.
+  struct Operands {
+    i32x8 ahi, alo, b[4];
+    int sa_hi, sa_lo, sw[4];
+  };
+  auto read = [&](const StepLds<kMT>& s, Operands& op) {
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       const uint2 h2 = s.a[0][wm][i][lane], l2 = s.a[1][wm][i][lane];
-      ahi[2 * i] = (int)h2.x;
-      ahi[2 * i + 1] = (int)h2.y;
-      alo[2 * i] = (int)l2.x;
-      alo[2 * i + 1] = (int)l2.y;
+      op.ahi[2 * i] = (int)h2.x;
+      op.ahi[2 * i + 1] = (int)h2.y;
+      op.alo[2 * i] = (int)l2.x;
+      op.alo[2 * i + 1] = (int)l2.y;
     }
-    ahi[6] = ahi[7] = alo[6] = alo[7] = 0;
-    const int sa_hi = (int)s.sa[0][wm][lane], sa_lo = (int)s.sa[1][wm][lane];
+    op.ahi[6] = op.ahi[7] = op.alo[6] = op.alo[7] = 0;
+    op.sa_hi = (int)s.sa[0][wm][lane];
+    op.sa_lo = (int)s.sa[1][wm][lane];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t nt = wn * 4 + j;
-      const uint4 wv = s.w[nt][lane];
-      i32x8 b;
-      b[0] = (int)wv.x;
-      b[1] = (int)wv.y;
-      b[2] = (int)wv.z;
-      b[3] = (int)wv.w;
-      b[4] = b[5] = b[6] = b[7] = 0;
-      const int sw = (int)s.sw[nt][lane];
-      acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ahi, b, acc[j], 2, 4, 0, sa_hi, 0, sw);
-      acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(alo, b, acc[j], 2, 4, 0, sa_lo, 0, sw);
+      const uint4 wv = s.w[wn * 4 + j][lane];
+      op.b[j][0] = (int)wv.x;
+      op.b[j][1] = (int)wv.y;
+      op.b[j][2] = (int)wv.z;
+      op.b[j][3] = (int)wv.w;
+      op.b[j][4] = op.b[j][5] = op.b[j][6] = op.b[j][7] = 0;
+      op.sw[j] = (int)s.sw[wn * 4 + j][lane];
     }
-    // Keep the step's matrix work inside the step: sinking it past later
-    // steps' barriers only lengthens the operands' live ranges.  The empty
-    // asm emits no instruction.
-#pragma unroll
-    for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(acc[j]));
-    __builtin_amdgcn_sched_barrier(0);
   };
-  // Loads issue in program order (the fences stop the scheduler from
-  // reordering ring sets), so the in-order load counter lets each compute
-  // wait for exactly its own set.
-  const Offsets<kWBlocks> offs = ThreadOffsets<kBM, kWBlocks>(g, q0, g0);
-  auto load = [&](Raw<kWBlocks>& rw, uint32_t step) {
-    __builtin_amdgcn_sched_barrier(0);
-    LoadRaw<kBM, kWBlocks, kMulti>(g, a, w, offs, step, steps, nblocks, rw);
-    __builtin_amdgcn_sched_barrier(0);
+  auto matrix = [&](const Operands& op) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op.ahi, op.b[j], acc[j], 2, 4, 0,
+                                                               op.sa_hi, 0, op.sw[j]);
+      acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op.alo, op.b[j], acc[j], 2, 4, 0,
+                                                               op.sa_lo, 0, op.sw[j]);
+    }
   };
-  // Ring of kRing register sets: each compute consumes the set loaded
-  // kRing - 1 steps earlier while the sets of the following steps are in
-  // flight.
+  Operands ops;
+  __syncthreads();  // steps 0 and 1 staged
+  read(lds[0], ops);
+  for (uint32_t step = 0; step < steps; step += 4) {
 #pragma unroll
-  for (int i = 0; i < kRing - 1; ++i) load(ring[i], i);
-  for (uint32_t step = 0; step < steps; step += kRing) {
+    for (int i = 0; i < 4; ++i) {  // iteration step + i
+      matrix(ops);
+      // Anchor the step's matrix work here (the empty asm emits nothing):
+      // left free, the compiler sinks the pure MFMA calls past later
+      // barriers and keeps every step's operands live.  The fence keeps
+      // the next reads behind the matrix issue, in the same registers.
 #pragma unroll
-    for (int i = 0; i < kRing; ++i) {
-      load(ring[(i + kRing - 1) % kRing], step + i + kRing - 1);
-      compute(ring[i], step + i);
+      for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(acc[j]));
+      __builtin_amdgcn_sched_barrier(0);
+      read(lds[(i + 1) % 4], ops);
+      __syncthreads();
     }
   }
-  if (unsafe) lds_unsafe = 1;
-  __syncthreads();
+  __syncthreads();  // producers' unsafe flags are in
   const bool slow = lds_unsafe != 0;
 
   // Results stay in the accumulator vectors: j is unrolled and r, where a
@@ -421,7 +473,7 @@ __global__ __launch_bounds__(kBM * 4) void FastFp4Kernel(GemmArgs g) {
 template <int kBM, bool kMulti>
 void Launch(const GemmArgs& args, hipStream_t stream) {
   hipLaunchKernelGGL((FastFp4Kernel<kBM, kMulti>), dim3(args.gx * args.gy * args.gz),
-                     dim3(kBM * 4), 0, stream, args);
+                     dim3(kBM * 8), 0, stream, args);
 }
 
 }  // namespace

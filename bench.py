@@ -9,8 +9,9 @@ and activations, L * 2.1 MB > the 256 MB last-level cache) in one batched
 launch; inputs are resident in HBM before timing starts.
 
 Extra fields (skipped with --quick): the same workload in exact mode (bitwise
-equal to the NPU), the M sweep {1, 16, 1024} in fast mode, and the W8 layer
-M=64 K=960 N=2560 with per-channel scale (MULP) and bias (ADDP).
+equal to the NPU), the M sweep {1, 16, 1024} in fast mode, the W8 layer
+M=64 K=960 N=2560 with per-channel scale (MULP) and bias (ADDP), and the
+SmolVLA action-expert step (its GEMM chain) at batch 1 and 32.
 
     python bench.py [--steps K] [--warmup W] [--mode exact|fast] [--layers L]
                     [--quick] [--no-cpu] [--copy-probe MIB]
@@ -157,6 +158,165 @@ class Workload:
         return layer_bytes(self.m, self.n, self.kb, 8 if self.w8 else 4, self.n_vectors) * self.layers
 
 
+def activation_table(kind="silu"):
+    """A 1024-entry TBUF in the layout of tools/compiler/tensors.cpp:28-62:
+    [0, 512) 2^(i/512), [512, 1024) the activation at i/32, each entry
+    {slope: hi32, value: lo32} as fp32 bits."""
+    seg = 512
+    i = np.arange(seg + 1, dtype=np.float64)
+    x = i / 32.0
+    act = 1.0 / (1.0 + np.exp(-x)) if kind == "silu" else \
+        0.5 * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+    out = np.zeros(1024, np.uint64)
+    for base, v in ((0, np.exp2(i / seg)), (512, act)):
+        vb = v.astype(np.float32)
+        slope = (vb[1:].astype(np.float64) - vb[:-1].astype(np.float64)).astype(np.float32)
+        out[base:base + seg] = (slope.view(np.uint32).astype(np.uint64) << np.uint64(32)) | \
+            vb[:-1].view(np.uint32).astype(np.uint64)
+    return out
+
+
+class ExpertStep:
+    """One SmolVLA action-expert step as the GEMM chain the reference compiler
+    emits for it (tools/compiler/smolvla_expert.cpp:250-420, 430-545): 16
+    layers of width 720 (K 736), 15 query / 5 KV heads of 64, SiLU-gated MLP
+    of 2048 (1920 rounded up to a multiple of 256, as the reference sizes it),
+    on a chunk of 50 action tokens per batch element.  Per layer: q (and k, v
+    on the self-attention layers, the even ones) requantized to MXINT8; o
+    with the residual add; up; gate with ACT_MUL(up) and requantize; down
+    with the residual add.  Then the W8 head GEMMs: action_in (+bias,
+    requantize), mlp_in from action and time (+bias, SiLU, requantize),
+    mlp_out (+bias), action_out (+bias).  MXFP4 weights except the W8 heads.
+    Attention, RMSNorm and RoPE are outside this path: their outputs are
+    synthetic MXINT8 tensors of the right shape."""
+
+    WIDTH, KB, Q, KV, HID, KBQ, KBH, LAYERS, CHUNK, ACT = 720, 23, 960, 320, 2048, 30, 64, 16, 50, 32
+
+    def __init__(self, hb, torch, batch, mode):
+        self.hb, self.torch = hb, torch
+        dev = "cuda:0"
+        g = torch.Generator(device=dev).manual_seed(11 + batch)
+        m = self.CHUNK * batch
+        quads = (m + 3) // 4
+        self.m, self.ops = m, 0.0
+        keep = []
+
+        def a_words(kb):  # MXINT8 activations [quads][kb] words, scales 122..127
+            t = torch.randint(0, 256, (quads * kb, 144), generator=g, device=dev, dtype=torch.uint8)
+            t[:, 128:132] = torch.randint(122, 128, (quads * kb, 4), generator=g, device=dev,
+                                          dtype=torch.uint8)
+            t[:, 132:] = 0
+            keep.append(t)
+            return t
+
+        def w_words(n, kb, lo=-10, hi=-2):  # MXFP4 / W8-plane words [n/8][kb]
+            t = torch.randint(0, 256, (n // 8 * kb, 144), generator=g, device=dev, dtype=torch.uint8)
+            t[:, 128:136] = torch.randint(127 + lo, 127 + hi + 1, (n // 8 * kb, 8), generator=g,
+                                          device=dev, dtype=torch.uint8)
+            t[:, 136:] = 0
+            keep.append(t)
+            return t
+
+        def f32(n, scale=1.0):
+            t = torch.randn((m, n), generator=g, device=dev) * scale
+            keep.append(t)
+            return t
+
+        def vec(n, scale):
+            t = torch.randn((n,), generator=g, device=dev) * scale
+            keep.append(t)
+            return t
+
+        tb = torch.from_numpy(activation_table("silu").view(np.int64)).to(dev)
+        keep.append(tb)
+        descs = []
+
+        def add(n, kb, a, planes, c, ops=(), q=None, onto=False):
+            modes = [1, 2] if len(planes) == 2 else [0]
+            md = hb.EXACT if len(planes) == 2 else mode
+            descs.append(hb.linear_desc(m, n, kb, a, planes, modes, c, ops=ops, tbuf=tb, q_out=q,
+                                        onto=onto, mode=md))
+            self.ops += 2.0 * m * n * kb * 32
+
+        x = [f32(self.WIDTH) for _ in range(3)]
+        for layer in range(self.LAYERS):
+            a1, ao, a2 = a_words(self.KB), a_words(self.KBQ), a_words(self.KB)
+            heads = [("q", self.Q)] + ([("k", self.KV), ("v", self.KV)] if layer % 2 == 0 else [])
+            for _, n in heads:
+                add(n, self.KB, a1, [w_words(n, self.KB)], f32(n), q=a_words(n // 32))
+            add(self.WIDTH, self.KBQ, ao, [w_words(self.WIDTH, self.KBQ)], x[1],
+                ops=[(hb.EP_ADD, x[0])])
+            up = f32(self.HID)
+            add(self.HID, self.KB, a2, [w_words(self.HID, self.KB)], up)
+            h = a_words(self.KBH)
+            add(self.HID, self.KB, a2, [w_words(self.HID, self.KB)], f32(self.HID),
+                ops=[(hb.EP_ACT_MUL, up)], q=h)
+            add(self.WIDTH, self.KBH, h, [w_words(self.WIDTH, self.KBH)], x[2],
+                ops=[(hb.EP_ADD, x[1])])
+        w8 = lambda n, kb: [w_words(n, kb, 6, 6), w_words(n, kb, 6, 6)]  # MXINT8 weights, e = 6
+        act, tim, hid, xin = a_words(1), a_words(self.KB), a_words(self.KB), a_words(self.KB)
+        pad = self.KB * 32
+        add(pad, 1, act, w8(pad, 1), f32(pad), ops=[(hb.EP_ADDP, vec(pad, 0.1))], q=xin)
+        mlp_in = f32(pad)
+        add(pad, self.KB, xin, w8(pad, self.KB), mlp_in)
+        add(pad, self.KB, tim, w8(pad, self.KB), mlp_in, onto=True,
+            ops=[(hb.EP_ADDP, vec(pad, 0.1)), (hb.EP_ACT, None)], q=hid)
+        add(self.WIDTH, self.KB, hid, w8(self.WIDTH, self.KB), x[0],
+            ops=[(hb.EP_ADDP, vec(self.WIDTH, 0.1))])
+        add(self.ACT, self.KB, hid, w8(self.ACT, self.KB), f32(self.ACT),
+            ops=[(hb.EP_ADDP, vec(self.ACT, 0.1))])
+        self.descs, self.keep = descs, keep
+        torch.cuda.synchronize()
+
+    def run(self, ctx):
+        for d in self.descs:
+            self.hb.launch(d, ctx)
+
+
+def time_expert_step(hb, torch, ctx, batch, mode, steps=10):
+    """Milliseconds per expert step: eager launches on one stream, and the
+    same chain replayed as one captured HIP graph."""
+    work = ExpertStep(hb, torch, batch, mode)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    for _ in range(2):
+        work.run(ctx)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        work.run(ctx)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    eager = t0.elapsed_time(t1) / steps
+    out = {"batch": batch, "m": work.m, "gemms": len(work.descs), "gops": round(work.ops / 1e9, 3),
+           "eager_ms": round(eager, 4)}
+    try:
+        side = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            ctx.set_stream(side.cuda_stream)
+            work.run(ctx)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+            work.run(ctx)
+        ctx.set_stream(stream.cuda_stream)
+        graph.replay()
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        out["graph_ms"] = round(t0.elapsed_time(t1) / steps, 4)
+    except Exception as e:  # capture is optional for the measurement
+        ctx.set_stream(stream.cuda_stream)
+        out["graph_error"] = str(e)[:200]
+    del work
+    return out
+
+
 def time_steps(hb, torch, ctx, stream, work, steps, warmup):
     """Average ms per step over `steps` back-to-back batched launches, timed
     with events on the stream the kernels run on."""
@@ -283,6 +443,11 @@ def main():
                                        "per step", "value": round(t8, 3), "unit": "TOPS",
                            "ms_per_step": round(ms8, 4), "roofline": r8}
         del w8
+
+        # SmolVLA action-expert step (GEMM chain), B = 1 and 32
+        out["smolvla_expert_step_ms"] = {f"B={b}": time_expert_step(hb, torch, ctx, b, mode)
+                                         for b in (1, 32)}
+        ctx.set_stream(stream.cuda_stream)
 
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.m, n, kb)

@@ -373,6 +373,12 @@ def linear(ctx: Context | None = None, sync: bool = True, **kw) -> None:
     _check(f(ctx.handle, C.byref(d)))
 
 
+def launch(desc: _LinearDesc, ctx: Context | None = None) -> None:
+    """hb_linear_async on a prebuilt descriptor (ordered on the context's stream)."""
+    ctx = ctx or default_context()
+    _check(lib().hb_linear_async(ctx.handle, C.byref(desc)))
+
+
 def linear_batched(descs, ctx: Context | None = None) -> None:
     ctx = ctx or default_context()
     arr = (_LinearDesc * len(descs))(*descs)

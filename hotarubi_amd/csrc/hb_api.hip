@@ -19,6 +19,7 @@ struct hb_ctx {
   hipStream_t stream = nullptr;
   bool own_stream = false;
   uint32_t* d_flag = nullptr;  // device flag word for hb_encode_mxint8
+  hb::Workspace ws;            // split partials / deferred epilogue inputs
 };
 
 struct hb_onchip {
@@ -394,6 +395,7 @@ int hb_ctx_destroy(hb_ctx* ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->d_flag) (void)hipFree(ctx->d_flag);
+  if (ctx->ws.ptr) (void)hipFree(ctx->ws.ptr);
   if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return HB_OK;
@@ -575,7 +577,7 @@ int hb_linear_async(hb_ctx* ctx, const hb_linear_desc* d) {
   if (int rc = Enter(ctx)) return rc;
   hb::GemmArgs g;
   if (int rc = LinearArgs(d, &g)) return rc;
-  hipError_t err = hb::LaunchLinear(g, 1, d->flags == HB_LINEAR_FAST, ctx->stream);
+  hipError_t err = hb::LaunchLinear(g, 1, d->flags == HB_LINEAR_FAST, ctx->ws, ctx->stream);
   if (err != hipSuccess) return HipFail(err, "linear launch");
   return HB_OK;
 }
@@ -624,7 +626,7 @@ int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count
       if (!same) return Fail(HB_EINVAL, "layer %u differs in shape, schedule, ops or stride", i);
     }
   }
-  hipError_t err = hb::LaunchLinear(g, count, d[0].flags == HB_LINEAR_FAST, ctx->stream);
+  hipError_t err = hb::LaunchLinear(g, count, d[0].flags == HB_LINEAR_FAST, ctx->ws, ctx->stream);
   if (err != hipSuccess) return HipFail(err, "linear launch");
   return HB_OK;
 }

@@ -50,16 +50,17 @@ __device__ __forceinline__ uint32_t Interpolate(uint64_t entry, uint32_t fractio
   return FAdd((uint32_t)entry, MulFractionBits((uint32_t)(entry >> 32), fraction));
 }
 
-// T(|x|) from TBUF[512, 1024): |x| truncated to UQ4.21, 9-bit index,
-// 16-bit fraction; 1.0 at |x| >= 16.
-__device__ __forceinline__ uint32_t Activation(uint32_t prod, const uint64_t* tbuf) {
+// T(|x|) from the activation half of TBUF, t = TBUF + 512 (the 512 entries
+// of [512, 1024)): |x| truncated to UQ4.21, 9-bit index, 16-bit fraction;
+// 1.0 at |x| >= 16.
+__device__ __forceinline__ uint32_t Activation(uint32_t prod, const uint64_t* t) {
   const uint32_t e = ExpField(prod);
   if (e >= 131u) return kOne;
   const uint32_t sig = Significand(prod);
   uint32_t fixed = 0;
   if (e == 130u) fixed = sig << 1;
   else if (e >= 105u) fixed = sig >> (129u - e);
-  return Interpolate(tbuf[512u + (fixed >> 16)], fixed & 0xFFFFu);
+  return Interpolate(t[fixed >> 16], fixed & 0xFFFFu);
 }
 
 // One VEC lane with c0 = 0, b = 1, post = ADD: Add(Mul(Add(x, c0), b), c1).
@@ -73,12 +74,35 @@ enum : uint32_t {
   kEpCopy = 6, kEpRelu = 7, kEpAct = 8, kEpActMul = 9, kEpAdd = 0x100
 };
 
-// ACT gate pass: x < 0 ? -(x*T) + x : x*T  (post = SIGNFIX, c1 = raw x)
-__device__ __forceinline__ uint32_t ActGate(uint32_t x, const uint64_t* tbuf) {
+// ACT gate pass: x < 0 ? -(x*T) + x : x*T  (post = SIGNFIX, c1 = raw x);
+// t = TBUF + 512.
+__device__ __forceinline__ uint32_t ActGate(uint32_t x, const uint64_t* t) {
   const uint32_t pre = FAdd(x, 0u);
-  const uint32_t t = Activation(FMul(pre, kOne), tbuf);
-  const uint32_t prod = FMul(pre, t);
+  const uint32_t a = Activation(FMul(pre, kOne), t);
+  const uint32_t prod = FMul(pre, a);
   return (x >> 31) ? FAdd(prod ^ kSign, x) : FAdd(prod, 0u);
+}
+
+// One fused epilogue op on one element y (lane formulas of the VEC library
+// entries).  Its operands are passed in already loaded: x2 the element of
+// the op's [m][n] tensor (ADD, ACT_MUL), p the column's vector value (ADDP,
+// MULP), imm the SCALE factor; t = TBUF + 512.
+__device__ __forceinline__ uint32_t EpApply(uint32_t kind, uint32_t imm, uint32_t y, uint32_t x2,
+                                            uint32_t p, const uint64_t* t) {
+  switch (kind) {
+    case kEpAddP: return LaneAddMul(y, p, kOne, 0u);
+    case kEpMulP: return LaneAddMul(y, 0u, p, 0u);
+    case kEpScale: return LaneAddMul(y, 0u, imm, 0u);
+    case kEpCopy: return LaneAddMul(y, 0u, kOne, 0u);
+    case kEpRelu: {
+      const uint32_t prod = FMul(FAdd(y, 0u), kOne);
+      return FAdd(MaxGreaterEqual(prod, 0u) ? prod : 0u, 0u);
+    }
+    case kEpAdd: return LaneAddMul(y, x2, kOne, 0u);
+    case kEpAct: return ActGate(y, t);
+    case kEpActMul: return LaneAddMul(ActGate(y, t), 0u, x2, 0u);
+    default: return y;
+  }
 }
 
 // QuantizeBlock for one token: values[32] -> bytes and scale byte.

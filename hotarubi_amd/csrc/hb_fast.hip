@@ -126,11 +126,11 @@ __device__ __forceinline__ Offsets<kWLoads> ThreadOffsets(const GemmArgs& g, uin
 // (uniform base, 32-bit lane offset).
 template <int kP, int kWLoads, bool kMulti>
 __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, const uint8_t* w,
-                                        const Offsets<kWLoads>& o, uint32_t t,
+                                        const Offsets<kWLoads>& o, uint32_t t, uint32_t s0,
                                         uint32_t live_step, uint32_t steps, uint32_t nblocks,
                                         Raw<kWLoads>& rw) {
   const uint32_t h = (t & 63) >> 5;
-  const uint32_t step = min(live_step, steps - 1);
+  const uint32_t step = s0 + min(live_step, steps - 1);  // steps of this split start at s0
   const uint32_t ub0 = BlockOf<kMulti>(g, 2 * step) * kDdrWord;
   const uint32_t ub1 = BlockOf<kMulti>(g, min(2 * step + 1, nblocks - 1)) * kDdrWord;
   const uint8_t* ab = a + ub0;                 // uniform
@@ -223,31 +223,6 @@ __device__ __forceinline__ uint32_t SlowLinear(const GemmArgs& g, const uint8_t*
   return acc;
 }
 
-// z: layer of a batched launch (op vectors advance by their per-layer stride).
-__device__ __forceinline__ uint32_t FastEp(const GemmArgs& g, uint32_t o, uint32_t z, uint32_t y,
-                                           uint32_t row, uint32_t col, bool row_ok) {
-  switch (g.op_kind[o]) {
-    case kEpAddP: return LaneAddMul(y, g.op_vec[o][z * g.op_vec_batch[o] + col], kOne, 0u);
-    case kEpMulP: return LaneAddMul(y, 0u, g.op_vec[o][z * g.op_vec_batch[o] + col], 0u);
-    case kEpScale: return LaneAddMul(y, 0u, g.op_imm[o], 0u);
-    case kEpCopy: return LaneAddMul(y, 0u, kOne, 0u);
-    case kEpRelu: {
-      const uint32_t prod = FMul(FAdd(y, 0u), kOne);
-      return FAdd(MaxGreaterEqual(prod, 0u) ? prod : 0u, 0u);
-    }
-    case kEpAdd: {
-      const uint32_t x2 = row_ok ? g.op_x2[o][z * g.op_x2_batch[o] + (size_t)row * g.n + col] : 0u;
-      return LaneAddMul(y, x2, kOne, 0u);
-    }
-    case kEpAct: return ActGate(y, g.tbuf);
-    case kEpActMul: {
-      const uint32_t x2 = row_ok ? g.op_x2[o][z * g.op_x2_batch[o] + (size_t)row * g.n + col] : 0u;
-      return LaneAddMul(ActGate(y, g.tbuf), 0u, x2, 0u);
-    }
-    default: return y;
-  }
-}
-
 // Producer/consumer split.  Threads [0, kBM*4) are producers: they stream
 // the raw A and W bytes through a ring of register sets, convert A into its
 // two FP6 planes and stage both operands in LDS.  Threads [kBM*4, kBM*8)
@@ -267,10 +242,13 @@ __global__ __launch_bounds__(kBM * 8) void FastFp4Kernel(GemmArgs g) {
   constexpr int kStages = 4;
   static_assert(kRing == 4 && kStages == 4, "the loop is unrolled by 4");
   __shared__ __attribute__((aligned(16))) StepLds<kMT> lds[kStages];
+  __shared__ uint64_t lds_act[512];  // activation half of TBUF, for the epilogue
   __shared__ uint32_t lds_unsafe;
 
   const TileId tile = LogicalTile(g.gx, g.gy, g.gz);
-  const uint32_t z = tile.z;
+  // z: the layer of a batched launch, or the K split of a split one layer
+  const uint32_t split = g.splits > 1 ? tile.z : 0u;
+  const uint32_t z = g.splits > 1 ? 0u : tile.z;
   const uint8_t* a = g.a + z * g.a_batch;
   const uint8_t* w = g.w[0] + z * g.w_batch;
   uint32_t* c = g.c + z * g.c_batch;
@@ -284,7 +262,9 @@ __global__ __launch_bounds__(kBM * 8) void FastFp4Kernel(GemmArgs g) {
 
   uint32_t nblocks = 0;
   for (uint32_t p = 0; p < g.n_pieces; ++p) nblocks += g.piece_kb[p];
-  const uint32_t steps = (nblocks + 1) / 2;
+  const uint32_t all_steps = (nblocks + 1) / 2;
+  const uint32_t s0 = split * g.split_steps;  // every split has at least one step
+  const uint32_t steps = g.splits > 1 ? min(all_steps - s0, g.split_steps) : all_steps;
 
   if (!consumer) {
     // Ring of kRing raw register sets (slot t % kRing holds step t): the
@@ -298,7 +278,7 @@ __global__ __launch_bounds__(kBM * 8) void FastFp4Kernel(GemmArgs g) {
     const Offsets<kWLoads> offs = ThreadOffsets<kP, kWLoads>(g, q0, g0, t);
     auto load = [&](Raw<kWLoads>& rw, uint32_t step) {
       __builtin_amdgcn_sched_barrier(0);
-      LoadRaw<kP, kWLoads, kMulti>(g, a, w, offs, t, step, steps, nblocks, rw);
+      LoadRaw<kP, kWLoads, kMulti>(g, a, w, offs, t, s0, step, steps, nblocks, rw);
       __builtin_amdgcn_sched_barrier(0);
     };
     bool unsafe = false;
@@ -319,6 +299,8 @@ __global__ __launch_bounds__(kBM * 8) void FastFp4Kernel(GemmArgs g) {
       }
     }
     if (unsafe) lds_unsafe = 1;
+    if (g.tbuf != nullptr)  // the producers are done: stage the activation table
+      for (uint32_t i = t; i < 512; i += kP) lds_act[i] = g.tbuf[512 + i];
     __syncthreads();
     return;
   }
@@ -336,7 +318,7 @@ __global__ __launch_bounds__(kBM * 8) void FastFp4Kernel(GemmArgs g) {
       const uint32_t row = row0 + wm * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r & 3);
       const uint32_t col = col0 + wn * 128 + j * 32 + (lane & 31);
       uint32_t init = 0;
-      if (g.acc && row < g.m && col < g.n) {
+      if (g.acc && split == 0 && row < g.m && col < g.n) {
         init = c[(size_t)row * g.n + col];
         unsafe |= ExpField(init) > 252u;
       }
@@ -422,18 +404,58 @@ __global__ __launch_bounds__(kBM * 8) void FastFp4Kernel(GemmArgs g) {
         const uint32_t row = row_l + 8 * (r / 4) + (r & 3), col = col_l + j * 32;
         if ((row >> 2) >= g.quads || col >= g.n) continue;
         const uint32_t init = (g.acc && row < g.m) ? c[(size_t)row * g.n + col] : 0u;
-        acc[j][r] = __uint_as_float(SlowLinear(g, a, w, init, row, col));
+        // a split layer's exact result comes whole from split 0
+        acc[j][r] = __uint_as_float(split == 0 ? SlowLinear(g, a, w, init, row, col) : 0u);
       }
   }
-  for (uint32_t o = 0; o < g.n_ops; ++o) {
+  if (g.ws != nullptr) {  // deferred epilogue: this split's sums, rows [0, 4*quads)
+    float* out = g.ws + (size_t)split * g.quads * 4 * g.n;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      for (uint32_t r = 0; r < 16; ++r) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
         const uint32_t row = row_l + 8 * (r / 4) + (r & 3), col = col_l + j * 32;
-        if ((row >> 2) < g.quads && col < g.n)
-          acc[j][r] =
-              __uint_as_float(FastEp(g, o, z, __float_as_uint(acc[j][r]), row, col, row < g.m));
+        if ((row >> 2) < g.quads && col < g.n) out[(size_t)row * g.n + col] = acc[j][r];
       }
+    return;
+  }
+  // Epilogue ops, op by op, in two halves of the lane's outputs.  A half's
+  // operands are loaded first, all at once (independent loads, one wait);
+  // the element loop then only computes.
+  for (uint32_t o = 0; o < g.n_ops; ++o) {
+    const uint32_t kind = g.op_kind[o], imm = g.op_imm[o];
+    const bool has_x2 = kind == kEpAdd || kind == kEpActMul;
+    const bool has_vec = kind == kEpAddP || kind == kEpMulP;
+    const uint32_t* x2 = g.op_x2[o] + z * g.op_x2_batch[o];
+    const uint32_t* v = g.op_vec[o] + z * g.op_vec_batch[o];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      f32x16 xv[2] = {};
+      uint32_t pv[2] = {0u, 0u};
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const uint32_t col = col_l + (2 * half + jj) * 32;
+        if (has_x2) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const uint32_t row = row_l + 8 * (r / 4) + (r & 3);
+            xv[jj][r] = __uint_as_float(row < g.m && col < g.n ? x2[(size_t)row * g.n + col] : 0u);
+          }
+        }
+        if (has_vec) pv[jj] = col < g.n ? v[col] : 0u;
+      }
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * half + jj;
+        const uint32_t col = col_l + j * 32;
+        for (uint32_t r = 0; r < 16; ++r) {
+          const uint32_t row = row_l + 8 * (r / 4) + (r & 3);
+          if ((row >> 2) < g.quads && col < g.n)
+            acc[j][r] = __uint_as_float(EpApply(kind, imm, __float_as_uint(acc[j][r]),
+                                                __float_as_uint(xv[jj][r]), pv[jj], lds_act));
+        }
+      }
+    }
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -477,6 +499,11 @@ void Launch(const GemmArgs& args, hipStream_t stream) {
 }
 
 }  // namespace
+
+void FastFp4Grid(const GemmArgs& args, uint32_t* gx, uint32_t* gy) {
+  *gx = (args.groups + kBN / 8 - 1) / (kBN / 8);
+  *gy = args.quads * 4 > 64 ? (args.quads + 31) / 32 : (args.quads + 15) / 16;
+}
 
 hipError_t LaunchLinearFastFp4(const GemmArgs& in, uint32_t batch, hipStream_t stream) {
   GemmArgs args = in;

@@ -309,32 +309,6 @@ __device__ __forceinline__ uint32_t SlowOutput(const GemmArgs& g, const uint8_t*
   return acc;
 }
 
-// One epilogue op on one element (lane formulas of the VEC library entries).
-// z: layer of a batched launch (op vectors advance by their per-layer stride).
-__device__ __forceinline__ uint32_t EpOp(const GemmArgs& g, uint32_t o, uint32_t z, uint32_t y,
-                                         uint32_t row, uint32_t col, bool row_ok) {
-  switch (g.op_kind[o]) {
-    case kEpAddP: return LaneAddMul(y, g.op_vec[o][z * g.op_vec_batch[o] + col], kOne, 0u);
-    case kEpMulP: return LaneAddMul(y, 0u, g.op_vec[o][z * g.op_vec_batch[o] + col], 0u);
-    case kEpScale: return LaneAddMul(y, 0u, g.op_imm[o], 0u);
-    case kEpCopy: return LaneAddMul(y, 0u, kOne, 0u);
-    case kEpRelu: {
-      const uint32_t prod = FMul(FAdd(y, 0u), kOne);
-      return FAdd(MaxGreaterEqual(prod, 0u) ? prod : 0u, 0u);
-    }
-    case kEpAdd: {
-      const uint32_t x2 = row_ok ? g.op_x2[o][z * g.op_x2_batch[o] + (size_t)row * g.n + col] : 0u;
-      return LaneAddMul(y, x2, kOne, 0u);
-    }
-    case kEpAct: return ActGate(y, g.tbuf);
-    case kEpActMul: {
-      const uint32_t x2 = row_ok ? g.op_x2[o][z * g.op_x2_batch[o] + (size_t)row * g.n + col] : 0u;
-      return LaneAddMul(ActGate(y, g.tbuf), 0u, x2, 0u);
-    }
-    default: return y;
-  }
-}
-
 // The exact tile kernel.  Per K block: stage A (bf16, scaled) and W (bf16,
 // unscaled) in LDS; per 16x16 tile one MFMA with a zero accumulator gives
 // s * 2^(ea-127) exactly; the fold is acc = fma(that, 2^(ew-127+SBIAS), acc),
@@ -348,6 +322,7 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint16_t lds_w[2][kBN * kLdsRow];
   __shared__ __attribute__((aligned(16))) uint8_t lds_ws[2][kBN];
   __shared__ uint32_t lut[2 * 256];
+  __shared__ uint64_t lds_act[512];  // activation half of TBUF, for the epilogue
   __shared__ uint32_t lds_unsafe;
 
   const uint8_t* a = g.a;
@@ -477,6 +452,8 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
     compute_chunk(set1, base + kChunk);
   }
   if (unsafe) lds_unsafe = 1;
+  if (kLinear && g.tbuf != nullptr)
+    for (uint32_t i = tid; i < 512; i += kThreads) lds_act[i] = g.tbuf[512 + i];
   __syncthreads();
   const bool slow = lds_unsafe != 0;
 
@@ -510,18 +487,55 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
         res[i][e] = __uint_as_float(SlowOutput<kLinear>(g, a, w0, w1, init, row, col));
       }
   }
-
-  // Epilogue ops, then stores.
-  if (kLinear) {
-    for (uint32_t o = 0; o < g.n_ops; ++o) {
+  if (kLinear && g.ws != nullptr) {  // deferred epilogue: the fold results, rows [0, 4*quads)
 #pragma unroll
-      for (int i = 0; i < T::kTI; ++i)
-        for (uint32_t e = 0; e < 16; ++e) {
-          const uint32_t row = row_l + i * 16 + (e & 3), col = col_l + (e >> 2) * 16;
-          if ((row >> 2) < g.quads && (col >> 3) < g.groups)
-            res[i][e] =
-                __uint_as_float(EpOp(g, o, z, __float_as_uint(res[i][e]), row, col, row < g.m));
+    for (int i = 0; i < T::kTI; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t row = row_l + i * 16 + (e & 3), col = col_l + (e >> 2) * 16;
+        if ((row >> 2) < g.quads && (col >> 3) < g.groups) g.ws[(size_t)row * g.n + col] = res[i][e];
+      }
+    return;
+  }
+
+  // Epilogue ops, op by op, in groups of two row tiles.  A group's operands
+  // are loaded first, all at once (independent loads, one wait); the element
+  // loop then only computes.
+  if (kLinear) {
+    constexpr int kGroup = T::kTI >= 2 ? 2 : 1;
+    for (uint32_t o = 0; o < g.n_ops; ++o) {
+      const uint32_t kind = g.op_kind[o], imm = g.op_imm[o];
+      const bool has_x2 = kind == kEpAdd || kind == kEpActMul;
+      const uint32_t* x2 = g.op_x2[o] + z * g.op_x2_batch[o];
+      uint32_t pv[4] = {0u, 0u, 0u, 0u};
+      if (kind == kEpAddP || kind == kEpMulP) {
+        const uint32_t* v = g.op_vec[o] + z * g.op_vec_batch[o];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) pv[jj] = col_l + jj * 16 < g.n ? v[col_l + jj * 16] : 0u;
+      }
+#pragma unroll
+      for (int i0 = 0; i0 < T::kTI; i0 += kGroup) {
+        f32x16 xv[kGroup] = {};
+        if (has_x2) {
+#pragma unroll
+          for (int ii = 0; ii < kGroup; ++ii)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const uint32_t row = row_l + (i0 + ii) * 16 + (e & 3), col = col_l + (e >> 2) * 16;
+              xv[ii][e] = __uint_as_float(row < g.m && col < g.n ? x2[(size_t)row * g.n + col] : 0u);
+            }
         }
+#pragma unroll
+        for (int ii = 0; ii < kGroup; ++ii) {
+          const int i = i0 + ii;
+          for (uint32_t e = 0; e < 16; ++e) {
+            const uint32_t row = row_l + i * 16 + (e & 3), col = col_l + (e >> 2) * 16;
+            if ((row >> 2) < g.quads && (col >> 3) < g.groups)
+              res[i][e] = __uint_as_float(EpApply(kind, imm, __float_as_uint(res[i][e]),
+                                                  __float_as_uint(xv[ii][e]), pv[e >> 2], lds_act));
+          }
+        }
+      }
     }
   }
 #pragma unroll
@@ -643,11 +657,65 @@ hipError_t LaunchGemmInstrAliased(const GemmArgs& args, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t LaunchLinear(const GemmArgs& args, uint32_t batch, bool fast, hipStream_t stream) {
-  if (fast && args.n_planes == 1 && args.modes[0] == kModeFp4)
-    return LaunchLinearFastFp4(args, batch, stream);
-  // every other layer runs exactly (which meets the fast-mode tolerance)
-  return LaunchTiles<true>(args, batch, stream);
+void ExactGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy) {
+  if (args.quads * 4 <= 32) {
+    *gx = (args.groups + 31) / 32;
+    *gy = (args.quads + 7) / 8;
+  } else {
+    *gx = (args.groups + 15) / 16;
+    *gy = (args.quads + 31) / 32;
+  }
+}
+
+namespace {
+// A single layer with fewer tiles than this spreads its work: K splits in
+// fast mode (to about kTargetWorkgroups workgroups, at least two K-steps
+// each) and the element-parallel deferred epilogue.
+constexpr uint32_t kSmallGrid = 128, kTargetWorkgroups = 256;
+}  // namespace
+
+hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace& ws,
+                        hipStream_t stream) {
+  GemmArgs args = in;
+  args.ws = nullptr;
+  args.splits = 1;
+  args.split_steps = 0;
+  // Fast mode runs MXFP4 on the block-scaled matrix cores; every other layer
+  // runs exactly (which meets the fast-mode tolerance).
+  const bool fp4 = fast && args.n_planes == 1 && args.modes[0] == kModeFp4;
+  uint32_t gx, gy;
+  if (fp4) FastFp4Grid(args, &gx, &gy);
+  else ExactGrid(args, &gx, &gy);
+  const bool small = batch == 1 && gx * gy < kSmallGrid;
+  if (small && fp4) {
+    uint32_t nblocks = 0;
+    for (uint32_t p = 0; p < args.n_pieces; ++p) nblocks += args.piece_kb[p];
+    const uint32_t steps = (nblocks + 1) / 2;
+    const uint32_t want = (kTargetWorkgroups + gx * gy - 1) / (gx * gy);
+    uint32_t per = (steps + want - 1) / want;
+    per = per < 2 ? 2 : per;
+    args.splits = (steps + per - 1) / per;
+    args.split_steps = per;
+  }
+  const bool defer = small && (args.n_ops > 0 || args.q_out != nullptr || args.splits > 1);
+  if (!defer) return fp4 ? LaunchLinearFastFp4(args, batch, stream) : LaunchTiles<true>(args, batch, stream);
+
+  const size_t bytes = (size_t)args.splits * args.quads * 4 * args.n * sizeof(float);
+  if (ws.bytes < bytes) {
+    hipError_t err = hipStreamSynchronize(stream);  // the old buffer may be in use
+    if (err != hipSuccess) return err;
+    if (ws.ptr != nullptr) (void)hipFree(ws.ptr);
+    ws.ptr = nullptr;
+    ws.bytes = 0;
+    err = hipMalloc(&ws.ptr, bytes);
+    if (err != hipSuccess) return err;
+    ws.bytes = bytes;
+  }
+  args.ws = ws.ptr;
+  const hipError_t err = fp4 ? LaunchLinearFastFp4(args, args.splits, stream)  // z = split
+                             : LaunchTiles<true>(args, 1, stream);
+  if (err != hipSuccess) return err;
+  return LaunchEpilogue(args, stream);
 }
 
 }  // namespace hb

@@ -50,8 +50,21 @@ struct GemmArgs {
   // batched linear: per-layer strides (bytes / elements), 0 for one layer
   uint64_t a_batch, w_batch, c_batch, q_batch;
   uint64_t op_vec_batch[kMaxOps], op_x2_batch[kMaxOps];  // elements
-  // tile grid (x: column tiles, y: row tiles, z: layers), launched 1-D
+  // tile grid (x: column tiles, y: row tiles, z: layers or K splits), 1-D
   uint32_t gx, gy, gz;
+  // Deferred epilogue (linear level, one layer): when ws is set the GEMM
+  // kernels write their raw fold results, rows [0, 4*quads), row-major
+  // [split][4*quads][n], and EpilogueKernel finishes (sum over splits, -0,
+  // ops, C, requantize).  K splits (fast mode): split s covers the steps
+  // [s * split_steps, (s + 1) * split_steps).
+  float* ws;
+  uint32_t splits, split_steps;
+};
+
+// Device scratch owned by a context, grown on demand.
+struct Workspace {
+  float* ptr = nullptr;
+  size_t bytes = 0;
 };
 
 // Workgroup -> tile mapping.  The hardware deals workgroups round-robin over
@@ -77,9 +90,19 @@ __device__ __forceinline__ TileId LogicalTile(uint32_t gx, uint32_t gy, uint32_t
 // Launchers (hb_gemm.hip).
 hipError_t LaunchGemmInstr(const GemmArgs& args, hipStream_t stream);
 hipError_t LaunchGemmInstrAliased(const GemmArgs& args, hipStream_t stream);
-hipError_t LaunchLinear(const GemmArgs& args, uint32_t batch, bool fast, hipStream_t stream);
+// Linear layer: picks the kernel, and for a single small layer (few tiles)
+// K splits (fast mode) and/or the deferred element-parallel epilogue, in
+// which case it may grow `ws` (synchronizing the stream first).
+hipError_t LaunchLinear(const GemmArgs& args, uint32_t batch, bool fast, Workspace& ws,
+                        hipStream_t stream);
 // Fast MXFP4 path (hb_fast.hip): one FP4 plane, block-scaled f8f6f4 MFMA.
+// Tile grid of the fast kernel for `args` (column tiles, row tiles).
+void FastFp4Grid(const GemmArgs& args, uint32_t* gx, uint32_t* gy);
 hipError_t LaunchLinearFastFp4(const GemmArgs& args, uint32_t batch, hipStream_t stream);
+// Exact tile kernel grid for a linear layer (column tiles, row tiles).
+void ExactGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy);
+// Deferred epilogue (hb_vec.hip): reads args.ws, writes C and q_out.
+hipError_t LaunchEpilogue(const GemmArgs& args, hipStream_t stream);
 
 // VEC (hb_vec.hip).
 struct VecPass {

@@ -111,7 +111,10 @@ const char* hb_last_error(void);
 int hb_ctx_create(int device, hb_ctx** out);
 int hb_ctx_destroy(hb_ctx* ctx);
 /* Order the context's work on an existing hipStream_t from now on (NULL is
- * the null stream); the context's own stream, if any, is released. */
+ * the null stream); the context's own stream, if any, is released.  A
+ * context reuses one device workspace across calls (small layers split
+ * their K range and finish in a separate element-parallel epilogue), so
+ * work issued on an earlier stream must be complete before the switch. */
 int hb_ctx_set_stream(hb_ctx* ctx, void* hip_stream);
 int hb_ctx_synchronize(hb_ctx* ctx);
 
@@ -218,6 +221,9 @@ typedef struct hb_linear_desc {
   uint32_t flags; /* HB_LINEAR_EXACT or HB_LINEAR_FAST */
 } hb_linear_desc;
 
+/* A single small layer (fewer than 128 output tiles) may grow the context's
+ * workspace on its first call of a larger shape (hipMalloc after a stream
+ * synchronize); warm a shape up before capturing it in a graph. */
 int hb_linear(hb_ctx* ctx, const hb_linear_desc* desc);
 int hb_linear_async(hb_ctx* ctx, const hb_linear_desc* desc);
 /* `count` independent layers in one launch (e.g. the same projection of

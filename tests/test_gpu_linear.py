@@ -161,6 +161,33 @@ def test_fast_mode_tolerance(gpu, m, w8):
         assert (err <= 2.0 ** -20 * block_abs_sums(m, n, kb, a, planes, modes) + 1e-30).all()
 
 
+@pytest.mark.parametrize("m", [1, 50, 128])
+def test_fast_split_layer_with_epilogue(gpu, m):
+    """A single small fast-mode layer takes the K-split path with the
+    element-parallel epilogue: pieces, onto, MULP and ADDP, requantize."""
+    rng = np.random.default_rng(70 + m)
+    n, k = 320, 1280
+    kb, a, planes, modes = make_layer(rng, m, n, k, False)
+    onto = helpers.random_fp32_words(rng, (m, n), 120, 130)
+    scale = helpers.random_fp32_words(rng, (n,), 117, 122)
+    bias = helpers.random_fp32_words(rng, (n,), 118, 124)
+    ops = [(hb.EP_MULP, scale), (hb.EP_ADDP, bias)]
+    pieces = [(24, 16), (0, 17), (17, 7)]
+    got, gq = run_linear(gpu, m, n, kb, a, planes, modes, ops, pieces=pieces, onto=onto,
+                         quantize=True, mode=hb.FAST)
+    want, wq = oracle_linear(m, n, kb, a, planes, modes, ops, pieces=pieces, onto=onto,
+                             quantize=True)
+    g, w = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
+    row_scale = np.abs(w).max(axis=1, keepdims=True)
+    assert (np.abs(g - w) <= 1e-5 * row_scale).all(), float((np.abs(g - w) / row_scale).max())
+    # requantized bytes: equal except where the fp32 values straddle a rounding step
+    gqb = gq.reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
+    wqb = wq.reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
+    assert np.abs(gqb - wqb).max() <= 1 and (gqb != wqb).mean() < 0.01
+    assert np.array_equal(gq.reshape(-1, 144)[:, 128:], wq.reshape(-1, 144)[:, 128:]) or \
+        (gq.reshape(-1, 144)[:, 128:132] != wq.reshape(-1, 144)[:, 128:132]).mean() < 0.01
+
+
 @pytest.mark.parametrize("w8", [False, True])
 def test_pieces_and_onto(gpu, w8):
     rng = np.random.default_rng(20 + w8)

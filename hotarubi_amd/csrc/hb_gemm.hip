@@ -680,14 +680,16 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   args.ws = nullptr;
   args.splits = 1;
   args.split_steps = 0;
-  // Fast mode runs MXFP4 on the block-scaled matrix cores; every other layer
-  // runs exactly (which meets the fast-mode tolerance).
-  const bool fp4 = fast && args.n_planes == 1 && args.modes[0] == kModeFp4;
+  // Fast mode runs MXFP4 and W8 (hi, lo) on the block-scaled matrix cores;
+  // any other plane list runs exactly (which meets the fast-mode tolerance).
+  const bool fastk = fast && FastEligible(args);
   uint32_t gx, gy;
-  if (fp4) FastFp4Grid(args, &gx, &gy);
+  if (fastk) FastGrid(args, &gx, &gy, &args.tile_rows);
   else ExactGrid(args, &gx, &gy);
+  args.gx = gx;
+  args.gy = gy;
   const bool small = batch == 1 && gx * gy < kSmallGrid;
-  if (small && fp4) {
+  if (small && fastk) {
     uint32_t nblocks = 0;
     for (uint32_t p = 0; p < args.n_pieces; ++p) nblocks += args.piece_kb[p];
     const uint32_t steps = (nblocks + 1) / 2;
@@ -698,9 +700,9 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
     args.split_steps = per;
   }
   const bool defer = small && (args.n_ops > 0 || args.q_out != nullptr || args.splits > 1);
-  if (!defer) return fp4 ? LaunchLinearFastFp4(args, batch, stream) : LaunchTiles<true>(args, batch, stream);
+  if (!defer) return fastk ? LaunchLinearFast(args, batch, stream) : LaunchTiles<true>(args, batch, stream);
 
-  const size_t bytes = (size_t)args.splits * args.quads * 4 * args.n * sizeof(float);
+  const size_t bytes = WorkspaceBytes(args);
   if (ws.bytes < bytes) {
     hipError_t err = hipStreamSynchronize(stream);  // the old buffer may be in use
     if (err != hipSuccess) return err;
@@ -712,7 +714,7 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
     ws.bytes = bytes;
   }
   args.ws = ws.ptr;
-  const hipError_t err = fp4 ? LaunchLinearFastFp4(args, args.splits, stream)  // z = split
+  const hipError_t err = fastk ? LaunchLinearFast(args, args.splits, stream)  // z = split
                              : LaunchTiles<true>(args, 1, stream);
   if (err != hipSuccess) return err;
   return LaunchEpilogue(args, stream);

@@ -56,10 +56,23 @@ struct GemmArgs {
   // kernels write their raw fold results, rows [0, 4*quads), row-major
   // [split][4*quads][n], and EpilogueKernel finishes (sum over splits, -0,
   // ops, C, requantize).  K splits (fast mode): split s covers the steps
-  // [s * split_steps, (s + 1) * split_steps).
+  // [s * split_steps, (s + 1) * split_steps).  With splits > 1 the kernels
+  // also write one flag per (split, tile), after the sums, [split][gy][gx]
+  // (tiles of tile_rows x 256): set when the split's scale bytes leave the
+  // fast path's window, and the epilogue then recomputes the tile's
+  // outputs exactly.
   float* ws;
-  uint32_t splits, split_steps;
+  uint32_t splits, split_steps, tile_rows;
 };
+
+// Byte size of the deferred-epilogue workspace of `args` (sums and flags).
+inline size_t WorkspaceBytes(const GemmArgs& args) {
+  const size_t sums = (size_t)args.splits * args.quads * 4 * args.n * sizeof(float);
+  return sums + (args.splits > 1 ? (size_t)args.splits * args.gx * args.gy * sizeof(uint32_t) : 0);
+}
+__device__ __forceinline__ uint32_t* SplitFlags(const GemmArgs& g) {
+  return reinterpret_cast<uint32_t*>(g.ws + (size_t)g.splits * g.quads * 4 * g.n);
+}
 
 // Device scratch owned by a context, grown on demand.
 struct Workspace {
@@ -95,10 +108,13 @@ hipError_t LaunchGemmInstrAliased(const GemmArgs& args, hipStream_t stream);
 // which case it may grow `ws` (synchronizing the stream first).
 hipError_t LaunchLinear(const GemmArgs& args, uint32_t batch, bool fast, Workspace& ws,
                         hipStream_t stream);
-// Fast MXFP4 path (hb_fast.hip): one FP4 plane, block-scaled f8f6f4 MFMA.
-// Tile grid of the fast kernel for `args` (column tiles, row tiles).
-void FastFp4Grid(const GemmArgs& args, uint32_t* gx, uint32_t* gy);
-hipError_t LaunchLinearFastFp4(const GemmArgs& args, uint32_t batch, hipStream_t stream);
+// Fast path (hb_fast.hip): block-scaled f8f6f4 MFMA for one FP4 plane or
+// the W8 planes (hi, lo), in that order.
+bool FastEligible(const GemmArgs& args);
+// Tile grid of the fast kernel for `args`: column tiles, row tiles, rows per
+// tile.
+void FastGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy, uint32_t* tile_rows);
+hipError_t LaunchLinearFast(const GemmArgs& args, uint32_t batch, hipStream_t stream);
 // Exact tile kernel grid for a linear layer (column tiles, row tiles).
 void ExactGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy);
 // Deferred epilogue (hb_vec.hip): reads args.ws, writes C and q_out.

@@ -134,6 +134,15 @@ __global__ __launch_bounds__(256) void EpilogueKernel(GemmArgs g) {
       y = __float_as_uint(__uint_as_float(y) + g.ws[s * plane + at]);
     if ((y << 1) == 0) y = 0;
   }
+  if (g.splits > 1 && in) {  // a split out of the fast window: the tile is exact
+    const uint32_t* flags = SplitFlags(g);
+    const uint32_t tile = (row / g.tile_rows) * g.gx + col / 256;  // fast tiles: 256 columns
+    uint32_t any = 0;
+    for (uint32_t s = 0; s < g.splits; ++s) any |= flags[s * g.gx * g.gy + tile];
+    if (any) {
+      y = SlowLinear(g, g.a, g.w[0], g.w[1], (g.acc && row < g.m) ? g.c[at] : 0u, row, col);
+    }
+  }
   for (uint32_t o = 0; o < g.n_ops; ++o) {
     const uint32_t kind = g.op_kind[o];
     const uint32_t x2 = (kind == kEpAdd || kind == kEpActMul) && in && row < g.m

@@ -146,10 +146,13 @@ def block_abs_sums(m, n, kb, a, planes, modes):
     return tot[:m]
 
 
-@pytest.mark.parametrize("m,w8", [(128, False), (1024, False), (64, True), (2048, True)])
-def test_fast_mode_tolerance(gpu, m, w8):
-    rng = np.random.default_rng(10 + m)
-    n, k = (960, 2560) if not w8 else (768, 768)
+@pytest.mark.parametrize("m,w8,n,k", [(128, False, 960, 2560), (1024, False, 960, 2560),
+                                      (64, True, 768, 768), (2048, True, 768, 768),
+                                      (64, True, 2560, 960), (200, True, 2304, 768)])
+def test_fast_mode_tolerance(gpu, m, w8, n, k):
+    """MXFP4 at the K=2560 N=960 workload, W8 at the W8 workload (M=64 K=960
+    N=2560) and at SigLIP-style shapes."""
+    rng = np.random.default_rng(10 + m + n)
     kb, a, planes, modes = make_layer(rng, m, n, k, w8)
     got, _ = run_linear(gpu, m, n, kb, a, planes, modes, mode=hb.FAST)
     want, _ = oracle_linear(m, n, kb, a, planes, modes)
@@ -161,13 +164,14 @@ def test_fast_mode_tolerance(gpu, m, w8):
         assert (err <= 2.0 ** -20 * block_abs_sums(m, n, kb, a, planes, modes) + 1e-30).all()
 
 
-@pytest.mark.parametrize("m", [1, 50, 128])
-def test_fast_split_layer_with_epilogue(gpu, m):
+@pytest.mark.parametrize("m,w8", [(1, False), (50, False), (128, False), (1, True), (50, True),
+                                  (128, True)])
+def test_fast_split_layer_with_epilogue(gpu, m, w8):
     """A single small fast-mode layer takes the K-split path with the
     element-parallel epilogue: pieces, onto, MULP and ADDP, requantize."""
-    rng = np.random.default_rng(70 + m)
+    rng = np.random.default_rng(70 + m + 1000 * w8)
     n, k = 320, 1280
-    kb, a, planes, modes = make_layer(rng, m, n, k, False)
+    kb, a, planes, modes = make_layer(rng, m, n, k, w8)
     onto = helpers.random_fp32_words(rng, (m, n), 120, 130)
     scale = helpers.random_fp32_words(rng, (n,), 117, 122)
     bias = helpers.random_fp32_words(rng, (n,), 118, 124)
@@ -263,7 +267,7 @@ def test_batched_layers(gpu):
 
 
 @pytest.mark.parametrize("w8,mode,quantize", [(True, hb.EXACT, False), (False, hb.EXACT, True),
-                                              (False, hb.FAST, False)])
+                                              (False, hb.FAST, False), (True, hb.FAST, True)])
 def test_batched_layers_with_epilogue(gpu, w8, mode, quantize):
     """Per-layer MULP scale and ADDP bias vectors at a uniform stride, as in
     the W8 workload (per-channel scale and bias), batched into one launch."""
@@ -301,6 +305,55 @@ def test_batched_layers_with_epilogue(gpu, w8, mode, quantize):
             w = want.view(np.float32).astype(np.float64)
             row_scale = np.abs(w).max(axis=1, keepdims=True)
             assert (np.abs(g - w) <= 1e-5 * row_scale).all()
+            if quantize:
+                gqb = gq[i].reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
+                wqb = wq.reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
+                assert np.abs(gqb - wqb).max() <= 1 and (gqb != wqb).mean() < 0.01
+
+
+@pytest.mark.parametrize("w8", [False, True])
+def test_fast_batched_pieces_and_onto(gpu, w8):
+    """Fast mode over a piece list (the multi-piece kernel), starting from C,
+    with rows and columns that leave partial tiles, batched."""
+    rng = np.random.default_rng(63 + w8)
+    layers, m, n, k = 3, 160, 320, 640
+    data = [make_layer(rng, m, n, k, w8) for _ in range(layers)]
+    kb, modes = data[0][0], data[0][3]
+    pieces = [(12, 8), (0, 5), (5, 7)]
+    onto = np.stack([helpers.random_fp32_words(rng, (m, n), 120, 130) for _ in range(layers)])
+    a_all = dev(np.stack([d[1] for d in data]))
+    w_all = [dev(np.stack([d[2][p] for d in data])) for p in range(len(modes))]
+    c_all = dev(onto.view(np.float32))
+    descs = [hb.linear_desc(m, n, kb, a_all[i], [w[i] for w in w_all], modes, c_all[i],
+                            pieces=pieces, onto=True, mode=hb.FAST) for i in range(layers)]
+    torch.cuda.synchronize()
+    say("fast batched pieces onto", dict(layers=layers, w8=w8))
+    hb.linear_batched(descs, gpu)
+    got = host(c_all).view(np.uint32)
+    for i, d in enumerate(data):
+        want, _ = oracle_linear(m, n, kb, d[1], d[2], d[3], pieces=pieces, onto=onto[i])
+        g = got[i].view(np.float32).astype(np.float64)
+        w = want.view(np.float32).astype(np.float64)
+        row_scale = np.abs(w).max(axis=1, keepdims=True)
+        assert (np.abs(g - w) <= 1e-5 * row_scale).all(), float((np.abs(g - w) / row_scale).max())
+
+
+@pytest.mark.parametrize("w8", [False, True])
+def test_fast_out_of_window_scales_recompute_exactly(gpu, w8):
+    """Row tiles whose scale bytes leave the fast path's window recompute
+    with the NPU's ordered fold, bit for bit; the other tiles stay within
+    the fast-mode tolerance."""
+    rng = np.random.default_rng(64 + w8)
+    m, n, k = 256, 512, 384
+    kb, a, planes, modes = make_layer(rng, m, n, k, w8)
+    a = a.copy()
+    a.reshape(m // 4, kb, 144)[:32, 3, 128] = 60   # rows 0..127: an out-of-window scale byte
+    got, _ = run_linear(gpu, m, n, kb, a, planes, modes, mode=hb.FAST)
+    want, _ = oracle_linear(m, n, kb, a, planes, modes)
+    assert_bits(got[:128], want[:128])
+    g, w = got[128:].view(np.float32).astype(np.float64), want[128:].view(np.float32).astype(np.float64)
+    row_scale = np.abs(w).max(axis=1, keepdims=True)
+    assert (np.abs(g - w) <= 1e-5 * row_scale).all()
 
 
 def test_batched_rejects_mismatched_layers(gpu):

@@ -10,7 +10,9 @@ launch; inputs are resident in HBM before timing starts.
 
 Extra fields (skipped with --quick): the same workload in exact mode (bitwise
 equal to the NPU), the M sweep {1, 16, 1024} in fast mode, the W8 layer
-M=64 K=960 N=2560 with per-channel scale (MULP) and bias (ADDP), and the
+M=64 K=960 N=2560 with per-channel scale (MULP) and bias (ADDP), the
+SigLIP-style W8 encoder set (M=2048), the SparseDrive-S stage-1 3x3 conv
+GEMM (MXFP4, M=67584 K=576 N=64), each in fast and exact mode, and the
 SmolVLA action-expert step (its GEMM chain) at batch 1 and 32.
 
     python bench.py [--steps K] [--warmup W] [--mode exact|fast] [--layers L]
@@ -176,7 +178,73 @@ def activation_table(kind="silu"):
     return out
 
 
-class ExpertStep:
+class Chain:
+    """A sequence of linear layers on synthetic device data, one descriptor
+    per layer, run in order on one stream.  MXINT8 activation words carry
+    random codes with scale bytes 122..127; MXFP4 weight words random codes
+    with E8M0 exponents in [lo, hi]; W8 weights are two nibble planes of
+    random codes sharing the scale byte 133 (MXINT8 of int8 values)."""
+
+    def __init__(self, hb, torch, m, mode, seed):
+        self.hb, self.torch, self.m, self.mode = hb, torch, m, mode
+        self.dev = "cuda:0"
+        self.g = torch.Generator(device=self.dev).manual_seed(seed)
+        self.quads = (m + 3) // 4
+        self.descs, self.keep, self.ops, self.bytes = [], [], 0.0, 0.0
+
+    def a_words(self, kb):
+        t = self.torch.randint(0, 256, (self.quads * kb, 144), generator=self.g, device=self.dev,
+                               dtype=self.torch.uint8)
+        t[:, 128:132] = self.torch.randint(122, 128, (self.quads * kb, 4), generator=self.g,
+                                           device=self.dev, dtype=self.torch.uint8)
+        t[:, 132:] = 0
+        self.keep.append(t)
+        return t
+
+    def w_words(self, n, kb, lo=-10, hi=-2):
+        t = self.torch.randint(0, 256, (n // 8 * kb, 144), generator=self.g, device=self.dev,
+                               dtype=self.torch.uint8)
+        t[:, 128:136] = self.torch.randint(127 + lo, 127 + hi + 1, (n // 8 * kb, 8),
+                                           generator=self.g, device=self.dev,
+                                           dtype=self.torch.uint8)
+        t[:, 136:] = 0
+        self.keep.append(t)
+        return t
+
+    def w8(self, n, kb):
+        return [self.w_words(n, kb, 6, 6), self.w_words(n, kb, 6, 6)]
+
+    def f32(self, n, scale=1.0):
+        t = self.torch.randn((self.m, n), generator=self.g, device=self.dev) * scale
+        self.keep.append(t)
+        return t
+
+    def vec(self, n, scale, offset=0.0):
+        t = self.torch.randn((n,), generator=self.g, device=self.dev) * scale + offset
+        self.keep.append(t)
+        return t
+
+    def table(self, kind):
+        tb = self.torch.from_numpy(activation_table(kind).view(np.int64)).to(self.dev)
+        self.keep.append(tb)
+        return tb
+
+    def add(self, n, kb, a, planes, c, ops=(), q=None, onto=False, tbuf=None):
+        modes = [1, 2] if len(planes) == 2 else [0]
+        self.descs.append(self.hb.linear_desc(self.m, n, kb, a, planes, modes, c, ops=ops,
+                                              tbuf=tbuf, q_out=q, onto=onto, mode=self.mode))
+        self.ops += 2.0 * self.m * n * kb * 32
+        vectors = sum(1 for k, _ in ops if k in (self.hb.EP_ADDP, self.hb.EP_MULP))
+        out = self.m * n * (1 + 1 / 32) if q is not None else 4 * self.m * n
+        self.bytes += layer_bytes(self.m, n, kb, 8 if len(planes) == 2 else 4, vectors) - \
+            4 * self.m * n + out + (4 * self.m * n if onto else 0)
+
+    def run(self, ctx):
+        for d in self.descs:
+            self.hb.launch(d, ctx)
+
+
+class ExpertStep(Chain):
     """One SmolVLA action-expert step as the GEMM chain the reference compiler
     emits for it (tools/compiler/smolvla_expert.cpp:250-420, 430-545): 16
     layers of width 720 (K 736), 15 query / 5 KV heads of 64, SiLU-gated MLP
@@ -193,90 +261,86 @@ class ExpertStep:
     WIDTH, KB, Q, KV, HID, KBQ, KBH, LAYERS, CHUNK, ACT = 720, 23, 960, 320, 2048, 30, 64, 16, 50, 32
 
     def __init__(self, hb, torch, batch, mode):
-        self.hb, self.torch = hb, torch
-        dev = "cuda:0"
-        g = torch.Generator(device=dev).manual_seed(11 + batch)
-        m = self.CHUNK * batch
-        quads = (m + 3) // 4
-        self.m, self.ops = m, 0.0
-        keep = []
-
-        def a_words(kb):  # MXINT8 activations [quads][kb] words, scales 122..127
-            t = torch.randint(0, 256, (quads * kb, 144), generator=g, device=dev, dtype=torch.uint8)
-            t[:, 128:132] = torch.randint(122, 128, (quads * kb, 4), generator=g, device=dev,
-                                          dtype=torch.uint8)
-            t[:, 132:] = 0
-            keep.append(t)
-            return t
-
-        def w_words(n, kb, lo=-10, hi=-2):  # MXFP4 / W8-plane words [n/8][kb]
-            t = torch.randint(0, 256, (n // 8 * kb, 144), generator=g, device=dev, dtype=torch.uint8)
-            t[:, 128:136] = torch.randint(127 + lo, 127 + hi + 1, (n // 8 * kb, 8), generator=g,
-                                          device=dev, dtype=torch.uint8)
-            t[:, 136:] = 0
-            keep.append(t)
-            return t
-
-        def f32(n, scale=1.0):
-            t = torch.randn((m, n), generator=g, device=dev) * scale
-            keep.append(t)
-            return t
-
-        def vec(n, scale):
-            t = torch.randn((n,), generator=g, device=dev) * scale
-            keep.append(t)
-            return t
-
-        tb = torch.from_numpy(activation_table("silu").view(np.int64)).to(dev)
-        keep.append(tb)
-        descs = []
-
-        def add(n, kb, a, planes, c, ops=(), q=None, onto=False):
-            modes = [1, 2] if len(planes) == 2 else [0]
-            md = hb.EXACT if len(planes) == 2 else mode
-            descs.append(hb.linear_desc(m, n, kb, a, planes, modes, c, ops=ops, tbuf=tb, q_out=q,
-                                        onto=onto, mode=md))
-            self.ops += 2.0 * m * n * kb * 32
-
-        x = [f32(self.WIDTH) for _ in range(3)]
+        super().__init__(hb, torch, self.CHUNK * batch, mode, 11 + batch)
+        tb = self.table("silu")
+        x = [self.f32(self.WIDTH) for _ in range(3)]
         for layer in range(self.LAYERS):
-            a1, ao, a2 = a_words(self.KB), a_words(self.KBQ), a_words(self.KB)
+            a1, ao, a2 = self.a_words(self.KB), self.a_words(self.KBQ), self.a_words(self.KB)
             heads = [("q", self.Q)] + ([("k", self.KV), ("v", self.KV)] if layer % 2 == 0 else [])
             for _, n in heads:
-                add(n, self.KB, a1, [w_words(n, self.KB)], f32(n), q=a_words(n // 32))
-            add(self.WIDTH, self.KBQ, ao, [w_words(self.WIDTH, self.KBQ)], x[1],
-                ops=[(hb.EP_ADD, x[0])])
-            up = f32(self.HID)
-            add(self.HID, self.KB, a2, [w_words(self.HID, self.KB)], up)
-            h = a_words(self.KBH)
-            add(self.HID, self.KB, a2, [w_words(self.HID, self.KB)], f32(self.HID),
-                ops=[(hb.EP_ACT_MUL, up)], q=h)
-            add(self.WIDTH, self.KBH, h, [w_words(self.WIDTH, self.KBH)], x[2],
-                ops=[(hb.EP_ADD, x[1])])
-        w8 = lambda n, kb: [w_words(n, kb, 6, 6), w_words(n, kb, 6, 6)]  # MXINT8 weights, e = 6
-        act, tim, hid, xin = a_words(1), a_words(self.KB), a_words(self.KB), a_words(self.KB)
+                self.add(n, self.KB, a1, [self.w_words(n, self.KB)], self.f32(n),
+                         q=self.a_words(n // 32))
+            self.add(self.WIDTH, self.KBQ, ao, [self.w_words(self.WIDTH, self.KBQ)], x[1],
+                     ops=[(hb.EP_ADD, x[0])])
+            up = self.f32(self.HID)
+            self.add(self.HID, self.KB, a2, [self.w_words(self.HID, self.KB)], up)
+            h = self.a_words(self.KBH)
+            self.add(self.HID, self.KB, a2, [self.w_words(self.HID, self.KB)], self.f32(self.HID),
+                     ops=[(hb.EP_ACT_MUL, up)], q=h, tbuf=tb)
+            self.add(self.WIDTH, self.KBH, h, [self.w_words(self.WIDTH, self.KBH)], x[2],
+                     ops=[(hb.EP_ADD, x[1])])
+        act, tim, hid, xin = self.a_words(1), self.a_words(self.KB), self.a_words(self.KB), \
+            self.a_words(self.KB)
         pad = self.KB * 32
-        add(pad, 1, act, w8(pad, 1), f32(pad), ops=[(hb.EP_ADDP, vec(pad, 0.1))], q=xin)
-        mlp_in = f32(pad)
-        add(pad, self.KB, xin, w8(pad, self.KB), mlp_in)
-        add(pad, self.KB, tim, w8(pad, self.KB), mlp_in, onto=True,
-            ops=[(hb.EP_ADDP, vec(pad, 0.1)), (hb.EP_ACT, None)], q=hid)
-        add(self.WIDTH, self.KB, hid, w8(self.WIDTH, self.KB), x[0],
-            ops=[(hb.EP_ADDP, vec(self.WIDTH, 0.1))])
-        add(self.ACT, self.KB, hid, w8(self.ACT, self.KB), f32(self.ACT),
-            ops=[(hb.EP_ADDP, vec(self.ACT, 0.1))])
-        self.descs, self.keep = descs, keep
+        self.add(pad, 1, act, self.w8(pad, 1), self.f32(pad), ops=[(hb.EP_ADDP, self.vec(pad, 0.1))],
+                 q=xin)
+        mlp_in = self.f32(pad)
+        self.add(pad, self.KB, xin, self.w8(pad, self.KB), mlp_in)
+        self.add(pad, self.KB, tim, self.w8(pad, self.KB), mlp_in, onto=True,
+                 ops=[(hb.EP_ADDP, self.vec(pad, 0.1)), (hb.EP_ACT, None)], q=hid, tbuf=tb)
+        self.add(self.WIDTH, self.KB, hid, self.w8(self.WIDTH, self.KB), x[0],
+                 ops=[(hb.EP_ADDP, self.vec(self.WIDTH, 0.1))])
+        self.add(self.ACT, self.KB, hid, self.w8(self.ACT, self.KB), self.f32(self.ACT),
+                 ops=[(hb.EP_ADDP, self.vec(self.ACT, 0.1))])
         torch.cuda.synchronize()
 
-    def run(self, ctx):
-        for d in self.descs:
-            self.hb.launch(d, ctx)
+
+class SiglipSet(Chain):
+    """SigLIP-style vision-encoder GEMM set, W8: per layer, on M = 2 cameras x
+    1024 patch tokens = 2048 rows with hidden 768, QKV 768->2304, out-proj
+    768->768, MLP up 768->3072 with GELU and MXINT8 requantize, MLP down
+    3072->768; per-channel scale (MULP) and bias (ADDP) on every GEMM; 12
+    layers of distinct random weights."""
+
+    M, D, QKV, FF, LAYERS = 2048, 768, 2304, 3072, 12
+
+    def __init__(self, hb, torch, mode):
+        super().__init__(hb, torch, self.M, mode, 21)
+        tb = self.table("gelu")
+        kb, kbf = self.D // 32, self.FF // 32
+
+        def ep(n):
+            return [(hb.EP_MULP, self.vec(n, 0.005, 0.0105)), (hb.EP_ADDP, self.vec(n, 0.1))]
+
+        for _ in range(self.LAYERS):
+            x = self.a_words(kb)
+            self.add(self.QKV, kb, x, self.w8(self.QKV, kb), self.f32(self.QKV), ops=ep(self.QKV))
+            self.add(self.D, kb, self.a_words(kb), self.w8(self.D, kb), self.f32(self.D),
+                     ops=ep(self.D))
+            h = self.a_words(kbf)
+            self.add(self.FF, kb, self.a_words(kb), self.w8(self.FF, kb), self.f32(self.FF),
+                     ops=ep(self.FF) + [(hb.EP_ACT, None)], q=h, tbuf=tb)
+            self.add(self.D, kbf, h, self.w8(self.D, kbf), self.f32(self.D), ops=ep(self.D))
+        torch.cuda.synchronize()
 
 
-def time_expert_step(hb, torch, ctx, batch, mode, steps=10):
-    """Milliseconds per expert step: eager launches on one stream, and the
-    same chain replayed as one captured HIP graph."""
-    work = ExpertStep(hb, torch, batch, mode)
+class SparseDriveConv(Chain):
+    """SparseDrive-S backbone stage-1 3x3 convolution as its im2col GEMM:
+    6 cameras x 64 x 176 output positions = 67,584 rows, K = 3*3*64 = 576,
+    N = 64, MXFP4 weights (E8M0 exponents -10..-2), fp32 output."""
+
+    M, K, N = 6 * 64 * 176, 576, 64
+
+    def __init__(self, hb, torch, mode):
+        super().__init__(hb, torch, self.M, mode, 31)
+        kb = self.K // 32
+        self.add(self.N, kb, self.a_words(kb), [self.w_words(self.N, kb)], self.f32(self.N))
+        torch.cuda.synchronize()
+
+
+def time_chain(torch, ctx, work, steps=10, graph=True):
+    """Milliseconds per pass over the chain: eager launches on one stream,
+    and (graph=True) the same chain replayed as one captured HIP graph."""
     stream = torch.cuda.current_stream()
     ctx.set_stream(stream.cuda_stream)
     for _ in range(2):
@@ -289,32 +353,54 @@ def time_expert_step(hb, torch, ctx, batch, mode, steps=10):
     t1.record(stream)
     torch.cuda.synchronize()
     eager = t0.elapsed_time(t1) / steps
-    out = {"batch": batch, "m": work.m, "gemms": len(work.descs), "gops": round(work.ops / 1e9, 3),
+    out = {"m": work.m, "gemms": len(work.descs), "gops": round(work.ops / 1e9, 3),
            "eager_ms": round(eager, 4)}
-    try:
-        side = torch.cuda.Stream()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(side):
-            ctx.set_stream(side.cuda_stream)
-            work.run(ctx)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=side):
-            ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-            work.run(ctx)
-        ctx.set_stream(stream.cuda_stream)
-        graph.replay()
-        torch.cuda.synchronize()
-        t0.record(stream)
-        for _ in range(steps):
-            graph.replay()
-        t1.record(stream)
-        torch.cuda.synchronize()
-        out["graph_ms"] = round(t0.elapsed_time(t1) / steps, 4)
-    except Exception as e:  # capture is optional for the measurement
-        ctx.set_stream(stream.cuda_stream)
-        out["graph_error"] = str(e)[:200]
+    if graph:
+        try:
+            side = torch.cuda.Stream()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side):
+                ctx.set_stream(side.cuda_stream)
+                work.run(ctx)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=side):
+                ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+                work.run(ctx)
+            ctx.set_stream(stream.cuda_stream)
+            g.replay()
+            torch.cuda.synchronize()
+            t0.record(stream)
+            for _ in range(steps):
+                g.replay()
+            t1.record(stream)
+            torch.cuda.synchronize()
+            out["graph_ms"] = round(t0.elapsed_time(t1) / steps, 4)
+        except Exception as e:  # capture is optional for the measurement
+            ctx.set_stream(stream.cuda_stream)
+            out["graph_error"] = str(e)[:200]
+    return out
+
+
+def time_expert_step(hb, torch, ctx, batch, mode, steps=10):
+    """Milliseconds per SmolVLA action-expert step (eager and graph)."""
+    work = ExpertStep(hb, torch, batch, mode)
+    out = {"batch": batch, **time_chain(torch, ctx, work, steps)}
     del work
     return out
+
+
+def chain_summary(work, ms, mfma_class):
+    """TOPS and roofline of one pass over a chain taking `ms`."""
+    tops = work.ops / (ms * 1e-3) / 1e12
+    gbs = work.bytes / (ms * 1e-3) / 1e9
+    peak = MFMA_PEAK[mfma_class]
+    if work.ops / work.bytes * HBM_PEAK_GBS / 1e3 < peak:
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(tops, 1), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(tops / peak, 4), "mfma_class": mfma_class}
+    return round(tops, 3), roof
 
 
 def time_steps(hb, torch, ctx, stream, work, steps, warmup):
@@ -434,15 +520,38 @@ def main():
         sweep["M=128"] = {"value": out["value"], "unit": "TOPS", "layers": args.layers,
                           "ms_per_step": out["ms_per_step"], "roofline": roof}
         out["mxfp4_fast_m_sweep"] = sweep
-        # W8 layer with per-channel scale and bias (exact)
+        # W8 layer with per-channel scale and bias, fast and exact
         L8 = 128
-        w8 = Workload(hb, torch, 64, 2560, 30, True, L8, hb.EXACT, epilogue=True, seed=4)
-        ms8 = time_steps(hb, torch, ctx, stream, w8, extra_steps, extra_warm)
-        t8, r8 = summarize(w8, ms8, "bf16")
-        out["w8_exact"] = {"workload": f"W8 linear M=64 K=960 N=2560 + MULP + ADDP, {L8} layers "
-                                       "per step", "value": round(t8, 3), "unit": "TOPS",
-                           "ms_per_step": round(ms8, 4), "roofline": r8}
-        del w8
+        w8 = {"workload": f"W8 linear M=64 K=960 N=2560 + MULP + ADDP, {L8} layers per step"}
+        for name, md, cls in (("fast", hb.FAST, "int8"), ("exact", hb.EXACT, "bf16")):
+            wk = Workload(hb, torch, 64, 2560, 30, True, L8, md, epilogue=True, seed=4)
+            ms8 = time_steps(hb, torch, ctx, stream, wk, extra_steps, extra_warm)
+            t8, r8 = summarize(wk, ms8, cls)
+            w8[name] = {"value": round(t8, 3), "unit": "TOPS", "ms_per_step": round(ms8, 4),
+                        "roofline": r8}
+            del wk
+        out["w8"] = w8
+
+        # SigLIP-style W8 encoder set (12 layers x 4 GEMMs, M=2048) and the
+        # SparseDrive-S stage-1 3x3 im2col GEMM (MXFP4), fast and exact
+        for key, desc, cls_fast, make in (
+                ("siglip_w8_set", "W8 SigLIP-style encoder: 12 layers x {QKV 768->2304, out "
+                 "768->768, up 768->3072 + GELU + requantize, down 3072->768}, M=2048, "
+                 "MULP + ADDP", "int8", lambda md: SiglipSet(hb, torch, md)),
+                ("sparsedrive_stage1_conv_mxfp4", "MXFP4 im2col GEMM M=67584 K=576 N=64 "
+                 "(SparseDrive-S stage-1 3x3 conv, 6 cameras)", "fp6_fp4",
+                 lambda md: SparseDriveConv(hb, torch, md))):
+            rec = {}
+            for name, md, cls in (("fast", hb.FAST, cls_fast), ("exact", hb.EXACT, "bf16")):
+                wk = make(md)
+                t = time_chain(torch, ctx, wk, steps=5, graph=False)
+                tops, roof = chain_summary(wk, t["eager_ms"], cls)
+                rec[name] = {"value": tops, "unit": "TOPS", "ms_per_pass": t["eager_ms"],
+                             "gemms": t["gemms"], "m": t["m"], "roofline": roof}
+                del wk
+            rec["workload"] = desc
+            out[key] = rec
+        ctx.set_stream(stream.cuda_stream)
 
         # SmolVLA action-expert step (GEMM chain), B = 1 and 32
         out["smolvla_expert_step_ms"] = {f"B={b}": time_expert_step(hb, torch, ctx, b, mode)

@@ -360,6 +360,88 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
   const uint32_t s0 = split * g.split_steps;  // every split has at least one step
   const uint32_t steps = g.splits > 1 ? min(all_steps - s0, g.split_steps) : all_steps;
 
+  // The epilogue runs from LDS on all 16 waves: the kMT*2 consumer waves'
+  // outputs are at lds.out[cw][e][lane], element e = 16 j + r of MFMA tile j
+  // (row tile j / kTN, column tile j % kTN of wave cw), register r.  Waves
+  // take whole tiles (e0, e1 multiples of 16), so a row's 32 columns of a
+  // tile are the 32 lanes of one half-wave for the requantize.
+  auto epilogue = [&](uint32_t cw, uint32_t l, uint32_t e0, uint32_t e1, bool slow) {
+    const uint32_t cwm = cw % kWavesM, cwn = cw / kWavesM;
+    float* vals = lds.out[cw];
+    auto row_at = [&](uint32_t e) {
+      const uint32_t j = e / 16, r = e % 16;
+      return row0 + (cwm * kTM + j / kTN) * 32 + 4 * (l >> 5) + 8 * (r / 4) + (r & 3);
+    };
+    auto col_at = [&](uint32_t e) { return col0 + (cwn * kTN + (e / 16) % kTN) * 32 + (l & 31); };
+    if (g.splits <= 1 && slow) {
+      for (uint32_t e = e0; e < e1; ++e) {
+        const uint32_t row = row_at(e), col = col_at(e);
+        if ((row >> 2) >= g.quads || col >= g.n) continue;
+        const uint32_t init = (g.acc && row < g.m) ? c[(size_t)row * g.n + col] : 0u;
+        vals[e * 64 + l] = __uint_as_float(SlowLinear(g, a, w0, w1, init, row, col));
+      }
+    }
+    if (g.ws != nullptr) {  // deferred epilogue: this split's sums, rows [0, 4*quads)
+      float* out = g.ws + (size_t)split * g.quads * 4 * g.n;
+      for (uint32_t e = e0; e < e1; ++e) {
+        const uint32_t row = row_at(e), col = col_at(e);
+        if ((row >> 2) < g.quads && col < g.n) out[(size_t)row * g.n + col] = vals[e * 64 + l];
+      }
+      return;
+    }
+    // Epilogue ops (FP32 hardware arithmetic), op by op, one MFMA tile at a
+    // time: the tile's operands are loaded first, all at once (independent
+    // loads, one wait); the element loop then only computes.
+    for (uint32_t o = 0; o < g.n_ops; ++o) {
+      const uint32_t kind = g.op_kind[o], imm = g.op_imm[o];
+      const bool has_x2 = kind == kEpAdd || kind == kEpActMul;
+      const bool has_vec = kind == kEpAddP || kind == kEpMulP;
+      const uint32_t* x2 = g.op_x2[o] + z * g.op_x2_batch[o];
+      const uint32_t* v = g.op_vec[o] + z * g.op_vec_batch[o];
+      for (uint32_t t0 = e0; t0 < e1; t0 += 16) {
+        const uint32_t col = col_at(t0);
+        f32x16 xv;  // a register vector: the runtime index below is wave-uniform
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t row = row_at(t0 + r);
+          xv[r] = __uint_as_float(has_x2 && row < g.m && col < g.n ? x2[(size_t)row * g.n + col]
+                                                                   : 0u);
+        }
+        const float pv = __uint_as_float(has_vec && col < g.n ? v[col] : 0u);
+#pragma unroll 1
+        for (uint32_t r = 0; r < 16; ++r) {
+          const uint32_t row = row_at(t0 + r);
+          float& y = vals[(t0 + r) * 64 + l];
+          if ((row >> 2) < g.quads && col < g.n)
+            y = EpApplyFast(kind, imm, y, xv[r], pv, lds_act);
+        }
+      }
+    }
+    for (uint32_t e = e0; e < e1; ++e) {
+      const uint32_t row = row_at(e), col = col_at(e);
+      if (row < g.m && col < g.n) c[(size_t)row * g.n + col] = __float_as_uint(vals[e * 64 + l]);
+    }
+    if (q_out != nullptr) {  // MXINT8 requantize over the 32 lanes holding a row's block
+      const uint32_t nb = g.n >> 5;
+      for (uint32_t e = e0; e < e1; ++e) {
+        const uint32_t y = __float_as_uint(vals[e * 64 + l]);
+        const uint32_t row = row_at(e), blk = (col_at(e) - (l & 31)) >> 5;
+        uint32_t x = ExpField(y);
+        x = max(x, (uint32_t)__shfl_xor((int)x, 1));
+        x = max(x, (uint32_t)__shfl_xor((int)x, 2));
+        x = max(x, (uint32_t)__shfl_xor((int)x, 4));
+        x = max(x, (uint32_t)__shfl_xor((int)x, 8));
+        x = max(x, (uint32_t)__shfl_xor((int)x, 16));
+        if ((row >> 2) < g.quads && blk < nb) {
+          uint8_t* word = q_out + ((size_t)(row >> 2) * nb + blk) * kDdrWord;
+          word[(row & 3) * 32 + (l & 31)] = QuantizeElement(y, x);
+          if ((l & 31) == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(x);
+          if ((l & 31) < 12 && (row & 3) == 0) word[132 + (l & 31)] = 0;
+        }
+      }
+    }
+  };
+
   if (!consumer) {
     // Ring of kU raw register sets (slot t % kU holds step t): the set of
     // step s + 2 is converted in iteration s and its slot refilled with step
@@ -396,6 +478,9 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
     if (g.tbuf != nullptr)  // the producers are done: stage the activation table
       for (uint32_t i = t; i < 512; i += kP) lds_act[i] = g.tbuf[512 + i];
     __syncthreads();
+    __syncthreads();  // the consumers' outputs are in LDS
+    // producer wave v takes tiles 2 and 3 of consumer wave v
+    epilogue(t >> 6, t & 63, 32, 64, lds_unsafe != 0);
     return;
   }
 
@@ -525,96 +610,22 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
   }
   __syncthreads();  // producers' unsafe flags are in; the pipeline buffers are free
   const bool slow = lds_unsafe != 0;
-
   // Adding +0 maps -0 to +0 (and, in the kernel's flush-to-zero mode, a
-  // denormal sum to +0) in place.
+  // denormal sum to +0) in place; then the outputs go to LDS for the
+  // epilogue of all waves.
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = acc[j] + 0.0f;
-  // Requantize one value: a 32-column block is one MFMA tile (j); a row's 32
-  // values sit in the 32 lanes of one half-wave at one register r.
-  auto quantize = [&](uint32_t j, uint32_t r, uint32_t y) {
-    const uint32_t nb = g.n >> 5, blk = (col_of(j) - (lane & 31)) >> 5, row = row_of(j, r);
-    uint32_t e = ExpField(y);
-    e = max(e, (uint32_t)__shfl_xor((int)e, 1));
-    e = max(e, (uint32_t)__shfl_xor((int)e, 2));
-    e = max(e, (uint32_t)__shfl_xor((int)e, 4));
-    e = max(e, (uint32_t)__shfl_xor((int)e, 8));
-    e = max(e, (uint32_t)__shfl_xor((int)e, 16));
-    if ((row >> 2) < g.quads && blk < nb) {
-      uint8_t* word = q_out + ((size_t)(row >> 2) * nb + blk) * kDdrWord;
-      word[(row & 3) * 32 + (lane & 31)] = QuantizeElement(y, e);
-      if ((lane & 31) == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(e);
-      if ((lane & 31) < 12 && (row & 3) == 0) word[132 + (lane & 31)] = 0;
-    }
-  };
-
-  // The epilogue works on the wave's outputs in LDS (over the pipeline
-  // buffers), element e = 16 j + r at [e][lane], with runtime loops and no
-  // register arrays: the accumulators are dead from here on, so the
-  // epilogue's own registers never push them to scratch memory.
-  float* out_l = lds.out[wave];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) out_l[(j * 16 + r) * 64 + lane] = acc[j][r];
-  // Opaque to the optimizer: later reads come from LDS, not forwarded from
-  // the accumulators (which would keep them live).
-  asm volatile("" ::: "memory");
-  if (g.splits > 1) {
-    // A K split sees only its own blocks' scale bytes: it reports them, and
-    // the epilogue recomputes the tile exactly if any split of it is out of
-    // the window.
-    if (tid == 0) SplitFlags(g)[(split * g.gy + tile.y) * g.gx + tile.x] = slow ? 1u : 0u;
-  } else if (slow) {
-    for (uint32_t e = 0; e < 64; ++e) {
-      const uint32_t row = row_of(e / 16, e % 16), col = col_of(e / 16);
-      if ((row >> 2) >= g.quads || col >= g.n) continue;
-      const uint32_t init = (g.acc && row < g.m) ? c[(size_t)row * g.n + col] : 0u;
-      out_l[e * 64 + lane] = __uint_as_float(SlowLinear(g, a, w0, w1, init, row, col));
-    }
-  }
-  if (g.ws != nullptr) {  // deferred epilogue: this split's sums, rows [0, 4*quads)
-    float* out = g.ws + (size_t)split * g.quads * 4 * g.n;
-    for (uint32_t e = 0; e < 64; ++e) {
-      const uint32_t row = row_of(e / 16, e % 16), col = col_of(e / 16);
-      if ((row >> 2) < g.quads && col < g.n) out[(size_t)row * g.n + col] = out_l[e * 64 + lane];
-    }
-    return;
-  }
-  // Epilogue ops, op by op, one MFMA tile of the lane's outputs at a time:
-  // the tile's operands are loaded first, all at once (independent loads,
-  // one wait); the element loop then only computes.
-  for (uint32_t o = 0; o < g.n_ops; ++o) {
-    const uint32_t kind = g.op_kind[o], imm = g.op_imm[o];
-    const bool has_x2 = kind == kEpAdd || kind == kEpActMul;
-    const bool has_vec = kind == kEpAddP || kind == kEpMulP;
-    const uint32_t* x2 = g.op_x2[o] + z * g.op_x2_batch[o];
-    const uint32_t* v = g.op_vec[o] + z * g.op_vec_batch[o];
-    for (uint32_t j = 0; j < 4; ++j) {
-      const uint32_t col = col_of(j);
-      f32x16 xv;  // a register vector: the runtime index r below is wave-uniform
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint32_t row = row_of(j, r);
-        xv[r] = __uint_as_float(has_x2 && row < g.m && col < g.n ? x2[(size_t)row * g.n + col] : 0u);
-      }
-      const uint32_t pv = has_vec && col < g.n ? v[col] : 0u;
-#pragma unroll 1
-      for (uint32_t r = 0; r < 16; ++r) {
-        const uint32_t row = row_of(j, r);
-        float& y = out_l[(j * 16 + r) * 64 + lane];
-        if ((row >> 2) < g.quads && col < g.n)
-          y = __uint_as_float(EpApply(kind, imm, __float_as_uint(y), __float_as_uint(xv[r]), pv,
-                                      lds_act));
-      }
-    }
-  }
-  for (uint32_t e = 0; e < 64; ++e) {
-    const uint32_t row = row_of(e / 16, e % 16), col = col_of(e / 16);
-    if (row < g.m && col < g.n) c[(size_t)row * g.n + col] = __float_as_uint(out_l[e * 64 + lane]);
-  }
-  if (q_out != nullptr)
-    for (uint32_t e = 0; e < 64; ++e) quantize(e / 16, e % 16, __float_as_uint(out_l[e * 64 + lane]));
+    for (int r = 0; r < 16; ++r) lds.out[wave][(j * 16 + r) * 64 + lane] = acc[j][r];
+  // A K split sees only its own blocks' scale bytes: it reports them, and
+  // the deferred epilogue recomputes the tile exactly if any split of it is
+  // out of the window.
+  if (g.splits > 1 && tid == 0)
+    SplitFlags(g)[(split * g.gy + tile.y) * g.gx + tile.x] = slow ? 1u : 0u;
+  __syncthreads();  // the outputs are in LDS
+  epilogue(wave, lane, 0, 32, slow);  // tiles 0 and 1 of this wave
 }
 
 template <int kBM, bool kMulti, bool kW8>

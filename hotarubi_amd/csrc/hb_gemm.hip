@@ -689,11 +689,13 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   args.gx = gx;
   args.gy = gy;
   const bool small = batch == 1 && gx * gy < kSmallGrid;
+  args.fast_ep = fastk ? 1u : 0u;
   if (small && fastk) {
+    // as many splits as fit in one round of kTargetWorkgroups workgroups
     uint32_t nblocks = 0;
     for (uint32_t p = 0; p < args.n_pieces; ++p) nblocks += args.piece_kb[p];
     const uint32_t steps = (nblocks + 1) / 2;
-    const uint32_t want = (kTargetWorkgroups + gx * gy - 1) / (gx * gy);
+    const uint32_t want = kTargetWorkgroups / (gx * gy);
     uint32_t per = (steps + want - 1) / want;
     per = per < 2 ? 2 : per;
     args.splits = (steps + per - 1) / per;

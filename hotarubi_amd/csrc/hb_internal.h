@@ -63,6 +63,9 @@ struct GemmArgs {
   // outputs exactly.
   float* ws;
   uint32_t splits, split_steps, tile_rows;
+  // epilogue arithmetic of a fast-mode layer: FP32 hardware operations
+  // instead of the VEC lane formulas (EpApplyFast)
+  uint32_t fast_ep;
 };
 
 // Byte size of the deferred-epilogue workspace of `args` (sums and flags).

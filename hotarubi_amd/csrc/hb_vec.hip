@@ -148,7 +148,11 @@ __global__ __launch_bounds__(256) void EpilogueKernel(GemmArgs g) {
     const uint32_t x2 = (kind == kEpAdd || kind == kEpActMul) && in && row < g.m
                             ? g.op_x2[o][at] : 0u;
     const uint32_t p = (kind == kEpAddP || kind == kEpMulP) && in ? g.op_vec[o][col] : 0u;
-    if (in) y = EpApply(kind, g.op_imm[o], y, x2, p, g.tbuf + 512);
+    if (in)
+      y = g.fast_ep ? __float_as_uint(EpApplyFast(kind, g.op_imm[o], __uint_as_float(y),
+                                                  __uint_as_float(x2), __uint_as_float(p),
+                                                  g.tbuf + 512))
+                    : EpApply(kind, g.op_imm[o], y, x2, p, g.tbuf + 512);
   }
   if (in && row < g.m) g.c[at] = y;
   if (g.q_out != nullptr) {  // n % 32 == 0: a 32-lane half is all in or all out

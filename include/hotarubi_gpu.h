@@ -218,7 +218,12 @@ typedef struct hb_linear_desc {
   hb_ep_op ops[HB_MAX_EP_OPS];
   const uint64_t* tbuf;
   void* q_out;
-  uint32_t flags; /* HB_LINEAR_EXACT or HB_LINEAR_FAST */
+  /* HB_LINEAR_EXACT: bitwise the NPU's result.  HB_LINEAR_FAST: MXFP4 and
+   * W8 layers run on block-scaled matrix cores (exact products, FP32 sums
+   * in the hardware's order) and the ops use FP32 hardware arithmetic; per
+   * output row, max |fast - exact| <= 1e-5 * max |exact|.  Tiles whose
+   * scale bytes leave the fast path's range are computed exactly. */
+  uint32_t flags;
 } hb_linear_desc;
 
 /* A single small layer (fewer than 128 output tiles) may grow the context's

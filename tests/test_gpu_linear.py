@@ -192,6 +192,23 @@ def test_fast_split_layer_with_epilogue(gpu, m, w8):
         (gq.reshape(-1, 144)[:, 128:132] != wq.reshape(-1, 144)[:, 128:132]).mean() < 0.01
 
 
+@pytest.mark.parametrize("mode", [hb.EXACT, hb.FAST])
+def test_narrow_layer_many_rows(gpu, mode):
+    """The SparseDrive-S stage-1 3x3 im2col shape (K=576, N=64: one partly
+    used column tile) on 1000 rows, a slice of its 67,584."""
+    rng = np.random.default_rng(80)
+    m, n, k = 1000, 64, 576
+    kb, a, planes, modes = make_layer(rng, m, n, k, False)
+    got, _ = run_linear(gpu, m, n, kb, a, planes, modes, mode=mode)
+    want, _ = oracle_linear(m, n, kb, a, planes, modes)
+    if mode == hb.EXACT:
+        assert_bits(got, want)
+    else:
+        g, w = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
+        row_scale = np.abs(w).max(axis=1, keepdims=True)
+        assert (np.abs(g - w) <= 1e-5 * row_scale).all(), float((np.abs(g - w) / row_scale).max())
+
+
 @pytest.mark.parametrize("w8", [False, True])
 def test_pieces_and_onto(gpu, w8):
     rng = np.random.default_rng(20 + w8)

@@ -149,6 +149,45 @@ __device__ __forceinline__ float EpApplyFast(uint32_t kind, uint32_t imm, float 
   }
 }
 
+// EpApplyFast over 16 values (one MFMA tile of a lane): the kind is
+// resolved once, each case is a straight run.  x2 holds the op's [m][n]
+// operand, p the column's vector value.
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ void EpApplyFast16(uint32_t kind, uint32_t imm, f32x16_t& y,
+                                              const f32x16_t& x2, float p, const uint64_t* t) {
+  switch (kind) {
+    case kEpAddP: y = (y + p) + 0.0f; break;
+    case kEpMulP: y = (y + 0.0f) * p + 0.0f; break;
+    case kEpScale: y = (y + 0.0f) * __uint_as_float(imm) + 0.0f; break;
+    case kEpCopy: y = y + 0.0f; break;
+    case kEpAdd: y = (y + x2) + 0.0f; break;
+    case kEpRelu:
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float prod = y[r] + 0.0f;
+        y[r] = (prod > 0.0f ? prod : 0.0f) + 0.0f;
+      }
+      break;
+    // (the fences keep the 16 table lookups from all being in flight at
+    // once, which would cost registers the caller needs)
+    case kEpAct:
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        y[r] = ActGateFast(y[r], t);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      break;
+    case kEpActMul:
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        y[r] = (ActGateFast(y[r], t) + 0.0f) * x2[r] + 0.0f;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      break;
+    default: break;
+  }
+}
+
 // QuantizeBlock for one token: values[32] -> bytes and scale byte.
 // emax = largest exponent field (0 -> scale byte 127).
 __device__ __forceinline__ uint32_t ScaleByteOf(uint32_t emax) { return emax == 0 ? 127u : emax; }

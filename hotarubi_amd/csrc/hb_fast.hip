@@ -335,7 +335,8 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
   static_assert(kWavesM * (8 / kTN) * 64 == kP && kTM * kTN == 4, "consumer wave grid");
   static_assert(kU >= 3, "LDS stages");
   __shared__ __attribute__((aligned(16))) Lds<kMT, kW8> lds;
-  __shared__ uint64_t lds_act[512];  // activation half of TBUF, for the epilogue
+  __shared__ uint64_t lds_act[512];             // activation half of TBUF
+  __shared__ float lds_vec[kMaxOps][kBN];         // the tile's columns of each op vector
   __shared__ uint32_t lds_unsafe;
 
   const TileId tile = LogicalTile(g.gx, g.gy, g.gz);
@@ -389,54 +390,66 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
       }
       return;
     }
-    // Epilogue ops (FP32 hardware arithmetic), op by op, one MFMA tile at a
-    // time: the tile's operands are loaded first, all at once (independent
-    // loads, one wait); the element loop then only computes.
-    for (uint32_t o = 0; o < g.n_ops; ++o) {
-      const uint32_t kind = g.op_kind[o], imm = g.op_imm[o];
-      const bool has_x2 = kind == kEpAdd || kind == kEpActMul;
-      const bool has_vec = kind == kEpAddP || kind == kEpMulP;
-      const uint32_t* x2 = g.op_x2[o] + z * g.op_x2_batch[o];
-      const uint32_t* v = g.op_vec[o] + z * g.op_vec_batch[o];
-      for (uint32_t t0 = e0; t0 < e1; t0 += 16) {
-        const uint32_t col = col_at(t0);
-        f32x16 xv;  // a register vector: the runtime index below is wave-uniform
+    if (g.n_ops == 0 && q_out == nullptr) {  // plain C: a rolled loop, few registers
+      for (uint32_t e = e0; e < e1; ++e) {
+        const uint32_t row = row_at(e), col = col_at(e);
+        if (row < g.m && col < g.n) c[(size_t)row * g.n + col] = __float_as_uint(vals[e * 64 + l]);
+      }
+      return;
+    }
+    // Ops (FP32 hardware arithmetic), C and requantize, one MFMA tile (16
+    // values per lane) at a time, all in registers: the tile's values and
+    // each op's operands are loaded at once (independent loads, one wait),
+    // and each op is a straight run over the 16 values.
+    for (uint32_t t0 = e0; t0 < e1; t0 += 16) {
+      // Output r of the tile is row row_l + RowStep(r), column col: the
+      // row step is uniform, so each access is a uniform base plus one
+      // per-lane 32-bit offset (no per-row 64-bit addresses to keep live).
+      const uint32_t col = col_at(t0), row_l = row_at(t0);
+      const uint32_t off_l = row_l * g.n + col;
+      auto row_step = [](int r) { return (uint32_t)(8 * (r / 4) + (r & 3)); };
+      f32x16 y;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) y[r] = vals[(t0 + r) * 64 + l];
+      for (uint32_t o = 0; o < g.n_ops; ++o) {
+        const uint32_t kind = g.op_kind[o];
+        f32x16 x2 = {};
+        float p = 0.0f;
+        if (kind == kEpAdd || kind == kEpActMul) {
+          const uint32_t* src = g.op_x2[o] + z * g.op_x2_batch[o];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const uint32_t* src_r = src + row_step(r) * g.n;  // uniform
+            x2[r] = __uint_as_float(row_l + row_step(r) < g.m && col < g.n ? src_r[off_l] : 0u);
+          }
+        } else if (kind == kEpAddP || kind == kEpMulP) {
+          p = lds_vec[o][col - col0];
+        }
+        EpApplyFast16(kind, g.op_imm[o], y, x2, p, lds_act);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        uint32_t* c_r = c + row_step(r) * g.n;  // uniform
+        if (row_l + row_step(r) < g.m && col < g.n) c_r[off_l] = __float_as_uint(y[r]);
+      }
+      if (q_out != nullptr) {  // MXINT8 requantize over the 32 lanes holding a row's block
+        const uint32_t nb = g.n >> 5, blk = (col - (l & 31)) >> 5;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const uint32_t row = row_at(t0 + r);
-          xv[r] = __uint_as_float(has_x2 && row < g.m && col < g.n ? x2[(size_t)row * g.n + col]
-                                                                   : 0u);
-        }
-        const float pv = __uint_as_float(has_vec && col < g.n ? v[col] : 0u);
-#pragma unroll 1
-        for (uint32_t r = 0; r < 16; ++r) {
-          const uint32_t row = row_at(t0 + r);
-          float& y = vals[(t0 + r) * 64 + l];
-          if ((row >> 2) < g.quads && col < g.n)
-            y = EpApplyFast(kind, imm, y, xv[r], pv, lds_act);
-        }
-      }
-    }
-    for (uint32_t e = e0; e < e1; ++e) {
-      const uint32_t row = row_at(e), col = col_at(e);
-      if (row < g.m && col < g.n) c[(size_t)row * g.n + col] = __float_as_uint(vals[e * 64 + l]);
-    }
-    if (q_out != nullptr) {  // MXINT8 requantize over the 32 lanes holding a row's block
-      const uint32_t nb = g.n >> 5;
-      for (uint32_t e = e0; e < e1; ++e) {
-        const uint32_t y = __float_as_uint(vals[e * 64 + l]);
-        const uint32_t row = row_at(e), blk = (col_at(e) - (l & 31)) >> 5;
-        uint32_t x = ExpField(y);
-        x = max(x, (uint32_t)__shfl_xor((int)x, 1));
-        x = max(x, (uint32_t)__shfl_xor((int)x, 2));
-        x = max(x, (uint32_t)__shfl_xor((int)x, 4));
-        x = max(x, (uint32_t)__shfl_xor((int)x, 8));
-        x = max(x, (uint32_t)__shfl_xor((int)x, 16));
-        if ((row >> 2) < g.quads && blk < nb) {
-          uint8_t* word = q_out + ((size_t)(row >> 2) * nb + blk) * kDdrWord;
-          word[(row & 3) * 32 + (l & 31)] = QuantizeElement(y, x);
-          if ((l & 31) == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(x);
-          if ((l & 31) < 12 && (row & 3) == 0) word[132 + (l & 31)] = 0;
+          const uint32_t v = __float_as_uint(y[r]), row = row_l + row_step(r);
+          uint32_t x = ExpField(v);
+          x = max(x, (uint32_t)__shfl_xor((int)x, 1));
+          x = max(x, (uint32_t)__shfl_xor((int)x, 2));
+          x = max(x, (uint32_t)__shfl_xor((int)x, 4));
+          x = max(x, (uint32_t)__shfl_xor((int)x, 8));
+          x = max(x, (uint32_t)__shfl_xor((int)x, 16));
+          if ((row >> 2) < g.quads && blk < nb) {
+            uint8_t* word = q_out + ((size_t)(row >> 2) * nb + blk) * kDdrWord;
+            word[(row & 3) * 32 + (l & 31)] = QuantizeElement(v, x);
+            if ((l & 31) == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(x);
+            if ((l & 31) < 12 && (row & 3) == 0) word[132 + (l & 31)] = 0;
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
@@ -457,6 +470,23 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
       LoadRaw<kP, kWLoads, kMulti>(g, a, w0, w1, offs, t, s0, step, steps, nblocks, rw);
       __builtin_amdgcn_sched_barrier(0);
     };
+    // The epilogue's small operands (the activation table, the tile's
+    // columns of each op vector) are fetched first, while the pipeline
+    // fills, and parked in LDS after the first conversions, so that their
+    // latency hides under the K loop.
+    constexpr int kActLoads = 512 / kP, kVecLoads = kMaxOps * kBN / kP;
+    uint64_t act_v[kActLoads];
+    uint32_t vec_v[kVecLoads];
+#pragma unroll
+    for (int k = 0; k < kActLoads; ++k)
+      act_v[k] = g.tbuf != nullptr ? g.tbuf[512 + t + kP * k] : 0u;
+#pragma unroll
+    for (int k = 0; k < kVecLoads; ++k) {
+      const uint32_t i = t + kP * k, o = i / kBN, col = col0 + i % kBN;
+      vec_v[k] = 0u;
+      if (o < g.n_ops && (g.op_kind[o] == kEpAddP || g.op_kind[o] == kEpMulP) && col < g.n)
+        vec_v[k] = g.op_vec[o][z * g.op_vec_batch[o] + col];
+    }
     bool unsafe = false;
 #pragma unroll
     for (int i = 0; i < kU; ++i) load(ring[i], i);
@@ -465,6 +495,10 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
       unsafe |= StoreRaw<kMT, kP, kWLoads, kW8>(ring[i], lds, i, t);
       load(ring[i], i + kU);
     }
+#pragma unroll
+    for (int k = 0; k < kActLoads; ++k) lds_act[t + kP * k] = act_v[k];
+#pragma unroll
+    for (int k = 0; k < kVecLoads; ++k) lds_vec[(t + kP * k) / kBN][(t + kP * k) % kBN] = __uint_as_float(vec_v[k]);
     __syncthreads();
     for (uint32_t step = 0; step < steps; step += kU) {
 #pragma unroll
@@ -475,8 +509,6 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
       }
     }
     if (unsafe) lds_unsafe = 1;
-    if (g.tbuf != nullptr)  // the producers are done: stage the activation table
-      for (uint32_t i = t; i < 512; i += kP) lds_act[i] = g.tbuf[512 + i];
     __syncthreads();
     __syncthreads();  // the consumers' outputs are in LDS
     // producer wave v takes tiles 2 and 3 of consumer wave v

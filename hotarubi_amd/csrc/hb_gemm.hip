@@ -683,6 +683,12 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   // Fast mode runs MXFP4 and W8 (hi, lo) on the block-scaled matrix cores;
   // any other plane list runs exactly (which meets the fast-mode tolerance).
   const bool fastk = fast && FastEligible(args);
+  // Split-K over the waves of one workgroup pays where a workgroup can hold
+  // every row and still many columns: up to 16 rows, or a single MXFP4 layer
+  // of up to 64 rows (which otherwise needs K splits and a second launch).
+  if (fastk && (args.quads * 4 <= 16 ||
+                (args.quads * 4 <= 64 && batch == 1 && args.n_planes == 1)))
+    return LaunchLinearSkinny(args, batch, stream);
   uint32_t gx, gy;
   if (fastk) FastGrid(args, &gx, &gy, &args.tile_rows);
   else ExactGrid(args, &gx, &gy);

@@ -118,6 +118,9 @@ bool FastEligible(const GemmArgs& args);
 // tile.
 void FastGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy, uint32_t* tile_rows);
 hipError_t LaunchLinearFast(const GemmArgs& args, uint32_t batch, hipStream_t stream);
+// Fast path for layers of at most 64 rows (hb_skinny.hip): split-K over the
+// waves of a workgroup, W streamed into registers.
+hipError_t LaunchLinearSkinny(const GemmArgs& args, uint32_t batch, hipStream_t stream);
 // Exact tile kernel grid for a linear layer (column tiles, row tiles).
 void ExactGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy);
 // Deferred epilogue (hb_vec.hip): reads args.ws, writes C and q_out.

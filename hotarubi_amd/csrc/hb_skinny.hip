@@ -1,0 +1,373 @@
+// Skinny fast linear kernel for gfx950 (HB_LINEAR_FAST, at most 64 rows):
+// MXFP4 or W8 weights streamed from HBM straight into the matrix cores.
+//
+// Matrix cores: v_mfma_scale_f32_16x16x128_f8f6f4.  One lane's A operand is
+// 32 values of one row and one K-block (lane l: row l % 16, block l / 16 of
+// a 4-block chunk), one lane's B operand 32 values of one column and block,
+// each with its own E8M0 scale; the formats and scale bytes are those of the
+// 128-row fast kernel (A as FP6 planes hi/2, lo/2 with ea-1, ea-5; MXFP4 W
+// untouched; W8 W as FP6 planes with ew-1, ew-5, K in the W8 byte order).
+//
+// Work split: a workgroup holds every row (16 * kMT <= 64) and kCols
+// columns; its 8 waves take contiguous ranges of 4-block K chunks (split-K).
+// Each lane loads its own A bytes and W column-block (16 B per plane, the
+// WBUF word layout) into registers, converts, and issues the chunk's MFMAs;
+// the next chunk's loads are in flight meanwhile.  No LDS staging: no A or W
+// byte is converted twice in a workgroup.  The waves' partial sums are then
+// added in wave order through LDS, and the epilogue (ops in FP32 hardware
+// arithmetic, C, requantize) runs over the workgroup's outputs.
+#include <utility>
+
+#include "hb_device.h"
+#include "hb_internal.h"
+
+namespace hb {
+namespace {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x6 __attribute__((ext_vector_type(6)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x32 __attribute__((ext_vector_type(32)));
+
+constexpr int kWaves = 8;
+constexpr uint32_t kSafeLo = 70, kSafeHi = 179;
+
+// Columns per workgroup: 16 * kNT, with the accumulators (kMT * kNT * 4) and
+// two chunks of raw loads within the 256 registers of a 512-thread group.
+template <int kMT, bool kW8>
+constexpr int NTiles() {
+  return kW8 ? (kMT == 4 ? 2 : 4) : (kMT == 1 ? 8 : 4);
+}
+
+template <bool kMulti>
+__device__ __forceinline__ uint32_t SkinnyBlockOf(const GemmArgs& g, uint32_t idx) {
+  uint32_t base = g.piece_off[0];
+  if (kMulti) {
+    uint32_t start = 0;
+#pragma unroll
+    for (uint32_t p = 1; p < kMaxPieces; ++p) {
+      start += g.piece_kb[p - 1];
+      const bool in = p < g.n_pieces && idx >= start;
+      base = in ? g.piece_off[p] - start : base;
+    }
+  }
+  return base + idx;
+}
+
+// f16 pair {byte i, byte j of nb} minus bias (see the 128-row kernel).
+__device__ __forceinline__ f16x2 PairS(uint32_t nb, uint32_t sel, f16x2 bias) {
+  return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x60606060u, nb, sel)) - bias;
+}
+constexpr uint32_t SelS(uint32_t i, uint32_t j) { return 0x04000400u | i | (j << 16); }
+
+// 32 int8 -> one FP6 plane (hi/2 or lo/2); kPermK: K in the W8 order.
+template <bool kPermK>
+__device__ __forceinline__ u32x6 APlane(const uint32_t* x, uint32_t nib, bool lo) {
+  const uint32_t shift = lo ? 0u : 4u, flip = lo ? 0u : 0x08080808u;
+  const _Float16 b = lo ? (_Float16)512.0f : (_Float16)516.0f;
+  const f16x2 bias = {b, b};
+  f16x32 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t n0 = ((x[2 * i] >> shift) & nib) ^ flip;
+    const uint32_t n1 = ((x[2 * i + 1] >> shift) & nib) ^ flip;
+    f16x2 d[4];
+    if (kPermK) {
+      d[0] = PairS(n0, SelS(0, 2), bias);
+      d[1] = PairS(n1, SelS(0, 2), bias);
+      d[2] = PairS(n0, SelS(1, 3), bias);
+      d[3] = PairS(n1, SelS(1, 3), bias);
+    } else {
+      d[0] = PairS(n0, SelS(0, 1), bias);
+      d[1] = PairS(n0, SelS(2, 3), bias);
+      d[2] = PairS(n1, SelS(0, 1), bias);
+      d[3] = PairS(n1, SelS(2, 3), bias);
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      v[8 * i + 2 * p] = d[p][0];
+      v[8 * i + 2 * p + 1] = d[p][1];
+    }
+  }
+  return __builtin_amdgcn_cvt_scalef32_pk32_fp6_f16(v, 1.0f);
+}
+
+// One W8 plane's 16 bytes -> 32 FP6 codes, K in the W8 order.
+__device__ __forceinline__ u32x6 WPlane(const uint32_t* x, bool lo) {
+  const uint32_t flip = lo ? 0u : 0x88888888u;
+  const _Float16 b = lo ? (_Float16)512.0f : (_Float16)516.0f;
+  const f16x2 bias = {b, b};
+  f16x32 v;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t y = x[j] ^ flip;
+    const uint32_t ev = y & 0x0F0F0F0Fu, od = (y >> 4) & 0x0F0F0F0Fu;
+    const f16x2 d[4] = {PairS(ev, SelS(0, 1), bias), PairS(ev, SelS(2, 3), bias),
+                        PairS(od, SelS(0, 1), bias), PairS(od, SelS(2, 3), bias)};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      v[8 * j + 2 * p] = d[p][0];
+      v[8 * j + 2 * p + 1] = d[p][1];
+    }
+  }
+  return __builtin_amdgcn_cvt_scalef32_pk32_fp6_f16(v, 1.0f);
+}
+
+template <typename Fn, int... kI>
+__device__ __forceinline__ void UnrollS(Fn&& f, std::integer_sequence<int, kI...>) {
+  (f(std::integral_constant<int, kI>{}), ...);
+}
+
+// One chunk's raw registers: per m-tile 32 A bytes and the scale dword, per
+// n-tile and plane 16 W bytes and the scale dword.
+template <int kMT, int kNT, int kWP>
+struct RawS {
+  uint32_t a[kMT][8], sa[kMT];
+  uint32_t w[kNT][kWP][4], sw[kNT][kWP];
+  uint32_t nib;  // 0x0F0F0F0F, or 0 for a block past the end (adds zero)
+};
+
+template <int kMT, bool kW8, bool kMulti>
+__global__ __launch_bounds__(kWaves * 64) void SkinnyKernel(GemmArgs g) {
+  constexpr int kNT = NTiles<kMT, kW8>(), kCols = 16 * kNT, kWP = kW8 ? 2 : 1;
+  constexpr int kRows = 16 * kMT, kOut = kRows * kCols;
+  __shared__ float lds_part[kWaves][kOut];  // the waves' partial sums
+  __shared__ uint64_t lds_act[512];
+  __shared__ uint32_t lds_unsafe;
+
+  const TileId tile = LogicalTile(g.gx, 1, g.gz);
+  const uint32_t z = tile.z;
+  const uint8_t* a = g.a + z * g.a_batch;
+  const uint8_t* w0 = g.w[0] + z * g.w_batch;
+  const uint8_t* w1 = kW8 ? g.w[1] + z * g.w_batch : w0;
+  uint32_t* c = g.c + z * g.c_batch;
+  uint8_t* q_out = g.q_out ? g.q_out + z * g.q_batch : nullptr;
+  const uint32_t col0 = tile.x * kCols;
+  const uint32_t t = threadIdx.x, lane = t & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const uint32_t r16 = lane & 15, kq = lane >> 4;
+
+  if (t == 0) lds_unsafe = 0;
+  if (g.tbuf != nullptr)
+    for (uint32_t i = t; i < 512; i += kWaves * 64) lds_act[i] = g.tbuf[512 + i];
+  __syncthreads();
+
+  uint32_t nblocks = 0;
+  for (uint32_t p = 0; p < g.n_pieces; ++p) nblocks += g.piece_kb[p];
+  const uint32_t chunks = (nblocks + 3) / 4, per = (chunks + kWaves - 1) / kWaves;
+  const uint32_t c_begin = wave * per, c_end = min(c_begin + per, chunks);
+  const uint32_t word_row = g.kb_total * kDdrWord;
+
+  // Per-lane byte offsets within a block's words (fixed for the K loop).
+  // The lane's row within a quad (r16 % 4) and column within a group (r16 %
+  // 8) are the same in every tile, so the scale dword's offset from the data
+  // and the scale byte's position are per lane, not per tile.
+  const uint32_t ashift = 8 * (r16 & 3), as_delta = 128 - (r16 & 3) * 32;
+  const uint32_t cl = r16 & 7, wshift = 8 * (cl & 3), ws_delta = 128 + (cl & 4) - cl * 16;
+  uint32_t a_off[kMT], w_off[kNT];
+#pragma unroll
+  for (int mi = 0; mi < kMT; ++mi) {
+    const uint32_t quad = min((mi * 16 + r16) >> 2, g.quads - 1);
+    a_off[mi] = quad * word_row + (r16 & 3) * 32;
+  }
+#pragma unroll
+  for (int nj = 0; nj < kNT; ++nj)
+    w_off[nj] = min((col0 + nj * 16 + r16) >> 3, g.groups - 1) * word_row + cl * 16;
+
+  // Loads of chunk ch (its lane's block); a chunk at or past c_end, or a
+  // block past the end, reloads a valid block and adds zero.
+  auto load = [&](RawS<kMT, kNT, kWP>& rw, uint32_t ch) {
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t idx = 4 * ch + kq;
+    rw.nib = (ch < c_end && idx < nblocks) ? 0x0F0F0F0Fu : 0u;
+    const uint32_t blk = SkinnyBlockOf<kMulti>(g, min(idx, nblocks - 1)) * kDdrWord;
+#pragma unroll
+    for (int mi = 0; mi < kMT; ++mi) {
+      const uint8_t* p = a + blk + a_off[mi];
+      const u32x4 v0 = *reinterpret_cast<const u32x4*>(p);
+      const u32x4 v1 = *reinterpret_cast<const u32x4*>(p + 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        rw.a[mi][i] = v0[i];
+        rw.a[mi][4 + i] = v1[i];
+      }
+      rw.sa[mi] = *reinterpret_cast<const uint32_t*>(a + blk + a_off[mi] + as_delta);
+    }
+#pragma unroll
+    for (int nj = 0; nj < kNT; ++nj)
+#pragma unroll
+      for (int pl = 0; pl < kWP; ++pl) {
+        const uint8_t* wb = (pl ? w1 : w0) + blk;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(wb + w_off[nj]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rw.w[nj][pl][i] = v[i];
+        rw.sw[nj][pl] = *reinterpret_cast<const uint32_t*>(wb + w_off[nj] + ws_delta);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  f32x4 acc[kMT][kNT];
+#pragma unroll
+  for (int mi = 0; mi < kMT; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < kNT; ++nj) acc[mi][nj] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  bool unsafe = false;
+
+  auto compute = [&](const RawS<kMT, kNT, kWP>& rw) {
+    i32x8 b[kNT][kWP];
+    uint32_t sb[kNT];
+#pragma unroll
+    for (int nj = 0; nj < kNT; ++nj) {
+      const uint32_t ewh = __builtin_amdgcn_ubfe(rw.sw[nj][0], wshift, 8);
+      unsafe |= ewh - kSafeLo > kSafeHi - kSafeLo;
+      if constexpr (kW8) {
+        const uint32_t ewl = __builtin_amdgcn_ubfe(rw.sw[nj][1], wshift, 8);
+        unsafe |= ewl - kSafeLo > kSafeHi - kSafeLo;
+        sb[nj] = (ewh - 1u) | ((ewl - 5u) << 8);
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) {
+          const u32x6 cw = WPlane(rw.w[nj][pl], pl != 0);
+#pragma unroll
+          for (int i = 0; i < 6; ++i) b[nj][pl][i] = (int)cw[i];
+          b[nj][pl][6] = b[nj][pl][7] = 0;
+        }
+      } else {
+        sb[nj] = ewh;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b[nj][0][i] = (int)rw.w[nj][0][i];
+        b[nj][0][4] = b[nj][0][5] = b[nj][0][6] = b[nj][0][7] = 0;
+      }
+    }
+#pragma unroll
+    for (int mi = 0; mi < kMT; ++mi) {
+      const uint32_t ea = __builtin_amdgcn_ubfe(rw.sa[mi], ashift, 8);
+      unsafe |= ea - kSafeLo > kSafeHi - kSafeLo;
+      const int sa = (int)((ea - 1u) | ((ea - 5u) << 8));
+      i32x8 ap[2];
+#pragma unroll
+      for (int pa = 0; pa < 2; ++pa) {
+        const u32x6 ca = APlane<kW8>(rw.a[mi], rw.nib, pa != 0);
+#pragma unroll
+        for (int i = 0; i < 6; ++i) ap[pa][i] = (int)ca[i];
+        ap[pa][6] = ap[pa][7] = 0;
+      }
+      // plane products outer, column tiles inner: consecutive MFMAs update
+      // different accumulators
+      UnrollS([&](auto pa_c) {
+        constexpr int pa = decltype(pa_c)::value;
+        UnrollS([&](auto pb_c) {
+          constexpr int pb = decltype(pb_c)::value;
+          UnrollS([&](auto nj_c) {
+            constexpr int nj = decltype(nj_c)::value;
+            acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                ap[pa], b[nj][pb], acc[mi][nj], 2, kW8 ? 2 : 4, pa, sa, pb, (int)sb[nj]);
+          }, std::make_integer_sequence<int, kNT>{});
+        }, std::make_integer_sequence<int, kWP>{});
+      }, std::make_integer_sequence<int, 2>{});
+    }
+  };
+
+  if (c_begin < c_end) {
+    // Two register sets: the next chunk's loads are in flight while this
+    // one computes; a chunk past the end adds zero (branch-free loop).
+    RawS<kMT, kNT, kWP> r0, r1;
+    load(r0, c_begin);
+    for (uint32_t ch = c_begin; ch < c_end; ch += 2) {
+      load(r1, ch + 1);
+      compute(r0);
+      load(r0, ch + 2);
+      compute(r1);
+    }
+  }
+  if (unsafe) lds_unsafe = 1;
+
+  // Partial sums to LDS: lane l holds rows 4*(l/16) + i of each 16x16 tile
+  // (column l % 16).
+#pragma unroll
+  for (int mi = 0; mi < kMT; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < kNT; ++nj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        lds_part[wave][(mi * 16 + 4 * kq + i) * kCols + nj * 16 + r16] = acc[mi][nj][i];
+  __syncthreads();
+  const bool slow = lds_unsafe != 0;
+
+  // Epilogue: output o = t + 512 p is row o / kCols, column col0 + o % kCols;
+  // 32 consecutive threads hold one row's 32-column block.
+  for (uint32_t o = t; o < kOut; o += kWaves * 64) {
+    const uint32_t row = o / kCols, col = col0 + o % kCols;
+    const bool in = (row >> 2) < g.quads && col < g.n;
+    uint32_t y = 0;
+    if (in) {
+      const uint32_t init = (g.acc && row < g.m) ? c[(size_t)row * g.n + col] : 0u;
+      if (slow) {
+        y = SlowLinear(g, a, w0, w1, init, row, col);
+      } else {
+        float s = __uint_as_float(init);
+#pragma unroll
+        for (int wv = 0; wv < kWaves; ++wv) s += lds_part[wv][o];
+        y = __float_as_uint(s + 0.0f);
+      }
+      for (uint32_t op = 0; op < g.n_ops; ++op) {
+        const uint32_t kind = g.op_kind[op];
+        const uint32_t x2 = (kind == kEpAdd || kind == kEpActMul) && row < g.m
+                                ? g.op_x2[op][z * g.op_x2_batch[op] + (size_t)row * g.n + col] : 0u;
+        const uint32_t pv = (kind == kEpAddP || kind == kEpMulP)
+                                ? g.op_vec[op][z * g.op_vec_batch[op] + col] : 0u;
+        y = __float_as_uint(EpApplyFast(kind, g.op_imm[op], __uint_as_float(y),
+                                        __uint_as_float(x2), __uint_as_float(pv), lds_act));
+      }
+      if (row < g.m) c[(size_t)row * g.n + col] = y;
+    }
+    if (q_out != nullptr) {
+      uint32_t e = in ? ExpField(y) : 0u;
+      e = max(e, (uint32_t)__shfl_xor((int)e, 1));
+      e = max(e, (uint32_t)__shfl_xor((int)e, 2));
+      e = max(e, (uint32_t)__shfl_xor((int)e, 4));
+      e = max(e, (uint32_t)__shfl_xor((int)e, 8));
+      e = max(e, (uint32_t)__shfl_xor((int)e, 16));
+      if (in) {
+        const uint32_t nb = g.n >> 5, c32 = col & 31;
+        uint8_t* word = q_out + ((size_t)(row >> 2) * nb + (col >> 5)) * kDdrWord;
+        word[(row & 3) * 32 + c32] = QuantizeElement(y, e);
+        if (c32 == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(e);
+        if (c32 < 12 && (row & 3) == 0) word[132 + c32] = 0;
+      }
+    }
+  }
+}
+
+template <int kMT, bool kW8, bool kMulti>
+void LaunchS(const GemmArgs& in, uint32_t batch, hipStream_t stream) {
+  constexpr int kCols = 16 * NTiles<kMT, kW8>();
+  GemmArgs args = in;
+  args.gx = (args.groups * 8 + kCols - 1) / kCols;
+  args.gy = 1;
+  args.gz = batch;
+  hipLaunchKernelGGL((SkinnyKernel<kMT, kW8, kMulti>), dim3(args.gx * args.gz), dim3(kWaves * 64),
+                     0, stream, args);
+}
+
+template <int kMT>
+void LaunchRowsS(const GemmArgs& args, uint32_t batch, hipStream_t stream) {
+  const bool multi = args.n_pieces > 1, w8 = args.n_planes == 2;
+  if (w8) multi ? LaunchS<kMT, true, true>(args, batch, stream)
+              : LaunchS<kMT, true, false>(args, batch, stream);
+  else multi ? LaunchS<kMT, false, true>(args, batch, stream)
+             : LaunchS<kMT, false, false>(args, batch, stream);
+}
+
+}  // namespace
+
+hipError_t LaunchLinearSkinny(const GemmArgs& args, uint32_t batch, hipStream_t stream) {
+  const uint32_t rows = args.quads * 4;
+  if (rows <= 16) LaunchRowsS<1>(args, batch, stream);
+  else if (rows <= 32) LaunchRowsS<2>(args, batch, stream);
+  else LaunchRowsS<4>(args, batch, stream);
+  return hipGetLastError();
+}
+
+}  // namespace hb

@@ -373,6 +373,30 @@ def test_fast_out_of_window_scales_recompute_exactly(gpu, w8):
     assert (np.abs(g - w) <= 1e-5 * row_scale).all()
 
 
+@pytest.mark.parametrize("w8", [False, True])
+def test_fast_skinny_out_of_window_and_onto(gpu, w8):
+    """A layer of at most 64 rows (one workgroup holds all rows): a weight
+    scale byte out of the window makes that workgroup's columns exact, bit
+    for bit; the rest, started from C with MULP and requantize, stays within
+    tolerance."""
+    rng = np.random.default_rng(65 + w8)
+    m, n, k = 40, 512, 736
+    kb, a, planes, modes = make_layer(rng, m, n, k, w8)
+    planes = [p.copy() for p in planes]
+    for p in planes:
+        p.reshape(n // 8, kb, 144)[0, 5, 128] = 200    # column 0, block 5: out of the window
+    onto = helpers.random_fp32_words(rng, (m, n), 120, 130)
+    scale = helpers.random_fp32_words(rng, (n,), 117, 122)
+    ops = [(hb.EP_MULP, scale)]
+    got, gq = run_linear(gpu, m, n, kb, a, planes, modes, ops, onto=onto, quantize=True,
+                         mode=hb.FAST)
+    want, wq = oracle_linear(m, n, kb, a, planes, modes, ops, onto=onto, quantize=True)
+    assert_bits(got[:, :32], want[:, :32])  # within the exact workgroup's columns
+    g, w = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
+    row_scale = np.abs(w).max(axis=1, keepdims=True)
+    assert (np.abs(g - w) <= 1e-5 * row_scale).all(), float((np.abs(g - w) / row_scale).max())
+
+
 def test_batched_rejects_mismatched_layers(gpu):
     rng = np.random.default_rng(62)
     m, n, k = 32, 64, 64

@@ -111,10 +111,11 @@ __device__ __forceinline__ void Unroll(Fn&& f) {
   UnrollImpl(f, std::make_integer_sequence<int, kN>{});
 }
 
-// Work split of the raw bytes of one step over the kP = kBM * 4 producer
-// threads (kBM / 16 waves; t below is the producer-local index):
-//   A: wave v converts plane v % 2 (0: hi, 1: lo) of m-tile v / 2; its lane
-//      l takes row l % 32 of the tile and block l / 32 (32 bytes + scale).
+// Work split of the raw bytes of one step over the kP = 512 producer threads
+// (8 waves; t below is the producer-local index):
+//   A: wave v < 2 * kMT converts plane v % 2 (0: hi, 1: lo) of m-tile v / 2;
+//      its lane l takes row l % 32 of the tile and block l / 32 (32 bytes +
+//      scale).  With 64-row tiles, waves 4..7 have no A work.
 //   W: the step's 256 columns x 2 blocks are 512 column-blocks of 16 bytes
 //      per plane; thread t loads column-blocks u = t + kP*k, k < kWLoads
 //      (column u % 256, block (u / 256) % 2, plane u / 512; block and plane
@@ -181,7 +182,7 @@ __device__ __forceinline__ Offsets<kWLoads> ThreadOffsets(const GemmArgs& g, uin
 // activations masked to zero, so they add nothing.  Block offsets are uniform
 // and folded into the scalar base pointer; each load is one instruction on
 // (uniform base, 32-bit lane offset).
-template <int kP, int kWLoads, bool kMulti>
+template <int kP, int kWLoads, bool kMulti, bool kAWave>
 __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, const uint8_t* w0,
                                         const uint8_t* w1, const Offsets<kWLoads>& o, uint32_t t,
                                         uint32_t s0, uint32_t live_step, uint32_t steps,
@@ -190,19 +191,21 @@ __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, con
   const uint32_t step = s0 + min(live_step, steps - 1);  // steps of this split start at s0
   const uint32_t ub0 = BlockOf<kMulti>(g, 2 * step) * kDdrWord;
   const uint32_t ub1 = BlockOf<kMulti>(g, min(2 * step + 1, nblocks - 1)) * kDdrWord;
-  const uint8_t* ab = a + ub0;                 // uniform
-  const uint32_t ao = o.a + (h ? ub1 - ub0 : 0u);  // ub1 - ub0 is uniform
-  const u32x4 v0 = *reinterpret_cast<const u32x4*>(ab + ao);
-  const u32x4 v1 = *reinterpret_cast<const u32x4*>(ab + ao + 16);
-  // Applied at conversion time, not here: a select on the loaded registers
-  // would make the compiler wait for the load right away.
-  rw.nib = (live_step >= steps || (h && 2 * step + 1 >= nblocks)) ? 0u : 0x0F0F0F0Fu;
+  if constexpr (kAWave) {
+    const uint8_t* ab = a + ub0;                 // uniform
+    const uint32_t ao = o.a + (h ? ub1 - ub0 : 0u);  // ub1 - ub0 is uniform
+    const u32x4 v0 = *reinterpret_cast<const u32x4*>(ab + ao);
+    const u32x4 v1 = *reinterpret_cast<const u32x4*>(ab + ao + 16);
+    // Applied at conversion time, not here: a select on the loaded registers
+    // would make the compiler wait for the load right away.
+    rw.nib = (live_step >= steps || (h && 2 * step + 1 >= nblocks)) ? 0u : 0x0F0F0F0Fu;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    rw.a[i] = v0[i];
-    rw.a[4 + i] = v1[i];
+    for (int i = 0; i < 4; ++i) {
+      rw.a[i] = v0[i];
+      rw.a[4 + i] = v1[i];
+    }
+    rw.sa = *reinterpret_cast<const uint32_t*>(ab + (o.a_scale + (h ? ub1 - ub0 : 0u)));
   }
-  rw.sa = *reinterpret_cast<const uint32_t*>(ab + (o.a_scale + (h ? ub1 - ub0 : 0u)));
 #pragma unroll
   for (int k = 0; k < kWLoads; ++k) {
     const uint32_t u = t + kP * k;
@@ -282,19 +285,22 @@ __device__ __forceinline__ u32x6 PlaneW8(const uint32_t* x, bool lo) {
   return __builtin_amdgcn_cvt_scalef32_pk32_fp6_f16(v, 1.0f);
 }
 
-template <int kMT, int kP, int kWLoads, bool kW8>
+template <int kMT, int kP, int kWLoads, bool kW8, bool kAWave>
 __device__ __forceinline__ bool StoreRaw(const Raw<kWLoads>& rw, Lds<kMT, kW8>& l, int st,
                                          uint32_t t) {
   const uint32_t lane = t & 63;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const uint32_t p = wave & 1, mt = wave >> 1;
-  const u32x6 codes = Plane32<kW8>(rw.a, rw.nib, p != 0);
-#pragma unroll
-  for (int i = 0; i < 3; ++i) l.a[st][p][mt][i][lane] = uint2{codes[2 * i], codes[2 * i + 1]};
   constexpr int kTM = Fmt<kW8>::kTM, kTN = Fmt<kW8>::kTN, kWP = Fmt<kW8>::kWPlanes;
-  const uint32_t ea = __builtin_amdgcn_ubfe(rw.sa, 8 * (lane & 3), 8);  // row t = lane % 4
-  PutByte(l.sa[st][mt / kTM][lane], (mt % kTM) * 2 + p, ea - (p ? 5u : 1u));
-  bool bad = ea - kSafeLo > kSafeHi - kSafeLo;
+  bool bad = false;
+  if constexpr (kAWave) {
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t p = wave & 1, mt = wave >> 1;
+    const u32x6 codes = Plane32<kW8>(rw.a, rw.nib, p != 0);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) l.a[st][p][mt][i][lane] = uint2{codes[2 * i], codes[2 * i + 1]};
+    const uint32_t ea = __builtin_amdgcn_ubfe(rw.sa, 8 * (lane & 3), 8);  // row t = lane % 4
+    PutByte(l.sa[st][mt / kTM][lane], (mt % kTM) * 2 + p, ea - (p ? 5u : 1u));
+    bad = ea - kSafeLo > kSafeHi - kSafeLo;
+  }
 #pragma unroll
   for (int k = 0; k < kWLoads; ++k) {
     const uint32_t u = t + kP * k, col = u % 256, half = (u >> 8) & 1;
@@ -314,25 +320,26 @@ __device__ __forceinline__ bool StoreRaw(const Raw<kWLoads>& rw, Lds<kMT, kW8>& 
   return bad;
 }
 
-// Producer/consumer split.  Threads [0, kBM*4) are producers: they stream
-// the raw A and W bytes through a ring of register sets, convert A (and W8)
-// into FP6 planes and stage the operands in LDS.  Threads [kBM*4, kBM*8) are
+// Producer/consumer split.  Threads [0, 512) are producers: they stream the
+// raw A and W bytes through a ring of register sets, convert A (and W8) into
+// FP6 planes and stage the operands in LDS.  Threads [512, 512 + kBM*4) are
 // consumers: they run the matrix cores and alone hold the accumulators.
-// Neither role needs more than 128 registers, so 16 waves share a CU, two
-// of each role per SIMD.  In iteration s the producers convert step s + 2;
+// Neither role needs more than 128 registers, so with 128-row tiles 16 waves
+// share a CU, two of each role per SIMD (64-row tiles: 8 producer and 4
+// consumer waves).  In iteration s the producers convert step s + 2;
 // the consumers issue step s's matrix work and then read step s + 1's
 // operands, whose latency hides under the matrix work.  One barrier per
 // iteration; with kU >= 3 LDS stages, the stage a producer writes in
 // iteration s was last read in iteration s - 2 or earlier.
 template <int kBM, bool kMulti, bool kW8>
-__global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
+__global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
   using F = Fmt<kW8>;
   constexpr int kMT = kBM / 32;
-  constexpr int kP = kBM * 4;  // producer threads
+  constexpr int kP = 512;  // producer threads
   constexpr int kWLoads = 512 * F::kWPlanes / kP;
   constexpr int kU = F::kU, kTM = F::kTM, kTN = F::kTN, kWP = F::kWPlanes;
   constexpr int kWavesM = kMT / kTM;  // consumer waves: kWavesM (rows) x 8 / kTN (columns)
-  static_assert(kWavesM * (8 / kTN) * 64 == kP && kTM * kTN == 4, "consumer wave grid");
+  static_assert(kWavesM * (8 / kTN) * 64 == kBM * 4 && kTM * kTN == 4, "consumer wave grid");
   static_assert(kU >= 3, "LDS stages");
   __shared__ __attribute__((aligned(16))) Lds<kMT, kW8> lds;
   __shared__ uint64_t lds_act[512];             // activation half of TBUF
@@ -455,7 +462,11 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
     }
   };
 
-  if (!consumer) {
+  // Producer waves: the first 2 * kMT convert A (and take a share of W),
+  // the rest (64-row tiles) only W.  The role is wave-uniform and fixed, so
+  // each role's loop is its own branch-free copy.
+  auto produce = [&](auto a_wave) {
+    constexpr bool kAWave = decltype(a_wave)::value;
     // Ring of kU raw register sets (slot t % kU holds step t): the set of
     // step s + 2 is converted in iteration s and its slot refilled with step
     // s + 2 + kU at once.  Loads issue in program order (the fences stop the
@@ -467,7 +478,7 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
     const Offsets<kWLoads> offs = ThreadOffsets<kP, kWLoads>(g, q0, g0, t);
     auto load = [&](Raw<kWLoads>& rw, uint32_t step) {
       __builtin_amdgcn_sched_barrier(0);
-      LoadRaw<kP, kWLoads, kMulti>(g, a, w0, w1, offs, t, s0, step, steps, nblocks, rw);
+      LoadRaw<kP, kWLoads, kMulti, kAWave>(g, a, w0, w1, offs, t, s0, step, steps, nblocks, rw);
       __builtin_amdgcn_sched_barrier(0);
     };
     // The epilogue's small operands (the activation table, the tile's
@@ -492,18 +503,19 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
     for (int i = 0; i < kU; ++i) load(ring[i], i);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      unsafe |= StoreRaw<kMT, kP, kWLoads, kW8>(ring[i], lds, i, t);
+      unsafe |= StoreRaw<kMT, kP, kWLoads, kW8, kAWave>(ring[i], lds, i, t);
       load(ring[i], i + kU);
     }
 #pragma unroll
     for (int k = 0; k < kActLoads; ++k) lds_act[t + kP * k] = act_v[k];
 #pragma unroll
-    for (int k = 0; k < kVecLoads; ++k) lds_vec[(t + kP * k) / kBN][(t + kP * k) % kBN] = __uint_as_float(vec_v[k]);
+    for (int k = 0; k < kVecLoads; ++k)
+      lds_vec[(t + kP * k) / kBN][(t + kP * k) % kBN] = __uint_as_float(vec_v[k]);
     __syncthreads();
     for (uint32_t step = 0; step < steps; step += kU) {
 #pragma unroll
       for (int i = 0; i < kU; ++i) {  // iteration step + i converts step + i + 2
-        unsafe |= StoreRaw<kMT, kP, kWLoads, kW8>(ring[(i + 2) % kU], lds, (i + 2) % kU, t);
+        unsafe |= StoreRaw<kMT, kP, kWLoads, kW8, kAWave>(ring[(i + 2) % kU], lds, (i + 2) % kU, t);
         load(ring[(i + 2) % kU], step + i + 2 + kU);
         __syncthreads();
       }
@@ -511,8 +523,16 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
     if (unsafe) lds_unsafe = 1;
     __syncthreads();
     __syncthreads();  // the consumers' outputs are in LDS
-    // producer wave v takes tiles 2 and 3 of consumer wave v
-    epilogue(t >> 6, t & 63, 32, 64, lds_unsafe != 0);
+    // producer wave v < 2 * kMT takes tiles 2 and 3 of consumer wave v
+    if (kAWave) epilogue(t >> 6, t & 63, 32, 64, lds_unsafe != 0);
+  };
+  if (!consumer) {
+    if constexpr (kMT * 2 == kP / 64) {
+      produce(std::true_type{});
+    } else {
+      if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < kMT * 2) produce(std::true_type{});
+      else produce(std::false_type{});
+    }
     return;
   }
 
@@ -663,7 +683,7 @@ __global__ __launch_bounds__(kBM * 8) void FastKernel(GemmArgs g) {
 template <int kBM, bool kMulti, bool kW8>
 void Launch(const GemmArgs& args, hipStream_t stream) {
   hipLaunchKernelGGL((FastKernel<kBM, kMulti, kW8>), dim3(args.gx * args.gy * args.gz),
-                     dim3(kBM * 8), 0, stream, args);
+                     dim3(512 + kBM * 4), 0, stream, args);
 }
 
 template <int kBM>

@@ -179,9 +179,8 @@ __device__ __forceinline__ Offsets<kWLoads> ThreadOffsets(const GemmArgs& g, uin
 }
 
 // Steps at or past `steps` reload the last step's words (cache hits) with the
-// activations masked to zero, so they add nothing.  Block offsets are uniform
-// and folded into the scalar base pointer; each load is one instruction on
-// (uniform base, 32-bit lane offset).
+// activations masked to zero, so they add nothing.  Each load is one
+// instruction on (uniform base, 32-bit lane offset).
 template <int kP, int kWLoads, bool kMulti, bool kAWave>
 __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, const uint8_t* w0,
                                         const uint8_t* w1, const Offsets<kWLoads>& o, uint32_t t,
@@ -192,10 +191,11 @@ __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, con
   const uint32_t ub0 = BlockOf<kMulti>(g, 2 * step) * kDdrWord;
   const uint32_t ub1 = BlockOf<kMulti>(g, min(2 * step + 1, nblocks - 1)) * kDdrWord;
   if constexpr (kAWave) {
-    const uint8_t* ab = a + ub0;                 // uniform
-    const uint32_t ao = o.a + (h ? ub1 - ub0 : 0u);  // ub1 - ub0 is uniform
-    const u32x4 v0 = *reinterpret_cast<const u32x4*>(ab + ao);
-    const u32x4 v1 = *reinterpret_cast<const u32x4*>(ab + ao + 16);
+    // the lane's block: a step's two blocks need not be in memory order (a
+    // piece list), so each lane addresses its own from the layer base
+    const uint32_t ub = h ? ub1 : ub0;
+    const u32x4 v0 = *reinterpret_cast<const u32x4*>(a + (o.a + ub));
+    const u32x4 v1 = *reinterpret_cast<const u32x4*>(a + (o.a + ub) + 16);
     // Applied at conversion time, not here: a select on the loaded registers
     // would make the compiler wait for the load right away.
     rw.nib = (live_step >= steps || (h && 2 * step + 1 >= nblocks)) ? 0u : 0x0F0F0F0Fu;
@@ -204,7 +204,7 @@ __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, con
       rw.a[i] = v0[i];
       rw.a[4 + i] = v1[i];
     }
-    rw.sa = *reinterpret_cast<const uint32_t*>(ab + (o.a_scale + (h ? ub1 - ub0 : 0u)));
+    rw.sa = *reinterpret_cast<const uint32_t*>(a + (o.a_scale + ub));
   }
 #pragma unroll
   for (int k = 0; k < kWLoads; ++k) {
@@ -710,6 +710,7 @@ hipError_t LaunchLinearFast(const GemmArgs& in, uint32_t batch, hipStream_t stre
   GemmArgs args = in;
   FastGrid(args, &args.gx, &args.gy, &args.tile_rows);
   args.gz = batch;
+  if (Fp4Eligible(args, args.tile_rows)) return LaunchFp4(args, stream);
   if (args.tile_rows == 128) LaunchRows<128>(args, stream);
   else LaunchRows<64>(args, stream);
   return hipGetLastError();

@@ -118,6 +118,10 @@ bool FastEligible(const GemmArgs& args);
 // tile.
 void FastGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy, uint32_t* tile_rows);
 hipError_t LaunchLinearFast(const GemmArgs& args, uint32_t batch, hipStream_t stream);
+// Streaming MXFP4 kernel (hb_fast4.hip) for 128-row tiles of plain layers
+// (no ops, no requantize, no K splits); `args` carries the tile grid.
+bool Fp4Eligible(const GemmArgs& args, uint32_t tile_rows);
+hipError_t LaunchFp4(const GemmArgs& args, hipStream_t stream);
 // Fast path for layers of at most 64 rows (hb_skinny.hip): split-K over the
 // waves of a workgroup, W streamed into registers.
 hipError_t LaunchLinearSkinny(const GemmArgs& args, uint32_t batch, hipStream_t stream);

@@ -331,12 +331,13 @@ def test_batched_layers_with_epilogue(gpu, w8, mode, quantize):
 @pytest.mark.parametrize("w8", [False, True])
 def test_fast_batched_pieces_and_onto(gpu, w8):
     """Fast mode over a piece list (the multi-piece kernel), starting from C,
-    with rows and columns that leave partial tiles, batched."""
+    with rows and columns that leave partial tiles, batched.  Step 3 pairs
+    block 19 with block 0 (a step's blocks out of memory order)."""
     rng = np.random.default_rng(63 + w8)
     layers, m, n, k = 3, 160, 320, 640
     data = [make_layer(rng, m, n, k, w8) for _ in range(layers)]
     kb, modes = data[0][0], data[0][3]
-    pieces = [(12, 8), (0, 5), (5, 7)]
+    pieces = [(13, 7), (0, 5), (5, 8)]
     onto = np.stack([helpers.random_fp32_words(rng, (m, n), 120, 130) for _ in range(layers)])
     a_all = dev(np.stack([d[1] for d in data]))
     w_all = [dev(np.stack([d[2][p] for d in data])) for p in range(len(modes))]
@@ -349,6 +350,33 @@ def test_fast_batched_pieces_and_onto(gpu, w8):
     got = host(c_all).view(np.uint32)
     for i, d in enumerate(data):
         want, _ = oracle_linear(m, n, kb, d[1], d[2], d[3], pieces=pieces, onto=onto[i])
+        g = got[i].view(np.float32).astype(np.float64)
+        w = want.view(np.float32).astype(np.float64)
+        row_scale = np.abs(w).max(axis=1, keepdims=True)
+        assert (np.abs(g - w) <= 1e-5 * row_scale).all(), float((np.abs(g - w) / row_scale).max())
+
+
+@pytest.mark.parametrize("m,k,pieces", [(130, 416, None), (257, 640, [(11, 3), (0, 6)])])
+def test_fast_batched_odd_blocks_partial_tiles(gpu, m, k, pieces):
+    """MXFP4 layers of more than 64 rows (128-row tiles) with an odd number
+    of K blocks (the last step's second block is padding), rows not a
+    multiple of 4 and a partly used last column tile, batched.  With the
+    piece list, step 1 pairs block 13 with block 0."""
+    rng = np.random.default_rng(66 + m)
+    layers, n = 3, 296
+    data = [make_layer(rng, m, n, k, False) for _ in range(layers)]
+    kb, modes = data[0][0], data[0][3]
+    a_all = dev(np.stack([d[1] for d in data]))
+    w_all = dev(np.stack([d[2][0] for d in data]))
+    c_all = torch.zeros((layers, m, n), dtype=torch.float32, device=DEV)
+    descs = [hb.linear_desc(m, n, kb, a_all[i], [w_all[i]], modes, c_all[i], pieces=pieces,
+                            mode=hb.FAST) for i in range(layers)]
+    torch.cuda.synchronize()
+    say("fast batched odd blocks", dict(m=m, k=k, pieces=pieces))
+    hb.linear_batched(descs, gpu)
+    got = host(c_all).view(np.uint32)
+    for i, d in enumerate(data):
+        want, _ = oracle_linear(m, n, kb, d[1], d[2], d[3], pieces=pieces)
         g = got[i].view(np.float32).astype(np.float64)
         w = want.view(np.float32).astype(np.float64)
         row_scale = np.abs(w).max(axis=1, keepdims=True)

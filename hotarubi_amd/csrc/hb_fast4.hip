@@ -45,7 +45,7 @@ typedef _Float16 f16x32 __attribute__((ext_vector_type(32)));
 
 constexpr int kBM = 128, kBN = 256;
 constexpr int kP = 256;    // producer threads
-constexpr int kRing = 8;   // raw register sets per producer thread (= loop unroll, even)
+constexpr int kU = 4;      // raw register sets per producer thread = loop unroll (even)
 constexpr uint32_t kSafeLo = 70, kSafeHi = 179;
 
 constexpr int kOutPitch = kBN + 8;  // floats: rows r and r + 4 fall on disjoint LDS banks
@@ -124,37 +124,75 @@ __device__ __forceinline__ void SplitA(const uint32_t* x, uint32_t mask, uint4* 
   out[2] = uint4{lo[2], lo[3], lo[4], lo[5]};
 }
 
+// Logical tiles of one workgroup: first + k * stride, k < count.  With more
+// tiles than workgroups (one per CU), each XCD (workgroups b with b % 8 = x;
+// the hardware deals workgroups round-robin over the 8 XCDs) takes one
+// contiguous eighth of the tiles, so the tiles in flight on an XCD are
+// neighbours (the column tiles of a layer share A in that XCD's L2).
+struct Schedule {
+  uint32_t first, stride, count;
+};
+__device__ __forceinline__ Schedule TilesOf(uint32_t total) {
+  const uint32_t b = blockIdx.x, grid = gridDim.x;
+  Schedule sc;
+  if (grid >= total) {  // one tile each, remapped as LogicalTile does
+    sc.first = total % kXcds == 0 ? (b % kXcds) * (total / kXcds) + b / kXcds : b;
+    sc.stride = 1;
+    sc.count = 1;
+    return sc;
+  }
+  const uint32_t per = grid / kXcds, x = b % kXcds, idx = b / kXcds;  // grid % 8 == 0
+  const uint32_t lo = (uint32_t)((uint64_t)x * total / kXcds);
+  const uint32_t hi = (uint32_t)((uint64_t)(x + 1) * total / kXcds);
+  sc.first = lo + idx;
+  sc.stride = per;
+  sc.count = hi > sc.first ? (hi - sc.first + per - 1) / per : 0u;
+  return sc;
+}
+
+// Persistent: a workgroup runs its tiles back to back.  The K loop of every
+// tile has `iters` iterations (the steps rounded up to kU; surplus steps add
+// zeros), and the producers' ring streams straight across tile boundaries:
+// global iteration u (tile u / iters) stages global step u + 2 and loads
+// ahead in bursts, so the next tile's first steps are in LDS when a tile
+// ends, and its epilogue (in LDS outside the stages) overlaps nothing but
+// its own stores.  Out-of-window scale bytes are flagged per tile (bit k % 2).
 template <bool kMulti>
 __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) union {
-    Stage stage[2];
-    float out[kBM][kOutPitch];  // after the K loop: the tile's outputs
-  } lds;
-  __shared__ uint32_t lds_unsafe;
+  __shared__ __attribute__((aligned(16))) Stage lds_stage[2];
+  __shared__ __attribute__((aligned(16))) float lds_out[kBM / 2][kOutPitch];  // half a tile
+  __shared__ uint32_t lds_unsafe[2];
 
-  const TileId tile = LogicalTile(g.gx, g.gy, g.gz);
-  const uint32_t z = tile.z;
-  const uint8_t* a = g.a + z * g.a_batch;
-  const uint8_t* w0 = g.w[0] + z * g.w_batch;
-  uint32_t* c = g.c + z * g.c_batch;
-
+  const Schedule sc = TilesOf(g.gx * g.gy * g.gz);
   const bool consumer = __builtin_amdgcn_readfirstlane(threadIdx.x >= kP);  // wave-uniform
-  const uint32_t q0 = tile.y * (kBM / 4), g0 = tile.x * (kBN / 8);
-  const uint32_t row0 = q0 * 4, col0 = g0 * 8;
-
   uint32_t nblocks = 0;
   for (uint32_t p = 0; p < g.n_pieces; ++p) nblocks += g.piece_kb[p];
-  const uint32_t steps = (nblocks + 1) / 2;  // both roles run this many iterations
+  const uint32_t steps = (nblocks + 1) / 2;
+  const uint32_t iters = (steps + kU - 1) / kU * kU;  // per tile, both roles
 
-  // Wave v of 8 stores tile rows v, v + 8, ...: lane l the 4 columns 4l ..
-  // 4l + 3 (n is a multiple of 8, so 4 columns are all in or all out).
-  auto store_rows = [&](uint32_t v) {
-    const uint32_t l = threadIdx.x & 63, col = col0 + 4 * l;
+  struct Tile {
+    uint32_t row0, col0, z;
+  };
+  auto tile_of = [&](uint32_t k) {
+    const uint32_t t = sc.first + k * sc.stride;
+    Tile tl;
+    tl.col0 = (t % g.gx) * kBN;
+    tl.row0 = ((t / g.gx) % g.gy) * kBM;
+    tl.z = t / (g.gx * g.gy);
+    return tl;
+  };
+  // Wave v of 8 stores rows v, v + 8, .. of half `half` of tile k: lane l
+  // the 4 columns 4l .. 4l + 3 (n is a multiple of 8: all in or all out).
+  auto store_half = [&](uint32_t k, uint32_t half, uint32_t v) {
+    const Tile tl = tile_of(k);
+    uint32_t* c = g.c + tl.z * g.c_batch;
+    const uint32_t l = threadIdx.x & 63, col = tl.col0 + 4 * l;
     if (col >= g.n) return;
-    for (uint32_t r = v; r < kBM; r += 8) {
-      if (row0 + r >= g.m) break;
-      const float4 val = *reinterpret_cast<const float4*>(&lds.out[r][4 * l]);
-      *reinterpret_cast<float4*>(c + (size_t)(row0 + r) * g.n + col) = val;
+    for (uint32_t r = v; r < kBM / 2; r += 8) {
+      const uint32_t row = tl.row0 + half * (kBM / 2) + r;
+      if (row >= g.m) break;
+      const float4 val = *reinterpret_cast<const float4*>(&lds_out[r][4 * l]);
+      *reinterpret_cast<float4*>(c + (size_t)row * g.n + col) = val;
     }
   };
 
@@ -162,18 +200,33 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
     const uint32_t t = threadIdx.x, lane = t & 63, mt = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t h = lane >> 5;  // the A lane's block within the step
     const uint32_t word_row = g.kb_total * kDdrWord;
-    const uint32_t r = mt * 32 + (lane & 31);
-    const uint32_t quad = min(q0 + (r >> 2), g.quads - 1);
-    const uint32_t o_a = quad * word_row + (r & 3) * 32, o_sa = quad * word_row + 128;
-    const uint32_t grp = min(g0 + (t >> 3), g.groups - 1), cl = t & 7;
-    const uint32_t o_w = grp * word_row + cl * 16, o_sw = grp * word_row + 128 + (cl & 4);
+    const uint32_t r = mt * 32 + (lane & 31), cl = t & 7;
 
-    // Steps at or past `steps` reload the last step's words (cache hits)
-    // with A masked to zero.  Each load is one instruction on (uniform
-    // base, 32-bit lane offset).
-    auto load = [&](Raw& rw, uint32_t live) {
+    // Load cursor: tile lk (clamped to the last), step ls; per-tile byte
+    // offsets cached while the cursor stays on one tile.
+    uint32_t lk = 0, ls = 0, cached = ~0u;
+    const uint8_t *a = nullptr, *w0 = nullptr;
+    uint32_t o_a = 0, o_sa = 0, o_w = 0, o_sw = 0;
+    // Steps past a tile's end (and past the last tile) reload a valid step
+    // with A masked to zero.  Each load is one instruction on (uniform base,
+    // 32-bit lane offset).
+    auto load = [&](Raw& rw) {
       __builtin_amdgcn_sched_barrier(0);
-      const uint32_t step = min(live, steps - 1);
+      const uint32_t k = min(lk, sc.count - 1);
+      if (k != cached) {  // uniform
+        cached = k;
+        const Tile tl = tile_of(k);
+        a = g.a + tl.z * g.a_batch;
+        w0 = g.w[0] + tl.z * g.w_batch;
+        const uint32_t quad = min(tl.row0 / 4 + (r >> 2), g.quads - 1);
+        o_a = quad * word_row + (r & 3) * 32;
+        o_sa = quad * word_row + 128;
+        const uint32_t grp = min(tl.col0 / 8 + (t >> 3), g.groups - 1);
+        o_w = grp * word_row + cl * 16;
+        o_sw = grp * word_row + 128 + (cl & 4);
+      }
+      const bool live = lk < sc.count && ls < steps;
+      const uint32_t step = min(ls, steps - 1);
       const uint32_t ub0 = BlockOf<kMulti>(g, 2 * step) * kDdrWord;
       const uint32_t ub1 = BlockOf<kMulti>(g, min(2 * step + 1, nblocks - 1)) * kDdrWord;
       // the lane's block: a step's two blocks need not be in memory order
@@ -188,13 +241,17 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
       rw.sw[1] = *reinterpret_cast<const uint32_t*>(w0 + ub1 + o_sw);
       // applied at conversion time: a select on the loaded registers here
       // would make the compiler wait for the loads at once
-      rw.mask = (live >= steps || (h && 2 * step + 1 >= nblocks)) ? 0u : 0xFFFFFFFFu;
+      rw.mask = (!live || (h && 2 * step + 1 >= nblocks)) ? 0u : 0xFFFFFFFFu;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         rw.a[i] = v0[i];
         rw.a[4 + i] = v1[i];
         rw.w[0][i] = x0[i];
         rw.w[1][i] = x1[i];
+      }
+      if (++ls == iters) {
+        ls = 0;
+        ++lk;
       }
       __builtin_amdgcn_sched_barrier(0);
     };
@@ -219,58 +276,62 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
       return bad;
     };
 
-    Raw ring[kRing];
-    bool unsafe = false;
-    if (t == 0) lds_unsafe = 0;
+    // Convert cursor: the tile (parity) of the step being staged, for the
+    // out-of-window flags (bit k % 2 of `flags`).
+    uint32_t ck = 0, cs = 0, flags = 0;
+    auto stage = [&](const Raw& rw, Stage& st) {
+      if (store(rw, st) && ck < sc.count) flags |= 1u << (ck & 1);
+      if (++cs == iters) {
+        cs = 0;
+        ++ck;
+      }
+    };
+    // Ring of kU register sets, slot j % kU holding global step j: iteration
+    // u stages step u + 2 and refills its slot with step u + 2 + kU.
+    Raw ring[kU];
+    if (t < 2) lds_unsafe[t] = 0;
 #pragma unroll
-    for (int i = 0; i < kRing; ++i) load(ring[i], i);
+    for (int i = 0; i < kU; ++i) load(ring[i]);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      unsafe |= store(ring[i], lds.stage[i]);
-      load(ring[i], i + kRing);
+      stage(ring[i], lds_stage[i]);
+      load(ring[i]);
     }
-    __syncthreads();  // steps 0 and 1 staged
+    __syncthreads();  // global steps 0 and 1 staged
     __syncthreads();  // the consumers hold step 0: its stage may be refilled
-    for (uint32_t s = 0; s < steps; s += kRing) {
+    for (uint32_t k = 0; k < sc.count; ++k) {
+      for (uint32_t s = 0; s < iters; s += kU) {
 #pragma unroll
-      for (int i = 0; i < kRing; ++i) {  // iteration s + i stages step s + i + 2
-        if (s + i >= steps) break;
-        unsafe |= store(ring[(i + 2) % kRing], lds.stage[i % 2]);
-        load(ring[(i + 2) % kRing], s + i + 2 + kRing);
-        __syncthreads();
+        for (int i = 0; i < kU; ++i) {  // global iteration u stages step u + 2
+          stage(ring[(i + 2) % kU], lds_stage[i % 2]);
+          load(ring[(i + 2) % kU]);
+          __syncthreads();
+        }
       }
+      // epilogue of tile k (all tile k steps are staged; its flag is final)
+      if (flags & (1u << (k & 1))) lds_unsafe[k & 1] = 1;
+      flags &= ~(1u << (k & 1));
+      __syncthreads();  // E0: flags in
+      __syncthreads();  // E1: rows 0-63 in LDS
+      store_half(k, 0, t >> 6);
+      __syncthreads();  // E2: half 0 read out
+      __syncthreads();  // E3: rows 64-127 in LDS
+      store_half(k, 1, t >> 6);
     }
-    if (unsafe) lds_unsafe = 1;
-    __syncthreads();  // the flags are in
-    __syncthreads();  // the outputs are in LDS
-    store_rows(t >> 6);
     return;
   }
 
   // Consumer wave cw: rows 64 * (cw % 2) .. + 64 (m-tiles 2 wm, 2 wm + 1),
   // columns 128 * (cw / 2) .. + 128 (n-tiles 4 wn .. 4 wn + 3).  MFMA tile
-  // j = mi * 4 + nj.
+  // j = mi * 4 + nj.  Output r of tile j of this lane is tile row
+  // 32 (2 wm + j / 4) + 4 (lane / 32) + 8 (r / 4) + r % 4, column
+  // 32 (4 wn + j % 4) + lane % 32.
   const uint32_t tid = threadIdx.x - kP, lane = tid & 63;
   const uint32_t cw = __builtin_amdgcn_readfirstlane(tid >> 6), wm = cw & 1, wn = cw >> 1;
-  auto row_of = [&](uint32_t mi, uint32_t r) {
-    return row0 + (2 * wm + mi) * 32 + 4 * (lane >> 5) + 8 * (r / 4) + (r & 3);
+  auto trow = [&](uint32_t mi, uint32_t r) {
+    return (2 * wm + mi) * 32 + 4 * (lane >> 5) + 8 * (r / 4) + (r & 3);
   };
-  auto col_of = [&](uint32_t nj) { return col0 + (4 * wn + nj) * 32 + (lane & 31); };
-
-  f32x16 acc[8];
-  bool unsafe = false;
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const uint32_t row = row_of(j / 4, r), col = col_of(j % 4);
-      uint32_t init = 0;
-      if (g.acc && row < g.m && col < g.n) {
-        init = c[(size_t)row * g.n + col];
-        unsafe |= ExpField(init) > 252u;
-      }
-      acc[j][r] = __uint_as_float(init);
-    }
+  auto tcol = [&](uint32_t nj) { return (4 * wn + nj) * 32 + (lane & 31); };
 
   struct Ops {
     i32x8 a[2][2];  // [mi][plane]
@@ -293,6 +354,7 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
     o.sa = (int)st.sa[wm][lane];
     o.sb = (int)st.sw[wn][lane];
   };
+  f32x16 acc[8];
   auto matrix = [&](const Ops& o) {
     Unroll<2>([&](auto p) {
       Unroll<8>([&](auto j) {
@@ -303,14 +365,14 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
       });
     });
   };
-  // Iteration s: read step s + 1 (stage st) into `nxt`, run step s from
-  // `cur`, then the barrier (which waits for the reads).  The accumulators
-  // are anchored on both sides of the barrier (the empty asm emits nothing),
-  // so the compiler neither sinks the matrix work past it nor hoists the
-  // next step's above it.
+  // Iteration: read the next step (stage st) into `nxt`, run this step
+  // from `cur`, then the barrier (which waits for the reads).  The
+  // accumulators are anchored on both sides of the barrier (the empty asm
+  // emits nothing), so the compiler neither sinks the matrix work past it
+  // nor hoists the next step's above it.
   auto iteration = [&](const Ops& cur, Ops& nxt, int st) {
     __builtin_amdgcn_sched_barrier(0);
-    read(lds.stage[st], nxt);
+    read(lds_stage[st], nxt);
     __builtin_amdgcn_sched_barrier(0);
     matrix(cur);
 #pragma unroll
@@ -322,42 +384,73 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
   };
 
   Ops x, y;
-  __syncthreads();  // steps 0 and 1 staged; the flag is clear
-  if (unsafe) lds_unsafe = 1;
-  read(lds.stage[0], x);
+  __syncthreads();  // global steps 0 and 1 staged; the flags are clear
+  read(lds_stage[0], x);
   __syncthreads();  // step 0 is in registers before producers refill its stage
-  for (uint32_t s = 0; s < steps; s += kRing) {
+  for (uint32_t k = 0; k < sc.count; ++k) {
+    const Tile tl = tile_of(k);
+    const uint8_t* a = g.a + tl.z * g.a_batch;
+    const uint8_t* w0 = g.w[0] + tl.z * g.w_batch;
+    uint32_t* c = g.c + tl.z * g.c_batch;
+    if (g.acc) {  // uniform: start from C
+      bool unsafe = false;
 #pragma unroll
-    for (int i = 0; i < kRing; i += 2) {
-      if (s + i >= steps) break;
-      iteration(x, y, 1);
-      if (s + i + 1 >= steps) break;
-      iteration(y, x, 0);
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t row = tl.row0 + trow(j / 4, r), col = tl.col0 + tcol(j % 4);
+          uint32_t init = 0;
+          if (row < g.m && col < g.n) {
+            init = c[(size_t)row * g.n + col];
+            unsafe |= ExpField(init) > 252u;
+          }
+          acc[j][r] = __uint_as_float(init);
+        }
+      if (unsafe) lds_unsafe[k & 1] = 1;  // read after E0 of this tile
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
     }
-  }
-  __syncthreads();  // the producers' flags are in; the stages are free
-  const bool slow = lds_unsafe != 0;
-  // Output r of MFMA tile j of this lane is tile row 32 (2 wm + j / 4) +
-  // 4 (lane / 32) + 8 (r / 4) + r % 4, column 32 (4 wn + j % 4) + lane % 32.
-  if (slow) {  // a scale byte left the window: every output of the tile exactly
-    for (uint32_t j = 0; j < 8; ++j)
-      for (uint32_t r = 0; r < 16; ++r) {
-        const uint32_t row = row_of(j / 4, r), col = col_of(j % 4);
-        if (row >= g.m || col >= g.n) continue;
-        const uint32_t init = g.acc ? c[(size_t)row * g.n + col] : 0u;
-        lds.out[row - row0][col - col0] = __uint_as_float(SlowLinear(g, a, w0, w0, init, row, col));
+    for (uint32_t s = 0; s < iters; s += kU) {
+#pragma unroll
+      for (int i = 0; i < kU; i += 2) {
+        iteration(x, y, 1);
+        iteration(y, x, 0);
       }
-  } else {
-    // Adding +0 maps -0 to +0 (and a denormal sum, in the kernel's
-    // flush-to-zero mode, to +0).
+    }
+    __syncthreads();  // E0: the producers' flags for tile k are in
+    const bool slow = lds_unsafe[k & 1] != 0;
+    // Half `half` of the tile (rows 64 half ..) belongs to the waves with
+    // wm == half.  Adding +0 maps -0 to +0 (and a denormal sum, in the
+    // kernel's flush-to-zero mode, to +0).
+    auto park = [&](uint32_t half) {
+      if (wm != half) return;
+      if (slow) {  // a scale byte left the window: every output exactly
+        for (uint32_t j = 0; j < 8; ++j)
+          for (uint32_t r = 0; r < 16; ++r) {
+            const uint32_t row = tl.row0 + trow(j / 4, r), col = tl.col0 + tcol(j % 4);
+            if (row >= g.m || col >= g.n) continue;
+            const uint32_t init = g.acc ? c[(size_t)row * g.n + col] : 0u;
+            lds_out[trow(j / 4, r) - 64 * half][tcol(j % 4)] =
+                __uint_as_float(SlowLinear(g, a, w0, w0, init, row, col));
+          }
+        return;
+      }
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < 8; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        lds.out[row_of(j / 4, r) - row0][col_of(j % 4) - col0] = acc[j][r] + 0.0f;
+        for (int r = 0; r < 16; ++r)
+          lds_out[trow(j / 4, r) - 64 * half][tcol(j % 4)] = acc[j][r] + 0.0f;
+    };
+    park(0);
+    __syncthreads();  // E1: rows 0-63 in LDS
+    if (tid == 0) lds_unsafe[k & 1] = 0;  // every consumer wave has read it
+    store_half(k, 0, 4 + cw);
+    __syncthreads();  // E2: half 0 read out
+    park(1);
+    __syncthreads();  // E3: rows 64-127 in LDS
+    store_half(k, 1, 4 + cw);
   }
-  __syncthreads();  // the outputs are in LDS
-  store_rows(4 + cw);
 }
 
 }  // namespace
@@ -368,7 +461,21 @@ bool Fp4Eligible(const GemmArgs& args, uint32_t tile_rows) {
 }
 
 hipError_t LaunchFp4(const GemmArgs& args, hipStream_t stream) {
-  const dim3 grid(args.gx * args.gy * args.gz), block(512);
+  // one workgroup per CU (a multiple of the 8 XCDs), or one per tile
+  static int cus[64] = {};
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  if (cus[dev] == 0) {
+    int n = 0;
+    err = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return err;
+    cus[dev] = n / (int)kXcds * (int)kXcds;
+    if (cus[dev] == 0) cus[dev] = (int)kXcds;
+  }
+  const uint32_t tiles = args.gx * args.gy * args.gz;
+  const dim3 grid(tiles < (uint32_t)cus[dev] ? tiles : (uint32_t)cus[dev]), block(512);
   if (args.n_pieces > 1) hipLaunchKernelGGL((Fp4Kernel<true>), grid, block, 0, stream, args);
   else hipLaunchKernelGGL((Fp4Kernel<false>), grid, block, 0, stream, args);
   return hipGetLastError();

@@ -383,6 +383,40 @@ def test_fast_batched_odd_blocks_partial_tiles(gpu, m, k, pieces):
         assert (np.abs(g - w) <= 1e-5 * row_scale).all(), float((np.abs(g - w) / row_scale).max())
 
 
+def test_fast_many_tiles_per_workgroup(gpu):
+    """More 128-row MXFP4 tiles than CUs (300 tiles over 25 layers): each
+    workgroup runs several tiles back to back.  Starting from C, an odd
+    number of K blocks, a partly used last column tile, and one row tile of
+    one layer with an out-of-window scale byte (that tile exact, bit for
+    bit; its neighbours within tolerance)."""
+    rng = np.random.default_rng(67)
+    layers, m, n, k = 25, 260, 1000, 160
+    data = [make_layer(rng, m, n, k, False) for _ in range(layers)]
+    kb, modes = data[0][0], data[0][3]
+    bad_layer = 12
+    a_bad = data[bad_layer][1].copy()
+    a_bad.reshape(-1, kb, 144)[5, 2, 128] = 60  # row 20 (row tile 0), block 2
+    data[bad_layer] = (kb, a_bad, data[bad_layer][2], modes)
+    onto = np.stack([helpers.random_fp32_words(rng, (m, n), 120, 130) for _ in range(layers)])
+    a_all = dev(np.stack([d[1] for d in data]))
+    w_all = dev(np.stack([d[2][0] for d in data]))
+    c_all = dev(onto.view(np.float32))
+    descs = [hb.linear_desc(m, n, kb, a_all[i], [w_all[i]], modes, c_all[i], onto=True,
+                            mode=hb.FAST) for i in range(layers)]
+    torch.cuda.synchronize()
+    say("fast many tiles", dict(layers=layers, m=m, n=n, k=k))
+    hb.linear_batched(descs, gpu)
+    got = host(c_all).view(np.uint32)
+    for i, d in enumerate(data):
+        want, _ = oracle_linear(m, n, kb, d[1], d[2], d[3], onto=onto[i])
+        if i == bad_layer:
+            assert_bits(got[i][:128], want[:128])
+        g = got[i].view(np.float32).astype(np.float64)
+        w = want.view(np.float32).astype(np.float64)
+        row_scale = np.abs(w).max(axis=1, keepdims=True)
+        assert (np.abs(g - w) <= 1e-5 * row_scale).all(), (i, float((np.abs(g - w) / row_scale).max()))
+
+
 @pytest.mark.parametrize("w8", [False, True])
 def test_fast_out_of_window_scales_recompute_exactly(gpu, w8):
     """Row tiles whose scale bytes leave the fast path's window recompute

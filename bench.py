@@ -471,8 +471,7 @@ def main():
 
     work = Workload(hb, torch, args.m, n, kb, False, args.layers, mode)
     ms = time_steps(hb, torch, ctx, stream, work, args.steps, args.warmup)
-    tag = ("FastKernel<128,false,false>" if args.m > 64 else "FastKernel<64,false,false>") \
-        if fast else "GemmTileKernel<linear,128,128>"
+    tag = "Fp4Kernel<false>" if fast else "GemmTileKernel<linear,128,128>"
     tops, roof = summarize(work, ms, "fp6_fp4" if fast else "bf16",
                            tag if (args.m == 128 and args.layers == 256) else None)
     del work

@@ -102,6 +102,41 @@ def cpu_baseline(m, n, kb, budget_s=15.0):
                       f"median {t:.3f} s"}
 
 
+def cpu_baseline_cores(m, n, kb, budget_s=10.0):
+    """The same layer on several host threads, each running the oracle over
+    its own slice of column groups (independent in the reference's loop nest,
+    gemm_array.cpp:123-147).  Threads: the host's cores, at most 16 (one
+    GPU's share of a GPU box's cores)."""
+    import oracle
+    from concurrent.futures import ThreadPoolExecutor
+    rng = np.random.default_rng(7)
+    a, w = make_inputs(rng, m, n, kb)
+    groups = n // 8
+    threads = max(1, min(16, os.cpu_count() or 1, groups))
+    bounds = [groups * i // threads for i in range(threads + 1)]
+    w0 = w[0].reshape(groups, kb, 144)
+    slices = [np.ascontiguousarray(w0[bounds[i]:bounds[i + 1]]).reshape(-1, 144)
+              for i in range(threads)]
+
+    def part(i):  # ctypes releases the GIL for the duration of the call
+        oracle.linear(m, 8 * (bounds[i + 1] - bounds[i]), kb, a, [slices[i]], [0])
+
+    times = []
+    t_end = time.perf_counter() + budget_s
+    with ThreadPoolExecutor(threads) as pool:
+        while True:
+            t0 = time.perf_counter()
+            list(pool.map(part, range(threads)))
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() + times[-1] > t_end or len(times) >= 5:
+                break
+    t = float(np.median(times))
+    return {"value": round(2.0 * m * n * kb * 32 / t / 1e12, 6), "unit": "TOPS", "cores": threads,
+            "kind": "port",
+            "sample": f"{len(times)} run(s) of one {m}x{kb * 32}x{n} MXFP4 layer (exact fold) "
+                      f"over {threads} threads by column groups, median {t:.3f} s"}
+
+
 def counted_traffic(kernel_tag):
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE, calibrated against
@@ -559,6 +594,7 @@ def main():
 
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.m, n, kb)
+        out["cpu_baseline_cores"] = cpu_baseline_cores(args.m, n, kb)
     print(json.dumps(out), flush=True)
     ctx.close()
 

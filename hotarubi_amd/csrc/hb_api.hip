@@ -646,3 +646,57 @@ int hb_encode_mxint8(hb_ctx* ctx, const float* x, uint32_t rows, uint32_t cols, 
 }
 
 }  // extern "C"
+
+namespace {
+
+int DmaSplit(hb_ctx* ctx, const void* src, uint64_t stride, uint32_t rows, uint32_t row_words,
+             void* hi, void* lo, bool t32, bool sync) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!src || !hi || !lo || rows < 1 || row_words < 1)
+    return Fail(HB_EINVAL, "bad %s arguments", t32 ? "T32_SPLIT8" : "SPLIT8");
+  if (stride % 16 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(hi) % 16 != 0 || reinterpret_cast<uintptr_t>(lo) % 16 != 0)
+    return Fail(HB_EINVAL, "%s buffers must be 16-byte aligned with a stride of whole 16-byte beats",
+                t32 ? "T32_SPLIT8" : "SPLIT8");
+  if (stride < (uint64_t)row_words * hb::kDdrWord)
+    return Fail(HB_EINVAL, "%s row stride %llu is shorter than %u words",
+                t32 ? "T32_SPLIT8" : "SPLIT8", (unsigned long long)stride, row_words);
+  // the reference's Require texts (dma_engine.cpp:305-306, 380-382)
+  if (!t32 && rows % 2 != 0) return Fail(HB_EBADCMD, "SPLIT8 with an odd number of rows %u", rows);
+  if (t32 && rows % 8 != 0)
+    return Fail(HB_EBADCMD, "T32_SPLIT8 with %u rows, not a multiple of 8", rows);
+  const uint8_t* s = static_cast<const uint8_t*>(src);
+  uint8_t* h = static_cast<uint8_t*>(hi);
+  uint8_t* l = static_cast<uint8_t*>(lo);
+  const hipError_t err = t32 ? hb::LaunchT32Split8(s, stride, rows, row_words, h, l, ctx->stream)
+                             : hb::LaunchSplit8(s, stride, rows, row_words, h, l, ctx->stream);
+  if (err != hipSuccess) return HipFail(err, t32 ? "T32_SPLIT8 launch" : "SPLIT8 launch");
+  if (sync) HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hb_split8(hb_ctx* ctx, const void* src, uint64_t src_stride, uint32_t rows, uint32_t row_words,
+              void* hi, void* lo) {
+  return DmaSplit(ctx, src, src_stride, rows, row_words, hi, lo, false, true);
+}
+
+int hb_split8_async(hb_ctx* ctx, const void* src, uint64_t src_stride, uint32_t rows,
+                    uint32_t row_words, void* hi, void* lo) {
+  return DmaSplit(ctx, src, src_stride, rows, row_words, hi, lo, false, false);
+}
+
+int hb_t32_split8(hb_ctx* ctx, const void* src, uint64_t src_stride, uint32_t rows,
+                  uint32_t row_words, void* hi, void* lo) {
+  return DmaSplit(ctx, src, src_stride, rows, row_words, hi, lo, true, true);
+}
+
+int hb_t32_split8_async(hb_ctx* ctx, const void* src, uint64_t src_stride, uint32_t rows,
+                        uint32_t row_words, void* hi, void* lo) {
+  return DmaSplit(ctx, src, src_stride, rows, row_words, hi, lo, true, false);
+}
+
+}  // extern "C"

@@ -130,6 +130,12 @@ void ExactGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy);
 // Deferred epilogue (hb_vec.hip): reads args.ws, writes C and q_out.
 hipError_t LaunchEpilogue(const GemmArgs& args, hipStream_t stream);
 
+// DMA-engine W8 operand builders (hb_dma.hip).
+hipError_t LaunchSplit8(const uint8_t* src, uint64_t stride, uint32_t rows, uint32_t row_words,
+                        uint8_t* hi, uint8_t* lo, hipStream_t stream);
+hipError_t LaunchT32Split8(const uint8_t* src, uint64_t stride, uint32_t rows, uint32_t row_words,
+                           uint8_t* hi, uint8_t* lo, hipStream_t stream);
+
 // VEC (hb_vec.hip).
 struct VecPass {
   uint32_t src, src2, d;   // register values (src, src2 masked to 12 bits)

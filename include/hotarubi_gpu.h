@@ -239,6 +239,49 @@ int hb_linear_async(hb_ctx* ctx, const hb_linear_desc* desc);
 int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* descs,
                             uint32_t count);
 
+/* --------------------------------------------- attention W8 operands -- */
+
+/* The DMA engine's on-chip W8 operand builders, over DDR words already in
+ * device memory: they make the K and V^T operands of the attention GEMMs
+ * (QK^T and PV, tools/compiler/kernels.cpp:155-244) in the W8 plane layout
+ * hb_linear takes (modes 1, 2: planes hi then lo).
+ *
+ * src: `rows` rows of `row_words` MXINT8 words (144 B: 4 tokens x 32 int8,
+ * the 4 token scales at byte 128, padding), row r at byte r * src_stride.
+ * src, hi, lo 16-byte aligned, src_stride a multiple of 16 (the DMA's beat)
+ * and at least row_words * 144, rows and row_words at least 1; otherwise
+ * HB_EINVAL.
+ *
+ * hb_split8 replaces LoadSplit8 (tools/iss/dma_engine.cpp:303-333): rows 2p
+ * and 2p + 1 at word position w become plane words (p, w) of hi and lo,
+ * [rows/2][row_words] x 144 B each (kb_total = row_words); token j of row
+ * 2p + r is column 4r + j, its int8's high nibble goes to hi and low nibble
+ * to lo, the token scales are copied, bytes 136..143 are zero.  An odd
+ * `rows` returns HB_EBADCMD with the reference's text
+ * ("SPLIT8 with an odd number of rows N").
+ *
+ * hb_t32_split8 replaces LoadT32 / TransposeGroup (dma_engine.cpp:336-398):
+ * the planes of the transpose.  Each group of 8 rows (32 tokens) and word
+ * position w is a 32 x 32 block; dimension d becomes column d % 8 of column
+ * group 4w + d / 8 and the token its K position.  emax is the largest scale
+ * among the block's tokens with a nonzero element (127 if none); each
+ * element becomes AlignElement(q, emax - e_t) = RNE(q / 2^(emax - e_t)), 0
+ * for a shift of 9 or more or an all-zero token (dma_engine.cpp:532-544);
+ * all 8 column scales are emax.  hi, lo: [4 * row_words][rows / 8] x 144 B
+ * (kb_total = rows / 8).  `rows` not a multiple of 8 returns HB_EBADCMD
+ * ("T32_SPLIT8 with N rows, not a multiple of 8").
+ *
+ * The _async forms are ordered on the context's stream; the others return
+ * once the planes are written. */
+int hb_split8(hb_ctx* ctx, const void* src, uint64_t src_stride, uint32_t rows,
+              uint32_t row_words, void* hi, void* lo);
+int hb_split8_async(hb_ctx* ctx, const void* src, uint64_t src_stride, uint32_t rows,
+                    uint32_t row_words, void* hi, void* lo);
+int hb_t32_split8(hb_ctx* ctx, const void* src, uint64_t src_stride, uint32_t rows,
+                  uint32_t row_words, void* hi, void* lo);
+int hb_t32_split8_async(hb_ctx* ctx, const void* src, uint64_t src_stride, uint32_t rows,
+                        uint32_t row_words, void* hi, void* lo);
+
 /* --------------------------------------------------------- formats -- */
 
 /* EncodeMxint8 + PackAbuf on device: x fp32 row-major [rows][cols] ->

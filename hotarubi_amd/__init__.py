@@ -38,6 +38,7 @@ EXACT, FAST = 0, 1
 EP_ADDP, EP_MULP, EP_SCALE, EP_COPY, EP_RELU, EP_ACT, EP_ACT_MUL = 3, 4, 5, 6, 7, 8, 9
 EP_ADD = 0x100
 MAX_PIECES, MAX_OPS = 16, 8
+ABI_VERSION = 2  # HB_ABI_VERSION of the structs mirrored below
 
 #: every symbol include/hotarubi_gpu.h declares
 EXPORTS = (
@@ -75,7 +76,7 @@ class _VecCmd(C.Structure):
 
 
 class _Piece(C.Structure):
-    _fields_ = [("kb_offset", C.c_uint32), ("kb", C.c_uint32)]
+    _fields_ = [("kb_offset", C.c_uint32), ("kb", C.c_uint32), ("a_word", C.c_uint32)]
 
 
 class _EpOp(C.Structure):
@@ -89,7 +90,7 @@ class _LinearDesc(C.Structure):
                 ("w", C.c_void_p * 2), ("n_pieces", C.c_uint32),
                 ("pieces", _Piece * MAX_PIECES), ("onto", C.c_uint32), ("c", C.c_void_p),
                 ("n_ops", C.c_uint32), ("ops", _EpOp * MAX_OPS), ("tbuf", C.c_void_p),
-                ("q_out", C.c_void_p), ("flags", C.c_uint32)]
+                ("q_out", C.c_void_p), ("flags", C.c_uint32), ("a_stride", C.c_uint32)]
 
 
 @dataclass
@@ -174,6 +175,9 @@ def lib():
             f = getattr(L, name)
             f.restype = res
             f.argtypes = args
+        if L.hb_abi_version() != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH} has ABI {L.hb_abi_version()}, this module {ABI_VERSION}: "
+                              "rebuild with `python -m hotarubi_amd.build`")
         _lib = L
     return _lib
 
@@ -332,10 +336,13 @@ def _ptr(t) -> int | None:
 
 
 def linear_desc(m, n, kb_total, a, planes, modes, c, pieces=None, onto=False, ops=(),
-                tbuf=None, q_out=None, mode=EXACT) -> _LinearDesc:
+                tbuf=None, q_out=None, mode=EXACT, a_stride=0) -> _LinearDesc:
     """Build an hb_linear_desc from device buffers (torch tensors or addresses).
 
     planes/modes: [w] with [0] (FP4) or [w_hi, w_lo] with [1, 2] (W8).
+    pieces: (kb_offset, kb) or, with a_stride (A words per quad) nonzero,
+    (kb_offset, kb, a_word): LinearPiece (kernels.hpp:69-74) with its A
+    place as a word offset from `a`.
     ops: sequence of (kind, arg): ADDP/MULP take a device vector, SCALE an FP32
     bit pattern, ACT_MUL/ADD a device [m][n] tensor, COPY/RELU/ACT None.
     """
@@ -350,8 +357,10 @@ def linear_desc(m, n, kb_total, a, planes, modes, c, pieces=None, onto=False, op
     if len(pieces) > MAX_PIECES:
         raise ValueError("too many pieces")
     d.n_pieces = len(pieces)
-    for i, (off, kb) in enumerate(pieces):
-        d.pieces[i] = _Piece(off, kb)
+    for i, pc in enumerate(pieces):
+        off, kb = pc[0], pc[1]
+        d.pieces[i] = _Piece(off, kb, pc[2] if len(pc) > 2 else 0)
+    d.a_stride = a_stride
     d.onto = 1 if onto else 0
     d.c = _ptr(c)
     if len(ops) > MAX_OPS:

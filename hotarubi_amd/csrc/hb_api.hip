@@ -4,6 +4,7 @@
 // fields; all arithmetic on operand data runs in the HIP kernels.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -281,7 +282,17 @@ int VecExec(hb_ctx* ctx, const hb_vec_cmd* cmd, hb_onchip* o) {
 
 bool ValidMode(uint32_t m) { return m <= 2; }
 
-int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g) {
+// Word offset of piece p's A words from its W blocks (a_word - kb_offset;
+// 0 without a_stride).  The kernels address A by the W block index: a layer
+// whose pieces share one offset runs with A's base moved by it.
+int64_t PieceShift(const hb_linear_desc& d, uint32_t p) {
+  return d.a_stride ? (int64_t)d.pieces[p].a_word - (int64_t)d.pieces[p].kb_offset : 0;
+}
+
+// Validates a descriptor and fills the kernel arguments.  *mixed is set when
+// its pieces' A words sit at different offsets from their W blocks (see
+// LinearChain).
+int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g, bool* mixed) {
   if (!d) return Fail(HB_EINVAL, "null descriptor");
   if (d->m < 1 || d->n < 8 || d->n % 8 != 0 || d->kb_total < 1)
     return Fail(HB_EINVAL, "linear m = %u, n = %u, kb_total = %u: need m >= 1, n %% 8 == 0",
@@ -301,6 +312,18 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g) {
     steps += (uint64_t)pc.kb * d->n_planes;
   }
   if (steps > 8192) return Fail(HB_EINVAL, "%llu fold steps exceed 8192", (unsigned long long)steps);
+  // the kernels address A and W words with 32-bit byte offsets from the
+  // (moved) A base and from w
+  const uint64_t quads = (d->m + 3) / 4, a_row = d->a_stride ? d->a_stride : d->kb_total;
+  uint64_t a_end = 0;
+  *mixed = false;
+  for (uint32_t p = 0; p < d->n_pieces; ++p) {
+    const hb_piece& pc = d->pieces[p];
+    a_end = std::max(a_end, (quads - 1) * a_row + std::max<uint64_t>(pc.kb_offset, pc.a_word) + pc.kb);
+    if (PieceShift(*d, p) != PieceShift(*d, 0)) *mixed = true;
+  }
+  if (a_end * hb::kDdrWord > (1ull << 32) || (uint64_t)(d->n / 8) * d->kb_total * hb::kDdrWord > (1ull << 32))
+    return Fail(HB_EINVAL, "A or W spans more than 4 GiB");
   if (!d->a || !d->c) return Fail(HB_EINVAL, "null A or C");
   if (d->n_ops > HB_MAX_EP_OPS) return Fail(HB_EINVAL, "n_ops = %u", d->n_ops);
   if (d->q_out && d->n % 32 != 0) return Fail(HB_EINVAL, "quantized output needs n %% 32 == 0");
@@ -332,7 +355,7 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g) {
     g->op_x2[o] = reinterpret_cast<const uint32_t*>(op.x2);
   }
   g->n_ops = d->n_ops;
-  g->a = static_cast<const uint8_t*>(d->a);
+  g->a = static_cast<const uint8_t*>(d->a) + PieceShift(*d, 0) * (int64_t)hb::kDdrWord;
   g->w[0] = static_cast<const uint8_t*>(d->w[0]);
   g->w[1] = static_cast<const uint8_t*>(d->n_planes > 1 ? d->w[1] : d->w[0]);
   g->c = reinterpret_cast<uint32_t*>(d->c);
@@ -341,6 +364,7 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g) {
   g->m = d->m;
   g->n = d->n;
   g->kb_total = d->kb_total;
+  g->a_row = (uint32_t)a_row;
   g->n_pieces = d->n_pieces;
   for (uint32_t p = 0; p < d->n_pieces; ++p) {
     g->piece_off[p] = d->pieces[p].kb_offset;
@@ -359,6 +383,80 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g) {
 template <class T>
 uint64_t Diff(const T* a, const T* b) {
   return (uint64_t)(reinterpret_cast<const uint8_t*>(b) - reinterpret_cast<const uint8_t*>(a));
+}
+
+int LinearChain(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count);
+
+int LinearBatched(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
+  if (!d || count < 1) return Fail(HB_EINVAL, "no layers");
+  hb::GemmArgs g;
+  bool mixed = false;
+  if (int rc = LinearArgs(&d[0], &g, &mixed)) return rc;
+  if (count > 1) {
+    const hb_linear_desc& d0 = d[0];
+    g.a_batch = Diff(d0.a, d[1].a);
+    g.w_batch = Diff(d0.w[0], d[1].w[0]);
+    g.c_batch = Diff(d0.c, d[1].c) / 4;
+    g.q_batch = d0.q_out ? Diff(d0.q_out, d[1].q_out) : 0;
+    for (uint32_t o = 0; o < d0.n_ops; ++o) {
+      g.op_vec_batch[o] = d0.ops[o].vec ? Diff(d0.ops[o].vec, d[1].ops[o].vec) / 4 : 0;
+      g.op_x2_batch[o] = d0.ops[o].x2 ? Diff(d0.ops[o].x2, d[1].ops[o].x2) / 4 : 0;
+    }
+    for (uint32_t i = 1; i < count; ++i) {
+      const hb_linear_desc& x = d[i];
+      bool same = x.m == d0.m && x.n == d0.n && x.kb_total == d0.kb_total &&
+                  x.a_stride == d0.a_stride &&
+                  x.n_planes == d0.n_planes && x.flags == d0.flags && x.onto == d0.onto &&
+                  x.n_pieces == d0.n_pieces && x.n_ops == d0.n_ops && x.tbuf == d0.tbuf &&
+                  (x.q_out != nullptr) == (d0.q_out != nullptr) &&
+                  Diff(d0.a, x.a) == i * g.a_batch && Diff(d0.w[0], x.w[0]) == i * g.w_batch &&
+                  (x.n_planes < 2 || Diff(d0.w[1], x.w[1]) == i * g.w_batch) &&
+                  Diff(d0.c, x.c) == i * g.c_batch * 4 &&
+                  (!x.q_out || Diff(d0.q_out, x.q_out) == i * g.q_batch);
+      for (uint32_t l = 0; same && l < d0.n_planes; ++l) same = x.modes[l] == d0.modes[l];
+      for (uint32_t p = 0; same && p < d0.n_pieces; ++p)
+        same = x.pieces[p].kb_offset == d0.pieces[p].kb_offset && x.pieces[p].kb == d0.pieces[p].kb &&
+               (d0.a_stride == 0 || x.pieces[p].a_word == d0.pieces[p].a_word);
+      for (uint32_t o = 0; same && o < d0.n_ops; ++o) {
+        const hb_ep_op &a = d0.ops[o], &b = x.ops[o];
+        same = a.op == b.op && a.imm == b.imm && (a.vec != nullptr) == (b.vec != nullptr) &&
+               (a.x2 != nullptr) == (b.x2 != nullptr) &&
+               (!a.vec || Diff(a.vec, b.vec) == i * g.op_vec_batch[o] * 4) &&
+               (!a.x2 || Diff(a.x2, b.x2) == i * g.op_x2_batch[o] * 4);
+      }
+      if (!same) return Fail(HB_EINVAL, "layer %u differs in shape, schedule, ops or stride", i);
+    }
+  }
+  if (mixed) return LinearChain(ctx, d, count);
+  hipError_t err = hb::LaunchLinear(g, count, d[0].flags == HB_LINEAR_FAST, ctx->ws, ctx->stream);
+  if (err != hipSuccess) return HipFail(err, "linear launch");
+  return HB_OK;
+}
+
+// A layer whose pieces' A words sit at different offsets from their W blocks
+// runs as a chain of launches, one per run of consecutive pieces with one
+// offset.  The fold is pieces-outer, so starting each run from the previous
+// one's C folds in the same order; the ops and the requantize go with the
+// last run.  The descriptors were validated as a whole.
+int LinearChain(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
+  std::vector<hb_linear_desc> part(d, d + count);
+  for (uint32_t p0 = 0, p1; p0 < d[0].n_pieces; p0 = p1) {
+    for (p1 = p0 + 1; p1 < d[0].n_pieces && PieceShift(d[0], p1) == PieceShift(d[0], p0);) ++p1;
+    const bool last = p1 == d[0].n_pieces;
+    for (uint32_t i = 0; i < count; ++i) {
+      hb_linear_desc& x = part[i];
+      x = d[i];
+      x.n_pieces = p1 - p0;
+      for (uint32_t p = p0; p < p1; ++p) x.pieces[p - p0] = d[i].pieces[p];
+      x.onto = p0 > 0 ? 1u : d[i].onto;
+      if (!last) {
+        x.n_ops = 0;
+        x.q_out = nullptr;
+      }
+    }
+    if (int rc = LinearBatched(ctx, part.data(), count)) return rc;
+  }
+  return HB_OK;
 }
 
 }  // namespace
@@ -575,11 +673,7 @@ int hb_vec_exec(hb_ctx* ctx, const hb_vec_cmd* cmd, hb_onchip* o) { return VecEx
 
 int hb_linear_async(hb_ctx* ctx, const hb_linear_desc* d) {
   if (int rc = Enter(ctx)) return rc;
-  hb::GemmArgs g;
-  if (int rc = LinearArgs(d, &g)) return rc;
-  hipError_t err = hb::LaunchLinear(g, 1, d->flags == HB_LINEAR_FAST, ctx->ws, ctx->stream);
-  if (err != hipSuccess) return HipFail(err, "linear launch");
-  return HB_OK;
+  return LinearBatched(ctx, d, 1);
 }
 
 int hb_linear(hb_ctx* ctx, const hb_linear_desc* d) {
@@ -590,45 +684,7 @@ int hb_linear(hb_ctx* ctx, const hb_linear_desc* d) {
 
 int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
   if (int rc = Enter(ctx)) return rc;
-  if (!d || count < 1) return Fail(HB_EINVAL, "no layers");
-  hb::GemmArgs g;
-  if (int rc = LinearArgs(&d[0], &g)) return rc;
-  if (count > 1) {
-    const hb_linear_desc& d0 = d[0];
-    g.a_batch = Diff(d0.a, d[1].a);
-    g.w_batch = Diff(d0.w[0], d[1].w[0]);
-    g.c_batch = Diff(d0.c, d[1].c) / 4;
-    g.q_batch = d0.q_out ? Diff(d0.q_out, d[1].q_out) : 0;
-    for (uint32_t o = 0; o < d0.n_ops; ++o) {
-      g.op_vec_batch[o] = d0.ops[o].vec ? Diff(d0.ops[o].vec, d[1].ops[o].vec) / 4 : 0;
-      g.op_x2_batch[o] = d0.ops[o].x2 ? Diff(d0.ops[o].x2, d[1].ops[o].x2) / 4 : 0;
-    }
-    for (uint32_t i = 1; i < count; ++i) {
-      const hb_linear_desc& x = d[i];
-      bool same = x.m == d0.m && x.n == d0.n && x.kb_total == d0.kb_total &&
-                  x.n_planes == d0.n_planes && x.flags == d0.flags && x.onto == d0.onto &&
-                  x.n_pieces == d0.n_pieces && x.n_ops == d0.n_ops && x.tbuf == d0.tbuf &&
-                  (x.q_out != nullptr) == (d0.q_out != nullptr) &&
-                  Diff(d0.a, x.a) == i * g.a_batch && Diff(d0.w[0], x.w[0]) == i * g.w_batch &&
-                  (x.n_planes < 2 || Diff(d0.w[1], x.w[1]) == i * g.w_batch) &&
-                  Diff(d0.c, x.c) == i * g.c_batch * 4 &&
-                  (!x.q_out || Diff(d0.q_out, x.q_out) == i * g.q_batch);
-      for (uint32_t l = 0; same && l < d0.n_planes; ++l) same = x.modes[l] == d0.modes[l];
-      for (uint32_t p = 0; same && p < d0.n_pieces; ++p)
-        same = x.pieces[p].kb_offset == d0.pieces[p].kb_offset && x.pieces[p].kb == d0.pieces[p].kb;
-      for (uint32_t o = 0; same && o < d0.n_ops; ++o) {
-        const hb_ep_op &a = d0.ops[o], &b = x.ops[o];
-        same = a.op == b.op && a.imm == b.imm && (a.vec != nullptr) == (b.vec != nullptr) &&
-               (a.x2 != nullptr) == (b.x2 != nullptr) &&
-               (!a.vec || Diff(a.vec, b.vec) == i * g.op_vec_batch[o] * 4) &&
-               (!a.x2 || Diff(a.x2, b.x2) == i * g.op_x2_batch[o] * 4);
-      }
-      if (!same) return Fail(HB_EINVAL, "layer %u differs in shape, schedule, ops or stride", i);
-    }
-  }
-  hipError_t err = hb::LaunchLinear(g, count, d[0].flags == HB_LINEAR_FAST, ctx->ws, ctx->stream);
-  if (err != hipSuccess) return HipFail(err, "linear launch");
-  return HB_OK;
+  return LinearBatched(ctx, d, count);
 }
 
 int hb_encode_mxint8(hb_ctx* ctx, const float* x, uint32_t rows, uint32_t cols, void* out) {

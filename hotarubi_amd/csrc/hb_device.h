@@ -204,7 +204,7 @@ __device__ __forceinline__ uint32_t SlowLinear(const GemmArgs& g, const uint8_t*
     for (uint32_t l = 0; l < g.n_planes; ++l)
       for (uint32_t b = 0; b < g.piece_kb[p]; ++b) {
         const uint32_t blk = g.piece_off[p] + b, mode = g.modes[l];
-        const uint8_t* aw = a + ((size_t)quad * g.kb_total + blk) * kDdrWord;
+        const uint8_t* aw = a + ((size_t)quad * g.a_row + blk) * kDdrWord;
         const uint8_t* ww = (l ? w1 : w0) + ((size_t)grp * g.kb_total + blk) * kDdrWord;
         int32_t sum = 0;
         for (uint32_t k = 0; k < 32; ++k) {

@@ -164,10 +164,10 @@ __device__ __forceinline__ Offsets<kWLoads> ThreadOffsets(const GemmArgs& g, uin
   const uint32_t lane = t & 63, mt = (t >> 6) >> 1;
   const uint32_t r = mt * 32 + (lane & 31);
   const uint32_t quad = min(q0 + (r >> 2), g.quads - 1);
-  const uint32_t word_row = g.kb_total * kDdrWord;
+  const uint32_t word_row = g.kb_total * kDdrWord, a_row = g.a_row * kDdrWord;
   Offsets<kWLoads> o;
-  o.a = quad * word_row + (r & 3) * 32;
-  o.a_scale = quad * word_row + 128;
+  o.a = quad * a_row + (r & 3) * 32;
+  o.a_scale = quad * a_row + 128;
 #pragma unroll
   for (int k = 0; k < kWLoads; ++k) {
     const uint32_t col = (t + kP * k) % 256;

@@ -199,7 +199,7 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
   if (!consumer) {
     const uint32_t t = threadIdx.x, lane = t & 63, mt = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t h = lane >> 5;  // the A lane's block within the step
-    const uint32_t word_row = g.kb_total * kDdrWord;
+    const uint32_t word_row = g.kb_total * kDdrWord, a_row = g.a_row * kDdrWord;
     const uint32_t r = mt * 32 + (lane & 31), cl = t & 7;
 
     // Load cursor: tile lk (clamped to the last), step ls; per-tile byte
@@ -219,8 +219,8 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
         a = g.a + tl.z * g.a_batch;
         w0 = g.w[0] + tl.z * g.w_batch;
         const uint32_t quad = min(tl.row0 / 4 + (r >> 2), g.quads - 1);
-        o_a = quad * word_row + (r & 3) * 32;
-        o_sa = quad * word_row + 128;
+        o_a = quad * a_row + (r & 3) * 32;
+        o_sa = quad * a_row + 128;
         const uint32_t grp = min(tl.col0 / 8 + (t >> 3), g.groups - 1);
         o_w = grp * word_row + cl * 16;
         o_sw = grp * word_row + 128 + (cl & 4);

@@ -82,7 +82,7 @@ __device__ __forceinline__ Step Next(const Step& s, const GemmArgs& g) {
 template <bool kLinear>
 __device__ __forceinline__ const uint8_t* AWord(const GemmArgs& g, const uint8_t* a, uint32_t q,
                                                 uint32_t blk) {
-  if (kLinear) return a + ((size_t)q * g.kb_total + blk) * kDdrWord;
+  if (kLinear) return a + ((size_t)q * g.a_row + blk) * kDdrWord;
   return a + (size_t)((g.a_base + q * g.a_stride + blk) & (kAbufDepth - 1)) * kAbufWord;
 }
 
@@ -145,8 +145,9 @@ struct Staged {
 };
 
 // Per-thread byte offsets of the staged bytes within a block's words
-// (linear level: word (q, blk) at (q * kb_total + blk) * 144, so the block
-// index only moves a uniform base).
+// (linear level: A word (q, blk) at (q * a_row + blk) * 144 and W word
+// (grp, blk) at (grp * kb_total + blk) * 144, so the block index only moves
+// a uniform base).
 struct Offsets {
   uint32_t a, a_scale, w, w_scale;
 };
@@ -157,11 +158,12 @@ __device__ __forceinline__ Offsets ThreadOffsets(const GemmArgs& g, const Lane<T
   const uint32_t quad = min(q0 + (ln.r >> 2), g.quads - 1), t = ln.r & 3;
   const uint32_t grp = min(g0 + (ln.col >> 3), g.groups - 1), cl = ln.col & 7;
   Offsets o;
-  const uint32_t astride = kLinear ? g.kb_total * kDdrWord : 0u;
+  const uint32_t astride = kLinear ? g.a_row * kDdrWord : 0u;
+  const uint32_t wstride = kLinear ? g.kb_total * kDdrWord : 0u;
   o.a = quad * astride + t * 32 + ln.aofs;
   o.a_scale = quad * astride + 128 + t;
-  o.w = grp * astride + cl * 16 + ln.wofs;
-  o.w_scale = grp * astride + 128 + cl;
+  o.w = grp * wstride + cl * 16 + ln.wofs;
+  o.w_scale = grp * wstride + 128 + cl;
   if (!kLinear) {  // keep the quad / group for the wrapping on-chip addresses
     o.a = (quad << 16) | (t * 32 + ln.aofs);
     o.a_scale = (quad << 16) | (128 + t);

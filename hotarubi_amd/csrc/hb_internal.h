@@ -29,8 +29,10 @@ struct GemmArgs {
   uint32_t n;           // linear: columns; instruction: 8 * groups
   // instruction addressing (gemm_array.cpp:123-147)
   uint32_t a_base, a_stride, w_base, w_stride, c_base;
-  // linear addressing
+  // linear addressing: W word (grp, blk) at grp * kb_total + blk, A word
+  // (q, blk) at q * a_row + blk
   uint32_t kb_total;
+  uint32_t a_row;
   // fold schedule: pieces outer, planes inner, blocks innermost
   uint32_t n_pieces;
   uint32_t piece_off[kMaxPieces];

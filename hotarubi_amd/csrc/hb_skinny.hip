@@ -165,7 +165,7 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
   for (uint32_t p = 0; p < g.n_pieces; ++p) nblocks += g.piece_kb[p];
   const uint32_t chunks = (nblocks + 3) / 4, per = (chunks + kWaves - 1) / kWaves;
   const uint32_t c_begin = wave * per, c_end = min(c_begin + per, chunks);
-  const uint32_t word_row = g.kb_total * kDdrWord;
+  const uint32_t word_row = g.kb_total * kDdrWord, a_row = g.a_row * kDdrWord;
 
   // Per-lane byte offsets within a block's words (fixed for the K loop).
   // The lane's row within a quad (r16 % 4) and column within a group (r16 %
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
 #pragma unroll
   for (int mi = 0; mi < kMT; ++mi) {
     const uint32_t quad = min((mi * 16 + r16) >> 2, g.quads - 1);
-    a_off[mi] = quad * word_row + (r16 & 3) * 32;
+    a_off[mi] = quad * a_row + (r16 & 3) * 32;
   }
 #pragma unroll
   for (int nj = 0; nj < kNT; ++nj)

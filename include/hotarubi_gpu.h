@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define HB_ABI_VERSION 1
+#define HB_ABI_VERSION 2
 
 typedef enum hb_status {
   HB_OK = 0,
@@ -164,9 +164,16 @@ int hb_vec_exec(hb_ctx* ctx, const hb_vec_cmd* cmd, hb_onchip* onchip);
 
 /* ---------------------------------------------------- linear level -- */
 
+/* One piece of the fold, LinearPiece (tools/compiler/kernels.hpp:69-74):
+ * W blocks [kb_offset, kb_offset + kb).  Its A words: with the descriptor's
+ * a_stride 0, the same block indices of A (A is [ceil(m/4)][kb_total]);
+ * otherwise block i of quad q is A word q * a_stride + a_word + i (the
+ * reference's piece place `a` as a word offset from the descriptor's a, and
+ * its a_stride, one stride for all pieces). */
 typedef struct hb_piece {
-  uint32_t kb_offset; /* first K block of the piece */
+  uint32_t kb_offset; /* first K block of the piece (in W) */
   uint32_t kb;        /* blocks in the piece, >= 1 */
+  uint32_t a_word;    /* A word of the piece's first block in quad 0 (a_stride != 0) */
 } hb_piece;
 
 /* Epilogue ops, numbered as the VEC library entries (isa.hpp:350-363). */
@@ -196,7 +203,8 @@ enum { HB_MAX_PIECES = 16, HB_MAX_EP_OPS = 8 };
  *   for piece p: for plane l: for block b in piece: acc += BlockValue(...)
  * then ops[0..n_ops) in order, each with the VEC lane formula, then (if
  * q_out) MXINT8 requantization per token and 32 columns.
- *   a       device, MXINT8 DDR words [ceil(m/4)][kb_total] x 144 B (PackAbuf)
+ *   a       device, MXINT8 DDR words [ceil(m/4)][kb_total] x 144 B (PackAbuf),
+ *           or [ceil(m/4)][a_stride] with per-piece offsets (a_stride != 0)
  *   w[l]    device, DDR words [n/8][kb_total] x 144 B (PackWbuf) per plane
  *   modes[l] 0 FP4 (E2M1), 1 W8_HI, 2 W8_LO; a W8 layer is 2 planes {1, 2}
  *   c       device, fp32 row-major [m][n]; read if onto, always written
@@ -224,6 +232,10 @@ typedef struct hb_linear_desc {
    * output row, max |fast - exact| <= 1e-5 * max |exact|.  Tiles whose
    * scale bytes leave the fast path's range are computed exactly. */
   uint32_t flags;
+  /* 0: A is [ceil(m/4)][kb_total] words.  Otherwise A words per quad, and
+   * each piece's blocks start at its a_word (see hb_piece); every A word a
+   * piece reads must lie below byte offset 4 GiB of a. */
+  uint32_t a_stride;
 } hb_linear_desc;
 
 /* A single small layer (fewer than 128 output tiles) may grow the context's

@@ -511,3 +511,93 @@ def test_encode_rejects_non_finite(gpu):
     torch.cuda.synchronize()
     with pytest.raises(hb.HbError):
         hb.encode_mxint8(x_d, 1, 3, out, gpu)
+
+
+# ---- A pieces with their own place and stride (LinearPiece.a / a_stride) ----
+
+def a_words_view(a, quads, words):
+    return a.reshape(quads, words, 144)
+
+
+@pytest.mark.parametrize("mode", [hb.EXACT, hb.FAST])
+@pytest.mark.parametrize("m,w8", [(50, True), (150, True), (128, False), (8, False)])
+def test_a_stride_selects_a_head(gpu, mode, m, w8):
+    """One piece whose A words are head h's 2 blocks inside a projection
+    output of 30 words per quad (kernels.cpp:155-170: Q per head, a_stride =
+    the row's words).  Expected: the oracle on the head's words copied out."""
+    rng = np.random.default_rng(200 + m + 7 * w8 + mode)
+    n, kb, row_words, head = 256, 2, 30, 11
+    quads = (m + 3) // 4
+    _, q_all = helpers.activations(rng, m, row_words * 32)
+    if w8:
+        planes, modes = list(helpers.w8_planes_from_int8(rng.integers(-127, 128, (n, kb * 32)))), [1, 2]
+    else:
+        code, e = helpers.mxfp4_weights(rng, n, kb * 32)
+        planes, modes = [oracle.pack_wbuf(code, e)], [0]
+    a_head = np.ascontiguousarray(a_words_view(q_all, quads, row_words)[:, 2 * head: 2 * head + 2])
+    want, _ = oracle_linear(m, n, kb, a_head.reshape(-1, 144), planes, modes)
+    c_d = torch.zeros((m, n), dtype=torch.float32, device=DEV)
+    say("a_stride head", dict(m=m, w8=w8, mode=mode))
+    hb.linear(gpu, a=dev(q_all), planes=[dev(p) for p in planes], modes=modes, c=c_d, m=m, n=n,
+              kb_total=kb, pieces=[(0, kb, 2 * head)], a_stride=row_words, mode=mode)
+    got = host(c_d).view(np.uint32)
+    if mode == hb.EXACT:
+        assert_bits(got, want)
+    else:
+        g, w = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
+        row_scale = np.abs(w).max(axis=1, keepdims=True)
+        assert (np.abs(g - w) <= 1e-5 * row_scale).all()
+
+
+@pytest.mark.parametrize("mode", [hb.EXACT, hb.FAST])
+def test_a_pieces_at_different_places_chain(gpu, mode):
+    """The output projection over head-major MXINT8 attention outputs
+    ([head][quad][2 words]): 15 pieces, piece h = W blocks [2h, 2h+2) and A
+    words from head h's own array (a_stride 2, a_word h * quads * 2), with
+    MULP, ADDP and requantize, batched over 2 layers.  The pieces sit at
+    different offsets, so the layer runs as a chain of launches; expected:
+    the oracle on the words gathered into [quad][30]."""
+    rng = np.random.default_rng(300 + mode)
+    layers, m, n, heads = 2, 50, 960, 15
+    quads, kb = (m + 3) // 4, 2 * heads
+    data = []
+    for _ in range(layers):
+        per_head = [helpers.activations(rng, m, 64)[1].reshape(quads, 2, 144) for _ in range(heads)]
+        a_std = np.concatenate(per_head, axis=1).reshape(-1, 144)
+        a_hm = np.stack(per_head).reshape(-1, 144)
+        planes = list(helpers.w8_planes_from_int8(rng.integers(-127, 128, (n, kb * 32))))
+        data.append((a_std, a_hm, planes))
+    scale = helpers.random_fp32_words(rng, (n,), 117, 122)
+    bias = helpers.random_fp32_words(rng, (n,), 118, 124)
+    a_d = dev(np.stack([d[1] for d in data]))
+    w_d = [dev(np.stack([d[2][p] for d in data])) for p in range(2)]
+    c_d = torch.zeros((layers, m, n), dtype=torch.float32, device=DEV)
+    q_d = torch.zeros((layers, quads * n // 32, 144), dtype=torch.uint8, device=DEV)
+    ops = [(hb.EP_MULP, dev(scale.view(np.float32))), (hb.EP_ADDP, dev(bias.view(np.float32)))]
+    pieces = [(2 * h, 2, h * quads * 2) for h in range(heads)]
+    descs = [hb.linear_desc(m, n, kb, a_d[i], [w[i] for w in w_d], [1, 2], c_d[i], pieces=pieces,
+                            ops=ops, q_out=q_d[i], mode=mode, a_stride=2) for i in range(layers)]
+    torch.cuda.synchronize()
+    say("a pieces chain", dict(mode=mode))
+    hb.linear_batched(descs, gpu)
+    got, gq = host(c_d).view(np.uint32), host(q_d)
+    for i, (a_std, _, planes) in enumerate(data):
+        want, wq = oracle_linear(m, n, kb, a_std, planes, [1, 2], ops=[(hb.EP_MULP, scale),
+                                 (hb.EP_ADDP, bias)], quantize=True)
+        if mode == hb.EXACT:
+            assert_bits(got[i], want)
+            assert np.array_equal(gq[i], wq.reshape(-1, 144)[: quads * n // 32])
+        else:
+            g, w = got[i].view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
+            row_scale = np.abs(w).max(axis=1, keepdims=True)
+            assert (np.abs(g - w) <= 1e-5 * row_scale).all()
+
+
+def test_a_stride_rejects_offsets_past_4gib(gpu):
+    a = torch.zeros((16, 144), dtype=torch.uint8, device=DEV)
+    w = torch.zeros((1, 144), dtype=torch.uint8, device=DEV)
+    c = torch.zeros((8, 8), dtype=torch.float32, device=DEV)
+    with pytest.raises(hb.HbError) as e:
+        hb.linear(gpu, a=a, planes=[w], modes=[0], c=c, m=8, n=8, kb_total=1,
+                  pieces=[(0, 1, 1 << 25)], a_stride=1)
+    assert e.value.code == hb.HB_EINVAL

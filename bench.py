@@ -330,6 +330,118 @@ class ExpertStep(Chain):
         torch.cuda.synchronize()
 
 
+class ExpertAttention:
+    """The attention of one SmolVLA action-expert step as the reference
+    compiler emits it (tools/compiler/kernels.cpp:78-244, plan from
+    smolvla_expert.cpp:361-390): 16 layers, 15 query / 5 KV heads of 64, a
+    chunk of 50 query rows per batch element, keys = 128 on the cross-
+    attention (odd) layers and 128 + 64 on the self-attention (even) layers.
+    Per layer: SPLIT8 of K and T32_SPLIT8 of V over every KV head and batch
+    element at once; per query head, scores = Q_h K_j^T (W8, with the mask
+    add on self layers and the 1/8 scale fused) and O_h = P_h V_j (W8).
+    The query head's words are read out of the projection output in place
+    (a_stride 30).  Softmax is outside this path: P is a synthetic MXINT8
+    tensor of its shape.  Each batch element's rows start on a quad (13
+    quads per element)."""
+
+    LAYERS, HEADS, KV, HW, QW, KVW, ROWS, PREFIX, SUFFIX = 16, 15, 5, 2, 30, 10, 50, 128, 64
+
+    def __init__(self, hb, torch, batch, mode, seed=41):
+        dev, self.hb, self.torch, self.batch = "cuda:0", hb, torch, batch
+        g = torch.Generator(device=dev).manual_seed(seed)
+        quads = (self.ROWS + 3) // 4
+        self.keep, self.steps, self.ops = [], [], 0.0
+
+        def words(n, lo=122, hi=128):
+            t = torch.randint(0, 256, (n, 144), generator=g, device=dev, dtype=torch.uint8)
+            t[:, 128:132] = torch.randint(lo, hi, (n, 4), generator=g, device=dev, dtype=torch.uint8)
+            t[:, 132:] = 0
+            self.keep.append(t)
+            return t
+
+        max_keys = self.PREFIX + self.SUFFIX
+        kbk_max = max_keys // 32
+        # intermediates reused by every layer: planes, scores, P, O
+        kh = torch.empty((2, batch * max_keys // 8 * self.KVW, 144), dtype=torch.uint8, device=dev)
+        vh = torch.empty((2, 4 * self.KVW * batch * kbk_max, 144), dtype=torch.uint8, device=dev)
+        s = torch.empty((batch * self.HEADS * self.ROWS * max_keys,), dtype=torch.float32, device=dev)
+        s_at = self.ROWS * max_keys  # element (b, h)'s scores: [ROWS][keys] from (b * 15 + h) * s_at
+        p_words = words(batch * self.HEADS * quads * kbk_max).view(batch, self.HEADS, -1, 144)
+        o = torch.empty((batch, self.HEADS, self.ROWS, 64), dtype=torch.float32, device=dev)
+        mask = torch.zeros((self.ROWS, max_keys), dtype=torch.float32, device=dev)
+        mask[:, self.PREFIX:] = -1e4 * torch.triu(torch.ones(self.ROWS, self.SUFFIX, device=dev), 1)
+        self.keep += [kh, vh, s, o, mask]
+        scale = int(np.array(0.125, np.float32).view(np.uint32))
+        for layer in range(self.LAYERS):
+            keys = self.PREFIX + (self.SUFFIX if layer % 2 == 0 else 0)
+            rows, kbk = batch * keys // 4, keys // 32
+            q = words(batch * quads * self.QW).view(batch, quads * self.QW, 144)
+            k, v = words(rows * self.KVW), words(rows * self.KVW)
+            self.steps.append(("split8", k, rows, kh))
+            self.steps.append(("t32", v, rows, vh))
+            ops = ([(hb.EP_ADD, mask)] if keys == max_keys else []) + [(hb.EP_SCALE, scale)]
+            for h in range(self.HEADS):
+                j = h // (self.HEADS // self.KV)
+                # scores: W = K_j planes of element b, 10 words per group row
+                self.steps.append(("linear", [hb.linear_desc(
+                    self.ROWS, keys, self.KVW, q[b, 2 * h:],
+                    [kh[pl, (b * keys // 8) * self.KVW + 2 * j:] for pl in range(2)], [1, 2],
+                    s[(b * self.HEADS + h) * s_at:], pieces=[(0, 2, 0)], a_stride=self.QW, ops=ops,
+                    mode=mode)
+                    for b in range(batch)]))
+                # O_h = P_h V_j: V^T planes of head j, element b's blocks in each group row
+                kb_all = batch * kbk
+                self.steps.append(("linear", [hb.linear_desc(
+                    self.ROWS, 64, kb_all, p_words[b, h],
+                    [vh[pl, 8 * j * kb_all + b * kbk:] for pl in range(2)], [1, 2], o[b, h],
+                    pieces=[(0, kbk, 0)], a_stride=kbk, mode=mode) for b in range(batch)]))
+                self.ops += batch * 2.0 * self.ROWS * 64 * keys * 2
+        torch.cuda.synchronize()
+        self.m, self.descs = batch * self.ROWS, [d for st in self.steps if st[0] == "linear" for d in st[1]]
+
+    def run(self, ctx):
+        hb = self.hb
+        for st in self.steps:
+            if st[0] == "split8":
+                hb.split8(st[1], st[2], self.KVW, st[3][0], st[3][1], ctx=ctx, sync=False)
+            elif st[0] == "t32":
+                hb.t32_split8(st[1], st[2], self.KVW, st[3][0], st[3][1], ctx=ctx, sync=False)
+            else:
+                hb.linear_batched(st[1], ctx)
+
+
+def time_split_kernels(hb, torch, ctx, stream, rows=200000, row_words=10, steps=10):
+    """HBM rate of SPLIT8 and T32_SPLIT8 over a K / V matrix of rows x
+    row_words MXINT8 words (rows * row_words * 144 B, larger than the
+    last-level cache): algorithmic bytes = the source read once plus both
+    planes written once = 2 x the source size."""
+    dev = "cuda:0"
+    src = torch.randint(0, 256, (rows * row_words, 144), dtype=torch.uint8, device=dev)
+    src[:, 128:132] = torch.randint(118, 136, (rows * row_words, 4), dtype=torch.uint8, device=dev)
+    hi = torch.empty((rows * row_words // 2, 144), dtype=torch.uint8, device=dev)
+    lo = torch.empty_like(hi)
+    nbytes = 2.0 * rows * row_words * 144
+    out = {"workload": f"{rows} rows x {row_words} MXINT8 words ({rows * row_words * 144 / 1e6:.0f} MB "
+                       "source), bytes = source + both planes"}
+    for name, fn in (("split8", hb.split8), ("t32_split8", hb.t32_split8)):
+        for _ in range(2):
+            fn(src, rows, row_words, hi, lo, ctx=ctx, sync=False)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(steps):
+            fn(src, rows, row_words, hi, lo, ctx=ctx, sync=False)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 4), "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
+                                                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                                      "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    del src, hi, lo
+    return out
+
+
 class SiglipSet(Chain):
     """SigLIP-style vision-encoder GEMM set, W8: per layer, on M = 2 cameras x
     1024 patch tokens = 2048 rows with hidden 768, QKV 768->2304, out-proj
@@ -478,6 +590,8 @@ def main():
     ap.add_argument("--layers", type=int, default=256)
     ap.add_argument("--m", type=int, default=128)
     ap.add_argument("--quick", action="store_true", help="headline only, no extra fields")
+    ap.add_argument("--only", choices=["attention"], default=None,
+                    help="headline plus this group of extra fields only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
@@ -532,7 +646,7 @@ def main():
         "roofline": roof,
     }
 
-    if not args.quick:
+    if not args.quick and args.only is None:
         extra_steps, extra_warm = 5, 1
         # the same workload in the other mode
         other = hb.EXACT if fast else hb.FAST
@@ -591,6 +705,21 @@ def main():
         out["smolvla_expert_step_ms"] = {f"B={b}": time_expert_step(hb, torch, ctx, b, mode)
                                          for b in (1, 32)}
         ctx.set_stream(stream.cuda_stream)
+
+    if not args.quick and args.only in (None, "attention"):
+        # attention operands built on device (SPLIT8 / T32_SPLIT8) and the
+        # expert step's attention GEMMs over them
+        out["attention_operands"] = time_split_kernels(hb, torch, ctx, stream)
+        att = {"workload": "SmolVLA expert attention: 16 layers x 15 heads, QK^T (mask, scale) "
+                           "and PV in W8 over SPLIT8 / T32_SPLIT8 operands, 50 rows per element"}
+        for b in (1, 32):
+            wk = ExpertAttention(hb, torch, b, mode)
+            t = time_chain(torch, ctx, wk, steps=5)
+            best = min(t["eager_ms"], t.get("graph_ms", t["eager_ms"]))
+            att[f"B={b}"] = {**t, "tops": round(wk.ops / (best * 1e-3) / 1e12, 3)}
+            del wk
+        ctx.set_stream(stream.cuda_stream)
+        out["smolvla_expert_attention_ms"] = att
 
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.m, n, kb)

@@ -53,81 +53,105 @@ __global__ __launch_bounds__(256) void Split8Kernel(const uint8_t* src, uint64_t
   ol[136 + c] = 0;
 }
 
-// AlignElement: RNE(q / 2^shift) as a byte, 0 for shift >= 9.
-__device__ __forceinline__ uint32_t Align(uint32_t value, uint32_t shift) {
-  if (shift >= 9) return 0;
-  const int32_t shifted = ((int32_t)(int8_t)value * 256) >> shift;
-  const bool guard = ((shifted >> 7) & 1) != 0, sticky = (shifted & 0x7F) != 0;
-  const bool odd = ((shifted >> 8) & 1) != 0;
-  return (uint32_t)((shifted >> 8) + (guard && (sticky || odd) ? 1 : 0)) & 0xFFu;
+// AlignElement for one token's shift s = emax - e_t: RNE(v / 2^s) of the
+// int8 v, 0 for s >= 9.  With s clamped to 9 and h = 2^(s-1) - 1 (0 for
+// s = 0), (v + h + lsb) >> s with lsb = bit s of v (0 for s = 0) rounds to
+// nearest, ties to even: the quotient q of v = q 2^s + r rises by one
+// exactly when r > 2^(s-1), or r = 2^(s-1) and q is odd; for s = 9 every
+// int8 gives 0.
+struct Shift {
+  uint32_t s, h, m;
+};
+__device__ __forceinline__ Shift ShiftOf(uint32_t emax, uint32_t e) {
+  const uint32_t s = min(emax - e, 9u);  // a zero token's shift is never used for a nonzero value
+  return {s, s ? (1u << (s - 1)) - 1u : 0u, s ? 1u : 0u};
+}
+__device__ __forceinline__ uint32_t AlignByte(uint32_t word, int byte, Shift k) {
+  const int32_t v = __builtin_amdgcn_sbfe((int32_t)word, 8 * byte, 8);
+  return (uint32_t)((v + (int32_t)k.h + ((v >> k.s) & (int32_t)k.m)) >> k.s) & 0xFFu;
 }
 
-// T32_SPLIT8: one wave per (group of 8 rows, word position): the 8 source
-// words go to LDS; lane t < 32 finds whether token t is nonzero, a
-// max-reduction gives emax; lane d < 32 then builds dimension d's column
-// (32 tokens -> 32 aligned int8 -> 16 bytes per plane) and lanes 32..63
-// write the scale and pad bytes.
-constexpr int kT32Waves = 4;
+// Bytes 0 of a, b, c, d as one dword {a, b, c, d}.
+__device__ __forceinline__ uint32_t Pack4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x0C0C0400u);  // {a0, b0, 0, 0}
+  const uint32_t hi = __builtin_amdgcn_perm(d, c, 0x0C0C0400u);  // {c0, d0, 0, 0}
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+// T32_SPLIT8: each wave transposes two 32 x 32 blocks (8 source rows x one
+// word position); 8 blocks per workgroup.  The block's 8 words go to LDS with
+// 16-byte loads.  Lane t of a block's half-wave finds whether token t is
+// nonzero; a 32-lane max gives emax.  Then lane (dq, tq) aligns dimensions
+// 4dq..4dq+3 of tokens 8tq..8tq+7 (one LDS dword per token), transposes
+// them into per-dimension dwords of 4 tokens, splits the nibbles, and stores
+// 4 bytes per plane and dimension: dimension d = 4dq + i is column d % 8 of
+// output group 4w + d / 8, tokens 8tq.. at byte 16 (d % 8) + 4tq.
+constexpr int kT32Waves = 4, kT32Blocks = 2 * kT32Waves;
 __global__ __launch_bounds__(64 * kT32Waves) void T32Split8Kernel(const uint8_t* src,
                                                                   uint64_t stride,
                                                                   uint32_t rows,
                                                                   uint32_t row_words,
                                                                   uint8_t* hi, uint8_t* lo) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kT32Waves][8][kDdrWord];
-  const uint32_t wv = threadIdx.x / 64, lane = threadIdx.x % 64;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kT32Blocks][8][kDdrWord];
   const uint32_t groups = rows / 8;
-  const uint64_t block = (uint64_t)blockIdx.x * kT32Waves + wv;
-  if (block >= (uint64_t)groups * row_words) return;  // wave-uniform
-  const uint32_t g = (uint32_t)(block / row_words), w = (uint32_t)(block % row_words);
-  uint8_t(*in)[kDdrWord] = lds[wv];
-  // 8 words x 9 pieces of 16 bytes = 72 pieces over 64 lanes
-  for (uint32_t piece = lane; piece < 72; piece += 64) {
-    const uint32_t f = piece / 9, o = (piece % 9) * 16;
-    *reinterpret_cast<u32x4*>(&in[f][o]) = *reinterpret_cast<const u32x4*>(
-        src + (uint64_t)(g * 8 + f) * stride + (uint64_t)w * kDdrWord + o);
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  uint32_t nz_bits, emax;
-  {
-    const uint32_t t = lane % 32;
-    const u32x4* blk = reinterpret_cast<const u32x4*>(&in[t / 4][(t % 4) * 32]);
-    const u32x4 a = blk[0], b = blk[1];
-    const bool nz = (a[0] | a[1] | a[2] | a[3] | b[0] | b[1] | b[2] | b[3]) != 0;
-    const uint32_t scale = in[t / 4][128 + t % 4];
-    uint32_t e = nz ? scale : 0u;
-    for (int off = 16; off >= 1; off >>= 1) e = max(e, (uint32_t)__shfl_xor((int)e, off, 32));
-    const uint64_t ballot = __ballot(nz);
-    nz_bits = (uint32_t)ballot;  // lanes 0..31: token t's flag in bit t
-    emax = nz_bits != 0 ? e : 127u;
-  }
-  const uint32_t kbt = groups;
-  if (lane < 32) {
-    const uint32_t d = lane;
-    uint32_t codes[8];  // 32 aligned int8, K (token) order
-#pragma unroll
-    for (int i = 0; i < 8; ++i) codes[i] = 0;
-#pragma unroll 4
-    for (uint32_t t = 0; t < 32; ++t) {
-      const uint32_t shift = emax - in[t / 4][128 + t % 4];
-      const uint32_t v = ((nz_bits >> t) & 1) ? Align(in[t / 4][(t % 4) * 32 + d], shift) : 0u;
-      codes[t / 4] |= v << (8 * (t % 4));
+  const uint64_t blocks = (uint64_t)groups * row_words;
+  const uint64_t first = (uint64_t)blockIdx.x * kT32Blocks;
+  // 8 blocks x 8 words x 9 pieces of 16 bytes over the workgroup
+  for (uint32_t piece = threadIdx.x; piece < kT32Blocks * 72; piece += 64 * kT32Waves) {
+    const uint32_t b = piece / 72, f = (piece % 72) / 9, o = (piece % 9) * 16;
+    const uint64_t blk = first + b;
+    if (blk < blocks) {
+      const uint32_t g = (uint32_t)(blk / row_words), w = (uint32_t)(blk % row_words);
+      *reinterpret_cast<u32x4*>(&lds[b][f][o]) = *reinterpret_cast<const u32x4*>(
+          src + (uint64_t)(g * 8 + f) * stride + (uint64_t)w * kDdrWord + o);
     }
-    uint32_t h[4], l[4];
-    SplitNibbles(codes[0], codes[1], h[0], l[0]);
-    SplitNibbles(codes[2], codes[3], h[1], l[1]);
-    SplitNibbles(codes[4], codes[5], h[2], l[2]);
-    SplitNibbles(codes[6], codes[7], h[3], l[3]);
-    const uint64_t idx = (uint64_t)(4 * w + d / 8) * kbt + g;
-    *reinterpret_cast<u32x4*>(hi + idx * kDdrWord + (d % 8) * 16) = u32x4{h[0], h[1], h[2], h[3]};
-    *reinterpret_cast<u32x4*>(lo + idx * kDdrWord + (d % 8) * 16) = u32x4{l[0], l[1], l[2], l[3]};
-  } else {
-    const uint32_t i = lane - 32, cg = i / 8, c = i % 8;
-    const uint64_t idx = (uint64_t)(4 * w + cg) * kbt + g;
-    hi[idx * kDdrWord + 128 + c] = (uint8_t)emax;
-    lo[idx * kDdrWord + 128 + c] = (uint8_t)emax;
-    hi[idx * kDdrWord + 136 + c] = 0;
-    lo[idx * kDdrWord + 136 + c] = 0;
+  }
+  __syncthreads();
+  const uint32_t lane = threadIdx.x % 64, b = (threadIdx.x / 64) * 2 + lane / 32, l = lane % 32;
+  const uint64_t blk = first + b;
+  if (blk >= blocks) return;  // no barrier follows
+  const uint32_t g = (uint32_t)(blk / row_words), w = (uint32_t)(blk % row_words);
+  uint8_t(*in)[kDdrWord] = lds[b];
+  uint32_t emax;
+  {
+    const u32x4* tok = reinterpret_cast<const u32x4*>(&in[l / 4][(l % 4) * 32]);
+    const u32x4 x = tok[0], y = tok[1];
+    const bool nz = (x[0] | x[1] | x[2] | x[3] | y[0] | y[1] | y[2] | y[3]) != 0;
+    uint32_t e = nz ? in[l / 4][128 + l % 4] : 0u;
+    for (int off = 16; off >= 1; off >>= 1) e = max(e, (uint32_t)__shfl_xor((int)e, off, 32));
+    const uint64_t any = __ballot(nz) >> (lane & 32);
+    emax = (uint32_t)any != 0 ? e : 127u;
+  }
+  const uint32_t dq = l % 8, tq = l / 8;
+  // aligned codes: v[u][i] = token 8tq + u, dimension 4dq + i
+  uint32_t v[8][4];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const uint32_t t = 8 * tq + u;
+    const uint32_t word = *reinterpret_cast<const uint32_t*>(&in[t / 4][(t % 4) * 32 + 4 * dq]);
+    const Shift k = ShiftOf(emax, in[t / 4][128 + t % 4]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[u][i] = AlignByte(word, i, k);
+  }
+  const uint64_t base = (uint64_t)(4 * w + dq / 2) * groups + g;
+  uint8_t* oh = hi + base * kDdrWord + 4 * tq;
+  uint8_t* ol = lo + base * kDdrWord + 4 * tq;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t x0 = Pack4(v[0][i], v[1][i], v[2][i], v[3][i]);
+    const uint32_t x1 = Pack4(v[4][i], v[5][i], v[6][i], v[7][i]);
+    uint32_t h, q;
+    SplitNibbles(x0, x1, h, q);
+    const uint32_t c = 4 * (dq % 2) + i;
+    *reinterpret_cast<uint32_t*>(oh + c * 16) = h;
+    *reinterpret_cast<uint32_t*>(ol + c * 16) = q;
+  }
+  // scale and pad bytes: lane l writes dword l % 4 of bytes 128..143 of
+  // output word l / 8 (group 4w + l / 8), plane (l / 4) % 2
+  {
+    const uint32_t cg = l / 8, plane = (l / 4) % 2, k = l % 4;
+    uint8_t* word = (plane ? lo : hi) + ((uint64_t)(4 * w + cg) * groups + g) * kDdrWord;
+    *reinterpret_cast<uint32_t*>(word + 128 + 4 * k) = k < 2 ? emax * 0x01010101u : 0u;
   }
 }
 
@@ -146,7 +170,7 @@ hipError_t LaunchT32Split8(const uint8_t* src, uint64_t stride, uint32_t rows, u
                            uint8_t* hi, uint8_t* lo, hipStream_t stream) {
   const uint64_t blocks = (uint64_t)(rows / 8) * row_words;
   if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL(T32Split8Kernel, dim3((uint32_t)((blocks + kT32Waves - 1) / kT32Waves)),
+  hipLaunchKernelGGL(T32Split8Kernel, dim3((uint32_t)((blocks + kT32Blocks - 1) / kT32Blocks)),
                      dim3(64 * kT32Waves), 0, stream, src, stride, rows, row_words, hi, lo);
   return hipGetLastError();
 }

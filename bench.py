@@ -345,6 +345,7 @@ class ExpertAttention:
     quads per element)."""
 
     LAYERS, HEADS, KV, HW, QW, KVW, ROWS, PREFIX, SUFFIX = 16, 15, 5, 2, 30, 10, 50, 128, 64
+    STREAMS = 4  # the head groups are independent: side streams, one context each
 
     def __init__(self, hb, torch, batch, mode, seed=41):
         dev, self.hb, self.torch, self.batch = "cuda:0", hb, torch, batch
@@ -380,34 +381,62 @@ class ExpertAttention:
             self.steps.append(("split8", k, rows, kh))
             self.steps.append(("t32", v, rows, vh))
             ops = ([(hb.EP_ADD, mask)] if keys == max_keys else []) + [(hb.EP_SCALE, scale)]
-            for h in range(self.HEADS):
-                j = h // (self.HEADS // self.KV)
-                # scores: W = K_j planes of element b, 10 words per group row
-                self.steps.append(("linear", [hb.linear_desc(
+            share, kb_all = self.HEADS // self.KV, batch * kbk
+
+            def qk(b, h):  # scores: W = K_j planes of element b, 10 words per group row
+                j = h // share
+                return hb.linear_desc(
                     self.ROWS, keys, self.KVW, q[b, 2 * h:],
                     [kh[pl, (b * keys // 8) * self.KVW + 2 * j:] for pl in range(2)], [1, 2],
-                    s[(b * self.HEADS + h) * s_at:], pieces=[(0, 2, 0)], a_stride=self.QW, ops=ops,
-                    mode=mode)
-                    for b in range(batch)]))
-                # O_h = P_h V_j: V^T planes of head j, element b's blocks in each group row
-                kb_all = batch * kbk
-                self.steps.append(("linear", [hb.linear_desc(
+                    s[(b * self.HEADS + h) * s_at:], pieces=[(0, 2, 0)], a_stride=self.QW,
+                    ops=ops, mode=mode)
+
+            def pv(b, h):  # O_h = P_h V_j: V^T planes of head j, element b's blocks per group row
+                j = h // share
+                return hb.linear_desc(
                     self.ROWS, 64, kb_all, p_words[b, h],
                     [vh[pl, 8 * j * kb_all + b * kbk:] for pl in range(2)], [1, 2], o[b, h],
-                    pieces=[(0, kbk, 0)], a_stride=kbk, mode=mode) for b in range(batch)]))
-                self.ops += batch * 2.0 * self.ROWS * 64 * keys * 2
+                    pieces=[(0, kbk, 0)], a_stride=kbk, mode=mode)
+
+            # one launch per (query head) over the batch elements, or, for one
+            # element, per position within the KV group over the KV heads
+            # (every operand then advances by one uniform stride)
+            groups = ([[(0, share * j + r) for j in range(self.KV)] for r in range(share)]
+                      if batch == 1 else
+                      [[(b, h) for b in range(batch)] for h in range(self.HEADS)])
+            # a head group's QK^T then PV, the groups on side streams in turn
+            self.steps.append(("fork",))
+            for i, grp in enumerate(groups):
+                for fn in (qk, pv):
+                    self.steps.append(("linear", [fn(b, h) for b, h in grp], i % self.STREAMS))
+            self.steps.append(("join",))
+            self.ops += batch * self.HEADS * 2.0 * self.ROWS * 64 * keys * 2
+        self.side = [torch.cuda.Stream() for _ in range(self.STREAMS)]
+        self.side_ctx = [hb.Context(0) for _ in range(self.STREAMS)]
+        for c, st in zip(self.side_ctx, self.side):
+            c.set_stream(st.cuda_stream)
         torch.cuda.synchronize()
         self.m, self.descs = batch * self.ROWS, [d for st in self.steps if st[0] == "linear" for d in st[1]]
 
     def run(self, ctx):
-        hb = self.hb
+        hb, main = self.hb, self.torch.cuda.current_stream()
         for st in self.steps:
             if st[0] == "split8":
                 hb.split8(st[1], st[2], self.KVW, st[3][0], st[3][1], ctx=ctx, sync=False)
             elif st[0] == "t32":
                 hb.t32_split8(st[1], st[2], self.KVW, st[3][0], st[3][1], ctx=ctx, sync=False)
+            elif st[0] == "fork":
+                for side in self.side:
+                    side.wait_stream(main)
+            elif st[0] == "join":
+                for side in self.side:
+                    main.wait_stream(side)
             else:
-                hb.linear_batched(st[1], ctx)
+                hb.linear_batched(st[1], self.side_ctx[st[2]])
+
+    def close(self):
+        for c in self.side_ctx:
+            c.close()
 
 
 def time_split_kernels(hb, torch, ctx, stream, rows=200000, row_words=10, steps=10):
@@ -717,6 +746,7 @@ def main():
             t = time_chain(torch, ctx, wk, steps=5)
             best = min(t["eager_ms"], t.get("graph_ms", t["eager_ms"]))
             att[f"B={b}"] = {**t, "tops": round(wk.ops / (best * 1e-3) / 1e12, 3)}
+            wk.close()
             del wk
         ctx.set_stream(stream.cuda_stream)
         out["smolvla_expert_attention_ms"] = att

@@ -515,6 +515,7 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
     for (uint32_t step = 0; step < steps; step += kU) {
 #pragma unroll
       for (int i = 0; i < kU; ++i) {  // iteration step + i converts step + i + 2
+        if (step + i >= steps) break;  // uniform; the consumers stop at the same step
         unsafe |= StoreRaw<kMT, kP, kWLoads, kW8, kAWave>(ring[(i + 2) % kU], lds, (i + 2) % kU, t);
         load(ring[(i + 2) % kU], step + i + 2 + kU);
         __syncthreads();
@@ -644,6 +645,7 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
   for (uint32_t step = 0; step < steps; step += kU) {
 #pragma unroll
     for (int i = 0; i < kU; ++i) {  // iteration step + i
+      if (step + i >= steps) break;  // uniform; the producers stop at the same step
       matrix(ops);
       // Anchor the step's matrix work here (the empty asm emits nothing):
       // left free, the compiler sinks the pure MFMA calls past later

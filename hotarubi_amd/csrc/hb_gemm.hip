@@ -709,7 +709,9 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
     args.splits = (steps + per - 1) / per;
     args.split_steps = per;
   }
-  const bool defer = small && (args.n_ops > 0 || args.q_out != nullptr || args.splits > 1);
+  // The exact kernels' epilogue arithmetic is spread over the elements of a
+  // small layer; the fast kernels finish an unsplit tile in place.
+  const bool defer = small && (args.splits > 1 || (!fastk && (args.n_ops > 0 || args.q_out != nullptr)));
   if (!defer) return fastk ? LaunchLinearFast(args, batch, stream) : LaunchTiles<true>(args, batch, stream);
 
   const size_t bytes = WorkspaceBytes(args);

@@ -4,7 +4,8 @@ Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg import
 this package, and only as the checker.  The product (hotarubi_amd) never does.
 
 `ref()` returns the reference's own FP32 code compiled from /root/reference
-into oracle/_ref (see oracle/Makefile), or None where it was not built.
+into oracle/_ref (see oracle/Makefile), or None where it was not built;
+`ref_vec()` likewise its VEC lane and scalar-unit code.
 """
 from __future__ import annotations
 
@@ -17,6 +18,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libref_fp32.so")
+REF_VEC_PATH = os.path.join(HERE, "_ref", "libref_vec.so")
 
 u8p = C.POINTER(C.c_uint8)
 u32p = C.POINTER(C.c_uint32)
@@ -57,6 +59,7 @@ ABUF_DEPTH, WBUF_DEPTH, FBUF_DEPTH, PBUF_DEPTH, TBUF_DEPTH = 8192, 2048, 4096, 5
 
 _lib = None
 _ref = None
+_ref_vec = None
 
 
 def build(quiet: bool = True) -> None:
@@ -110,6 +113,16 @@ def lib():
             ("hbo_align_element", C.c_uint8, [C.c_uint8, C.c_uint32]),
             ("hbo_split8", C.c_int, [u8p, C.c_uint64, C.c_uint32, C.c_uint32, u8p, u8p]),
             ("hbo_t32_split8", C.c_int, [u8p, C.c_uint64, C.c_uint32, C.c_uint32, u8p, u8p]),
+            ("hbo_reciprocal", C.c_uint32, [C.c_uint32]),
+            ("hbo_rsqrt", C.c_uint32, [C.c_uint32]),
+            ("hbo_count_reciprocal", C.c_uint32, [C.c_uint32]),
+            ("hbo_sum_tree", C.c_uint32, [u32p]),
+            ("hbo_max_tree", C.c_uint32, [u32p]),
+            ("hbo_fp32_max", C.c_uint32, [C.c_uint32, C.c_uint32]),
+            ("hbo_exp2", C.c_uint32, [C.c_uint32, u64p]),
+            ("hbo_row_lane", C.c_uint32, [C.c_int] * 5 + [C.c_uint32] * 9 + [u64p]),
+            ("hbo_apply_row_scalar", None, [C.c_int] * 5 + [u32p, u32p, C.c_uint32,
+                                                             C.c_uint32, u32p]),
             ("hbo_fp32_add_n", None, [u32p, u32p, u32p, C.c_uint64]),
             ("hbo_fp32_mul_n", None, [u32p, u32p, u32p, C.c_uint64]),
             ("hbo_fp32_mul_fraction_n", None, [u32p, u32p, u32p, C.c_uint64]),
@@ -180,6 +193,26 @@ def ref_batched(name, *arrays):
     fn = getattr(R, name)
     fn.argtypes = None
     return _batched(fn, *arrays)
+
+
+def ref_vec():
+    """The reference's compiled VEC lane / scalar-unit code (oracle/_ref), or None."""
+    global _ref_vec
+    if _ref_vec is None and os.path.exists(REF_VEC_PATH):
+        R = C.CDLL(REF_VEC_PATH)
+        u32 = C.c_uint32
+        for name, res, args in [
+            ("ref_reciprocal", u32, [u32]), ("ref_rsqrt", u32, [u32]),
+            ("ref_count_reciprocal", u32, [u32]), ("ref_fp32_max", u32, [u32, u32]),
+            ("ref_sum_tree", u32, [u32p]), ("ref_max_tree", u32, [u32p]),
+            ("ref_exp2", u32, [u32, u64p]),
+            ("ref_lane_output", u32, [C.c_int] * 5 + [u32] * 9 + [u64p]),
+            ("ref_apply_row_scalar", None, [C.c_int] * 5 + [u32p, u32p, u32, u32, u32p]),
+        ]:
+            getattr(R, name).restype = res
+            getattr(R, name).argtypes = args
+        _ref_vec = R
+    return _ref_vec
 
 
 def _untyped(name):

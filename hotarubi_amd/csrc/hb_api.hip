@@ -230,13 +230,112 @@ int CheckPass(const hb::VecPass& p, const PassSpec& s) {
   return HB_OK;
 }
 
+uint32_t HostNegate(uint32_t b) { return (b & 0x7FFFFFFFu) == 0 ? 0u : b ^ 0x80000000u; }
+
+// CountReciprocal (tools/iss/scalar.cpp:44-52, 64-69) for the Smem kRn
+// step of the norm programs.
+uint32_t HostCountReciprocal(uint32_t count) {
+  const uint32_t n = count & 0x3FFFu;
+  const int top = n == 0 ? 0 : hb::BitWidth32(n) - 1;
+  const uint32_t x = ((uint32_t)(127 + top) << 23) | ((n << (23 - top)) & 0x7FFFFFu);
+  uint32_t y = 0x7EF311C7u - x;
+  for (int i = 0; i < 4; ++i) y = hb::MulBits(y, hb::AddBits(0x40000000u, HostNegate(hb::MulBits(x, y))));
+  return y;
+}
+
+// Row programs (SOFTMAX, LAYERNORM, RMSNORM): the engine's failures in its
+// order (pairs of quads pass by pass, vec_rom.cpp:84-131 with two row
+// contexts; vec_engine.cpp:264-266, 383-387, 282-283), then this backend's
+// condition for running quads in parallel, then the launch.
+int VecRows(hb_ctx* ctx, const hb_vec_cmd* cmd, hb_onchip* o) {
+  hb::VecRowArgs a{};
+  a.entry = cmd->entry;
+  a.quantize = cmd->quantize ? 1u : 0u;
+  a.rows_q = cmd->rows_q & 0x1FFu;
+  a.n8 = cmd->n8 & 0xFFu;
+  a.src = cmd->src & 0xFFFu;
+  a.dst = cmd->dst & 0x1FFFu;
+  a.pbase = cmd->p_base & 0x1FFu;
+  a.aux = cmd->aux & 0x7FFu;
+  a.imm = cmd->imm;
+  a.quarter = a.n8 >> 2;
+  a.dst_step = a.n8 - (a.n8 - a.quarter) * a.quantize;
+  a.scratch = a.entry == hb::kRowSoftmax ? a.imm : (cmd->src2 & 0xFFFu);
+  a.rn = HostCountReciprocal(a.aux);
+  const uint32_t fmask = hb::kFbufDepth - 1, amask = hb::kAbufDepth - 1;
+  std::vector<uint8_t> written(hb::kFbufDepth);
+  hb::RowPassSpan spans[2][5];
+  const uint32_t groups = a.rows_q >> 1, tail = a.rows_q & 1u;
+  for (uint32_t g = 0; g <= groups; ++g) {
+    const uint32_t slots = g < groups ? 2u : tail;
+    int n = 0;
+    for (uint32_t k = 0; k < slots; ++k) n = hb::RowProgramSpans(a, 2 * g + k, spans[k]);
+    for (int i = 0; i < n; ++i)
+      for (uint32_t k = 0; k < slots; ++k) {
+        const hb::RowPassSpan& sp = spans[k][i];
+        if (a.n8 == 0) return Fail(HB_EBADCMD, "a PASS has 1 quads and 0 words");
+        std::fill(written.begin(), written.end(), 0);
+        const bool fbuf_store = sp.writes && !(sp.final_ && a.quantize);
+        for (uint32_t w = 0; w < a.n8; ++w) {
+          const uint32_t xa = (sp.src + w) & fmask;
+          if (written[xa]) return Fail(HB_EBADCMD, "a PASS reads FBUF word %u after writing it", xa);
+          if (fbuf_store) written[(sp.dst + w) & fmask] = 1;
+        }
+        if (sp.final_ && a.quantize && a.n8 % 4 != 0)
+          return Fail(HB_EBADCMD, "a PASS ends inside a block of 4 quantized words");
+      }
+  }
+  // The quads run in parallel: no word one quad writes may be touched by another.
+  std::vector<int32_t> owner(hb::kFbufDepth, -1), abuf_owner(hb::kAbufDepth, -1);
+  for (uint32_t q = 0; q < a.rows_q; ++q) {
+    hb::RowPassSpan sp[5];
+    const int n = hb::RowProgramSpans(a, q, sp);
+    for (int i = 0; i < n; ++i) {
+      if (!sp[i].writes) continue;
+      if (sp[i].final_ && a.quantize) {
+        for (uint32_t b = 0; b < a.n8 / 4; ++b) {
+          int32_t& ow = abuf_owner[((sp[i].dst & amask) + b) & amask];
+          if (ow >= 0 && ow != (int32_t)q)
+            return Fail(HB_EUNSUPPORTED, "row program quads %d and %u write one ABUF word", ow, q);
+          ow = (int32_t)q;
+        }
+        continue;
+      }
+      for (uint32_t w = 0; w < a.n8; ++w) {
+        int32_t& ow = owner[(sp[i].dst + w) & fmask];
+        if (ow >= 0 && ow != (int32_t)q)
+          return Fail(HB_EUNSUPPORTED, "row program quads %d and %u write one FBUF word", ow, q);
+        ow = (int32_t)q;
+      }
+    }
+  }
+  for (uint32_t q = 0; q < a.rows_q; ++q) {
+    hb::RowPassSpan sp[5];
+    const int n = hb::RowProgramSpans(a, q, sp);
+    for (int i = 0; i < n; ++i)
+      for (uint32_t w = 0; w < a.n8; ++w) {
+        const int32_t ow = owner[(sp[i].src + w) & fmask];
+        if (ow >= 0 && ow != (int32_t)q)
+          return Fail(HB_EUNSUPPORTED, "row program quad %u reads an FBUF word quad %d writes", q, ow);
+      }
+  }
+  hipError_t err = hb::LaunchVecRows(a, o->abuf, o->fbuf, o->pbuf, o->tbuf, ctx->stream);
+  if (err != hipSuccess) return HipFail(err, "VEC row program launch");
+  HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+
 int VecExec(hb_ctx* ctx, const hb_vec_cmd* cmd, hb_onchip* o) {
   if (int rc = Enter(ctx)) return rc;
   if (!cmd || !o) return Fail(HB_EINVAL, "null argument");
+  if (cmd->entry == hb::kRowSoftmax || cmd->entry == hb::kRowLayerNorm ||
+      cmd->entry == hb::kRowRmsNorm)
+    return VecRows(ctx, cmd, o);
   PassSpec specs[3];
   const int n = LibraryPasses(cmd->entry, specs);
   if (n == 0)
-    return Fail(HB_EUNSUPPORTED, "VEC library entry %u is not an epilogue program (0-9)",
+    return Fail(HB_EUNSUPPORTED,
+                "VEC library entry %u is not supported (0-9, 12 SOFTMAX, 22 LAYERNORM, 34 RMSNORM)",
                 cmd->entry);
   // VecEngine::Initialize (vec_engine.cpp:227-239): operand field widths.
   uint32_t reg[16] = {0};

@@ -158,4 +158,24 @@ hipError_t LaunchVecPass(const VecPass& pass, uint8_t* abuf, uint32_t* fbuf,
 hipError_t LaunchEncodeMxint8(const float* x, uint32_t rows, uint32_t cols, uint8_t* out,
                               uint32_t* bad_flag, hipStream_t stream);
 
+// Row programs of the VEC library (12 SOFTMAX, 22 LAYERNORM, 34 RMSNORM):
+// the register values of quad 0's slot and the per-quad steps.
+struct VecRowArgs {
+  uint32_t entry, quantize, rows_q, n8;
+  uint32_t src, scratch, dst, dst_step;  // unmasked register values
+  uint32_t pbase, quarter, aux, imm;
+  uint32_t rn;  // CountReciprocal(aux)
+};
+constexpr uint32_t kRowSoftmax = 12, kRowLayerNorm = 22, kRowRmsNorm = 34;
+// The FBUF (and PBUF) words each pass of a row program reads and writes for
+// one quad, for the host's checks: up to 5 passes.
+struct RowPassSpan {
+  uint32_t src, dst;  // register values (masked on use)
+  bool writes;        // an FBUF or final store
+  bool final_;        // the program's last pass (ABUF when quantizing)
+};
+int RowProgramSpans(const VecRowArgs& a, uint32_t quad, RowPassSpan* out);
+hipError_t LaunchVecRows(const VecRowArgs& a, uint8_t* abuf, uint32_t* fbuf, const uint32_t* pbuf,
+                         const uint64_t* tbuf, hipStream_t stream);
+
 }  // namespace hb

@@ -92,6 +92,6 @@ def test_failures(gpu, fields, text):
         hb.vec_execute(hb.VecCommand(**fields), dm)
     assert err.value.message == text
     with pytest.raises(hb.HbError) as err:
-        hb.vec_execute(hb.VecCommand(entry=12, rows_q=1, n8=4), dm)
+        hb.vec_execute(hb.VecCommand(entry=10, rows_q=1, n8=4), dm)
     assert err.value.code == hb.HB_EUNSUPPORTED
     dm.close()

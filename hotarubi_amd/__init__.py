@@ -48,7 +48,7 @@ EXPORTS = (
     "hb_gemm_encode", "hb_gemm_check", "hb_gemm_access", "hb_gemm_exec", "hb_gemm_exec_async",
     "hb_gemm_cycles", "hb_vec_exec", "hb_linear", "hb_linear_async",
     "hb_linear_batched_async", "hb_encode_mxint8", "hb_split8", "hb_split8_async",
-    "hb_t32_split8", "hb_t32_split8_async",
+    "hb_t32_split8", "hb_t32_split8_async", "hb_rows", "hb_rows_async",
 )
 
 
@@ -82,6 +82,13 @@ class _Piece(C.Structure):
 class _EpOp(C.Structure):
     _fields_ = [("op", C.c_uint32), ("imm", C.c_uint32), ("vec", C.c_void_p),
                 ("x2", C.c_void_p)]
+
+
+class _RowsDesc(C.Structure):
+    _fields_ = [("entry", C.c_uint32), ("rows", C.c_uint32), ("cols", C.c_uint32),
+                ("aux", C.c_uint32), ("imm", C.c_uint32), ("x", C.c_void_p),
+                ("gamma", C.c_void_p), ("beta", C.c_void_p), ("tbuf", C.c_void_p),
+                ("y", C.c_void_p), ("q_out", C.c_void_p)]
 
 
 class _LinearDesc(C.Structure):
@@ -166,6 +173,8 @@ def lib():
             "hb_linear_async": (i, [vp, C.POINTER(_LinearDesc)]),
             "hb_linear_batched_async": (i, [vp, C.POINTER(_LinearDesc), u32]),
             "hb_encode_mxint8": (i, [vp, vp, u32, u32, vp]),
+            "hb_rows": (i, [vp, C.POINTER(_RowsDesc)]),
+            "hb_rows_async": (i, [vp, C.POINTER(_RowsDesc)]),
             "hb_split8": (i, [vp, vp, C.c_uint64, u32, u32, vp, vp]),
             "hb_split8_async": (i, [vp, vp, C.c_uint64, u32, u32, vp, vp]),
             "hb_t32_split8": (i, [vp, vp, C.c_uint64, u32, u32, vp, vp]),
@@ -397,6 +406,21 @@ def linear_batched(descs, ctx: Context | None = None) -> None:
     ctx = ctx or default_context()
     arr = (_LinearDesc * len(descs))(*descs)
     _check(lib().hb_linear_batched_async(ctx.handle, arr, len(descs)))
+
+
+ROWS_SOFTMAX, ROWS_LAYERNORM, ROWS_RMSNORM = 12, 22, 34
+
+
+def rows(entry: int, x, rows: int, cols: int, aux: int, imm: int = 0, gamma=None, beta=None,
+         tbuf=None, y=None, q_out=None, ctx: Context | None = None, sync: bool = True) -> None:
+    """hb_rows: a VEC row program (12 SOFTMAX, 22 LAYERNORM, 34 RMSNORM;
+    vec_rom.cpp:133-212, 239-272) over fp32 [rows][cols] device rows, into y
+    (fp32) or q_out (MXINT8 DDR words, the A of `linear`)."""
+    ctx = ctx or default_context()
+    d = _RowsDesc(entry, rows, cols, aux, imm, _ptr(x), _ptr(gamma), _ptr(beta), _ptr(tbuf),
+                  _ptr(y), _ptr(q_out))
+    fn = lib().hb_rows if sync else lib().hb_rows_async
+    _check(fn(ctx.handle, C.byref(d)))
 
 
 def split8(src, rows: int, row_words: int, hi, lo, src_stride: int | None = None,

@@ -325,6 +325,48 @@ int VecRows(hb_ctx* ctx, const hb_vec_cmd* cmd, hb_onchip* o) {
   return HB_OK;
 }
 
+int Rows(hb_ctx* ctx, const hb_rows_desc* d, bool sync) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!d) return Fail(HB_EINVAL, "null descriptor");
+  if (d->entry != HB_ROWS_SOFTMAX && d->entry != HB_ROWS_LAYERNORM && d->entry != HB_ROWS_RMSNORM)
+    return Fail(HB_EUNSUPPORTED, "row program %u (12 SOFTMAX, 22 LAYERNORM, 34 RMSNORM)", d->entry);
+  if (d->rows < 1 || d->cols < 8 || d->cols % 8 != 0 || d->cols > 2040)
+    return Fail(HB_EINVAL, "rows = %u, cols = %u: need rows >= 1, cols a multiple of 8 up to 2040",
+                d->rows, d->cols);
+  if (!d->x || (d->y == nullptr) == (d->q_out == nullptr))
+    return Fail(HB_EINVAL, "need x and exactly one of y, q_out");
+  if (d->q_out && d->cols % 32 != 0) return Fail(HB_EINVAL, "q_out needs cols %% 32 == 0");
+  if (d->entry != HB_ROWS_SOFTMAX && !d->gamma) return Fail(HB_EINVAL, "the norm needs gamma");
+  if (d->entry == HB_ROWS_LAYERNORM && !d->beta) return Fail(HB_EINVAL, "LAYERNORM needs beta");
+  // the program reads beta from PBUF word p_base + n8/4: a separate row only
+  // when gamma fills whole words
+  if (d->entry == HB_ROWS_LAYERNORM && d->cols % 32 != 0)
+    return Fail(HB_EINVAL, "LAYERNORM needs cols %% 32 == 0");
+  if (d->entry == HB_ROWS_SOFTMAX && !d->tbuf) return Fail(HB_EINVAL, "SOFTMAX needs TBUF");
+  if ((d->rows + 3) / 4 > 0x7FFFFFFFu) return Fail(HB_EINVAL, "too many rows");
+  hb::VecRowArgs a{};
+  a.entry = d->entry;
+  a.quantize = d->q_out ? 1u : 0u;
+  a.rows_q = (d->rows + 3) / 4;
+  a.n8 = d->cols / 8;
+  a.quarter = a.n8 >> 2;
+  a.aux = d->aux & 0x7FFu;  // the command field's width
+  a.imm = d->imm;
+  a.rn = HostCountReciprocal(a.aux);
+  hb::VecRowDdr r{};
+  r.x = reinterpret_cast<const uint32_t*>(d->x);
+  r.gamma = reinterpret_cast<const uint32_t*>(d->gamma);
+  r.beta = reinterpret_cast<const uint32_t*>(d->beta);
+  r.y = reinterpret_cast<uint32_t*>(d->y);
+  r.q_out = static_cast<uint8_t*>(d->q_out);
+  r.rows = d->rows;
+  r.cols = d->cols;
+  hipError_t err = hb::LaunchRowsDdr(a, r, d->tbuf, ctx->stream);
+  if (err != hipSuccess) return HipFail(err, "row program launch");
+  if (sync) HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+
 int VecExec(hb_ctx* ctx, const hb_vec_cmd* cmd, hb_onchip* o) {
   if (int rc = Enter(ctx)) return rc;
   if (!cmd || !o) return Fail(HB_EINVAL, "null argument");
@@ -769,6 +811,9 @@ uint64_t hb_gemm_cycles(const hb_gemm_cmd* c, uint32_t fixed_cycles) {
 }
 
 int hb_vec_exec(hb_ctx* ctx, const hb_vec_cmd* cmd, hb_onchip* o) { return VecExec(ctx, cmd, o); }
+
+int hb_rows(hb_ctx* ctx, const hb_rows_desc* d) { return Rows(ctx, d, true); }
+int hb_rows_async(hb_ctx* ctx, const hb_rows_desc* d) { return Rows(ctx, d, false); }
 
 int hb_linear_async(hb_ctx* ctx, const hb_linear_desc* d) {
   if (int rc = Enter(ctx)) return rc;

@@ -175,7 +175,18 @@ struct RowPassSpan {
   bool final_;        // the program's last pass (ABUF when quantizing)
 };
 int RowProgramSpans(const VecRowArgs& a, uint32_t quad, RowPassSpan* out);
+// The same programs over row-major DDR tensors (hb_rows): rows of the last
+// quad past `rows` are zero rows whose results are not stored.
+struct VecRowDdr {
+  const uint32_t* x;  // fp32 [rows][cols]
+  const uint32_t *gamma, *beta;  // fp32 [cols]
+  uint32_t* y;        // fp32 [rows][cols] (not quantizing)
+  uint8_t* q_out;     // MXINT8 DDR words [ceil(rows/4)][cols/32] (quantizing)
+  uint32_t rows, cols;
+};
 hipError_t LaunchVecRows(const VecRowArgs& a, uint8_t* abuf, uint32_t* fbuf, const uint32_t* pbuf,
                          const uint64_t* tbuf, hipStream_t stream);
+hipError_t LaunchRowsDdr(const VecRowArgs& a, const VecRowDdr& d, const uint64_t* tbuf,
+                         hipStream_t stream);
 
 }  // namespace hb

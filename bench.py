@@ -338,13 +338,16 @@ class ExpertAttention:
     attention (odd) layers and 128 + 64 on the self-attention (even) layers.
     Per layer: SPLIT8 of K and T32_SPLIT8 of V over every KV head and batch
     element at once; per query head, scores = Q_h K_j^T (W8, with the mask
-    add on self layers and the 1/8 scale fused) and O_h = P_h V_j (W8).
-    The query head's words are read out of the projection output in place
-    (a_stride 30).  Softmax is outside this path: P is a synthetic MXINT8
-    tensor of its shape.  Each batch element's rows start on a quad (13
-    quads per element)."""
+    add on self layers and the 1/8 scale fused); the SOFTMAX program with
+    MXINT8 requantize over every head's scores at once (valid keys: all on
+    self layers, the 77-token prefix on cross layers); per query head
+    O_h = P_h V_j (W8).  The query head's words are read out of the
+    projection output in place (a_stride 30).  Each (element, head) block
+    of scores has 52 rows (13 quads; rows 50 and 51 stay zero), so its
+    probabilities are whole MXINT8 words, the A of its PV layer."""
 
     LAYERS, HEADS, KV, HW, QW, KVW, ROWS, PREFIX, SUFFIX = 16, 15, 5, 2, 30, 10, 50, 128, 64
+    VALID_PREFIX = 77  # smolvla_parts_test.cpp:36: one camera, Prefix() 77 of Tokens() 128
     STREAMS = 4  # the head groups are independent: side streams, one context each
 
     def __init__(self, hb, torch, batch, mode, seed=41):
@@ -365,13 +368,14 @@ class ExpertAttention:
         # intermediates reused by every layer: planes, scores, P, O
         kh = torch.empty((2, batch * max_keys // 8 * self.KVW, 144), dtype=torch.uint8, device=dev)
         vh = torch.empty((2, 4 * self.KVW * batch * kbk_max, 144), dtype=torch.uint8, device=dev)
-        s = torch.empty((batch * self.HEADS * self.ROWS * max_keys,), dtype=torch.float32, device=dev)
-        s_at = self.ROWS * max_keys  # element (b, h)'s scores: [ROWS][keys] from (b * 15 + h) * s_at
-        p_words = words(batch * self.HEADS * quads * kbk_max).view(batch, self.HEADS, -1, 144)
+        blocks = batch * self.HEADS
+        s = torch.zeros((blocks * quads * 4 * max_keys,), dtype=torch.float32, device=dev)
+        p_words = torch.zeros((blocks * quads * kbk_max, 144), dtype=torch.uint8, device=dev)
         o = torch.empty((batch, self.HEADS, self.ROWS, 64), dtype=torch.float32, device=dev)
+        tb = torch.from_numpy(activation_table("silu").view(np.int64)).to(dev)
         mask = torch.zeros((self.ROWS, max_keys), dtype=torch.float32, device=dev)
         mask[:, self.PREFIX:] = -1e4 * torch.triu(torch.ones(self.ROWS, self.SUFFIX, device=dev), 1)
-        self.keep += [kh, vh, s, o, mask]
+        self.keep += [kh, vh, s, p_words, o, mask, tb]
         scale = int(np.array(0.125, np.float32).view(np.uint32))
         for layer in range(self.LAYERS):
             keys = self.PREFIX + (self.SUFFIX if layer % 2 == 0 else 0)
@@ -382,6 +386,7 @@ class ExpertAttention:
             self.steps.append(("t32", v, rows, vh))
             ops = ([(hb.EP_ADD, mask)] if keys == max_keys else []) + [(hb.EP_SCALE, scale)]
             share, kb_all = self.HEADS // self.KV, batch * kbk
+            s_at, p_at = quads * 4 * keys, quads * kbk  # block (b, h) = b * 15 + h
 
             def qk(b, h):  # scores: W = K_j planes of element b, 10 words per group row
                 j = h // share
@@ -394,7 +399,7 @@ class ExpertAttention:
             def pv(b, h):  # O_h = P_h V_j: V^T planes of head j, element b's blocks per group row
                 j = h // share
                 return hb.linear_desc(
-                    self.ROWS, 64, kb_all, p_words[b, h],
+                    self.ROWS, 64, kb_all, p_words[(b * self.HEADS + h) * p_at:],
                     [vh[pl, 8 * j * kb_all + b * kbk:] for pl in range(2)], [1, 2], o[b, h],
                     pieces=[(0, kbk, 0)], a_stride=kbk, mode=mode)
 
@@ -404,12 +409,17 @@ class ExpertAttention:
             groups = ([[(0, share * j + r) for j in range(self.KV)] for r in range(share)]
                       if batch == 1 else
                       [[(b, h) for b in range(batch)] for h in range(self.HEADS)])
-            # a head group's QK^T then PV, the groups on side streams in turn
-            self.steps.append(("fork",))
-            for i, grp in enumerate(groups):
-                for fn in (qk, pv):
+            # the head groups' QK^T on side streams in turn, one softmax over
+            # every block's scores, then the groups' PV
+            valid = keys if keys == max_keys else self.VALID_PREFIX
+            for fn in (qk, None, pv):
+                if fn is None:
+                    self.steps.append(("softmax", s, blocks * quads * 4, keys, valid, tb, p_words))
+                    continue
+                self.steps.append(("fork",))
+                for i, grp in enumerate(groups):
                     self.steps.append(("linear", [fn(b, h) for b, h in grp], i % self.STREAMS))
-            self.steps.append(("join",))
+                self.steps.append(("join",))
             self.ops += batch * self.HEADS * 2.0 * self.ROWS * 64 * keys * 2
         self.side = [torch.cuda.Stream() for _ in range(self.STREAMS)]
         self.side_ctx = [hb.Context(0) for _ in range(self.STREAMS)]
@@ -425,6 +435,9 @@ class ExpertAttention:
                 hb.split8(st[1], st[2], self.KVW, st[3][0], st[3][1], ctx=ctx, sync=False)
             elif st[0] == "t32":
                 hb.t32_split8(st[1], st[2], self.KVW, st[3][0], st[3][1], ctx=ctx, sync=False)
+            elif st[0] == "softmax":
+                hb.rows(hb.ROWS_SOFTMAX, st[1], st[2], st[3], st[4], tbuf=st[5], q_out=st[6],
+                        ctx=ctx, sync=False)
             elif st[0] == "fork":
                 for side in self.side:
                     side.wait_stream(main)
@@ -437,6 +450,44 @@ class ExpertAttention:
     def close(self):
         for c in self.side_ctx:
             c.close()
+
+
+def time_row_programs(hb, torch, ctx, stream, steps=10):
+    """The VEC row programs over device rows with MXINT8 output (hb_rows) at
+    model shapes; algorithmic bytes = fp32 rows read + MXINT8 words written
+    + the fp32 row vectors."""
+    dev, out = "cuda:0", {}
+    tb = torch.from_numpy(activation_table("silu").view(np.int64)).to(dev)
+    eps = int(np.array(1e-6, np.float32).view(np.uint32))
+    for name, entry, rows, cols, aux in (
+            ("rmsnorm_q SmolVLA LM B=32 (4512 x 960)", hb.ROWS_RMSNORM, 32 * 141, 960, 960),
+            ("layernorm_q SigLIP (2048 x 768)", hb.ROWS_LAYERNORM, 2048, 768, 768),
+            ("softmax_q expert attention B=32 (24960 x 192)", hb.ROWS_SOFTMAX, 32 * 15 * 52, 192, 192)):
+        x = torch.randn((rows, cols), device=dev)
+        g = torch.rand(cols, device=dev) + 0.5
+        b = torch.randn(cols, device=dev) * 0.1
+        q = torch.empty(((rows + 3) // 4 * cols // 32, 144), dtype=torch.uint8, device=dev)
+
+        def call():
+            hb.rows(entry, x, rows, cols, aux, eps, g, b, tb, q_out=q, ctx=ctx, sync=False)
+        for _ in range(2):
+            call()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(steps):
+            call()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        vectors = {hb.ROWS_RMSNORM: 1, hb.ROWS_LAYERNORM: 2}.get(entry, 0)
+        nbytes = 4.0 * rows * cols + q.numel() + 4.0 * cols * vectors
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 4), "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
+                                                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                                      "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+        del x, g, b, q
+    return out
 
 
 def time_split_kernels(hb, torch, ctx, stream, rows=200000, row_words=10, steps=10):
@@ -736,11 +787,14 @@ def main():
         ctx.set_stream(stream.cuda_stream)
 
     if not args.quick and args.only in (None, "attention"):
-        # attention operands built on device (SPLIT8 / T32_SPLIT8) and the
-        # expert step's attention GEMMs over them
+        # attention operands built on device (SPLIT8 / T32_SPLIT8), the row
+        # programs (norms, softmax) with requantize, and the expert step's
+        # attention over them
         out["attention_operands"] = time_split_kernels(hb, torch, ctx, stream)
-        att = {"workload": "SmolVLA expert attention: 16 layers x 15 heads, QK^T (mask, scale) "
-                           "and PV in W8 over SPLIT8 / T32_SPLIT8 operands, 50 rows per element"}
+        out["row_programs"] = time_row_programs(hb, torch, ctx, stream)
+        att = {"workload": "SmolVLA expert attention: 16 layers x 15 heads, QK^T (mask, scale), "
+                           "softmax + MXINT8, PV in W8 over SPLIT8 / T32_SPLIT8 operands, 50 rows "
+                           "per element"}
         for b in (1, 32):
             wk = ExpertAttention(hb, torch, b, mode)
             t = time_chain(torch, ctx, wk, steps=5)

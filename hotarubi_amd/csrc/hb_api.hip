@@ -875,9 +875,85 @@ int DmaSplit(hb_ctx* ctx, const void* src, uint64_t stride, uint32_t rows, uint3
   return HB_OK;
 }
 
+// Row format (dma_engine.cpp:96-125): the reference's checks in its order,
+// then this backend's alignment needs.
+int RowFormatCheck(uint32_t rows, uint32_t row_words, uint32_t tok, bool indexed,
+                   uint32_t* token_bytes) {
+  if (rows == 0 || row_words == 0)
+    return Fail(HB_EBADCMD, "a DMA transfer with %u rows of %u words", rows, row_words);
+  if (tok < 1 || tok > 32) return Fail(HB_EBADCMD, "row format with tok = %u", tok);
+  const uint32_t bytes = (2 * tok + (tok > 16 ? 2u : 1u)) * 16u;
+  const uint64_t units = (uint64_t)rows * row_words;
+  if (units % 4 != 0)
+    return Fail(HB_EBADCMD, "row format with %llu tokens, not a multiple of 4",
+                (unsigned long long)units);
+  if (!indexed && (uint64_t)row_words * (bytes / 16) >= 65536)
+    return Fail(HB_EBADCMD, "row format with %u tokens of %u bytes per row", row_words, bytes);
+  if (units * tok >= (1ull << 32)) return Fail(HB_EINVAL, "too many tokens");
+  *token_bytes = bytes;
+  return HB_OK;
+}
+
+bool Aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+int RowLoad(hb_ctx* ctx, const void* src, uint64_t stride, uint32_t rows, uint32_t row_words,
+            uint32_t tok, const uint32_t* index, void* out, bool sync) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!src || !out) return Fail(HB_EINVAL, "null row format buffer");
+  uint32_t bytes = 0;
+  if (int rc = RowFormatCheck(rows, row_words, tok, index != nullptr, &bytes)) return rc;
+  if (!Aligned16(src) || !Aligned16(out) || (!index && stride % 16 != 0))
+    return Fail(HB_EINVAL, "row format buffers must be 16-byte aligned, the stride whole beats");
+  if (!index && stride < (uint64_t)row_words * bytes)
+    return Fail(HB_EINVAL, "row stride %llu is shorter than %u tokens of %u bytes",
+                (unsigned long long)stride, row_words, bytes);
+  const hipError_t err = hb::LaunchRowLoad(static_cast<const uint8_t*>(src), stride, rows,
+                                           row_words, tok, bytes, index,
+                                           static_cast<uint8_t*>(out), ctx->stream);
+  if (err != hipSuccess) return HipFail(err, "row format load launch");
+  if (sync) HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+
+int RowStore(hb_ctx* ctx, const void* words, uint32_t rows, uint32_t row_words, uint32_t tok,
+             void* dst, uint64_t stride, bool sync) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!words || !dst) return Fail(HB_EINVAL, "null row format buffer");
+  uint32_t bytes = 0;
+  if (int rc = RowFormatCheck(rows, row_words, tok, false, &bytes)) return rc;
+  if (!Aligned16(words) || !Aligned16(dst) || stride % 16 != 0)
+    return Fail(HB_EINVAL, "row format buffers must be 16-byte aligned, the stride whole beats");
+  if (stride < (uint64_t)row_words * bytes)
+    return Fail(HB_EINVAL, "row stride %llu is shorter than %u tokens of %u bytes",
+                (unsigned long long)stride, row_words, bytes);
+  const hipError_t err = hb::LaunchRowStore(static_cast<const uint8_t*>(words), rows, row_words,
+                                            tok, bytes, static_cast<uint8_t*>(dst), stride,
+                                            ctx->stream);
+  if (err != hipSuccess) return HipFail(err, "row format store launch");
+  if (sync) HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int hb_row_load(hb_ctx* ctx, const void* src, uint64_t row_stride, uint32_t rows,
+                uint32_t row_words, uint32_t tok, const uint32_t* index, void* out) {
+  return RowLoad(ctx, src, row_stride, rows, row_words, tok, index, out, true);
+}
+int hb_row_load_async(hb_ctx* ctx, const void* src, uint64_t row_stride, uint32_t rows,
+                      uint32_t row_words, uint32_t tok, const uint32_t* index, void* out) {
+  return RowLoad(ctx, src, row_stride, rows, row_words, tok, index, out, false);
+}
+int hb_row_store(hb_ctx* ctx, const void* words, uint32_t rows, uint32_t row_words, uint32_t tok,
+                 void* dst, uint64_t row_stride) {
+  return RowStore(ctx, words, rows, row_words, tok, dst, row_stride, true);
+}
+int hb_row_store_async(hb_ctx* ctx, const void* words, uint32_t rows, uint32_t row_words,
+                       uint32_t tok, void* dst, uint64_t row_stride) {
+  return RowStore(ctx, words, rows, row_words, tok, dst, row_stride, false);
+}
 
 int hb_split8(hb_ctx* ctx, const void* src, uint64_t src_stride, uint32_t rows, uint32_t row_words,
               void* hi, void* lo) {

@@ -135,6 +135,11 @@ hipError_t LaunchEpilogue(const GemmArgs& args, hipStream_t stream);
 // DMA-engine W8 operand builders (hb_dma.hip).
 hipError_t LaunchSplit8(const uint8_t* src, uint64_t stride, uint32_t rows, uint32_t row_words,
                         uint8_t* hi, uint8_t* lo, hipStream_t stream);
+hipError_t LaunchRowLoad(const uint8_t* src, uint64_t stride, uint32_t rows, uint32_t row_words,
+                        uint32_t tok, uint32_t token_bytes, const uint32_t* index, uint8_t* out,
+                        hipStream_t stream);
+hipError_t LaunchRowStore(const uint8_t* words, uint32_t rows, uint32_t row_words, uint32_t tok,
+                         uint32_t token_bytes, uint8_t* dst, uint64_t stride, hipStream_t stream);
 hipError_t LaunchT32Split8(const uint8_t* src, uint64_t stride, uint32_t rows, uint32_t row_words,
                            uint8_t* hi, uint8_t* lo, hipStream_t stream);
 

@@ -299,6 +299,35 @@ int hb_t32_split8(hb_ctx* ctx, const void* src, uint64_t src_stride, uint32_t ro
 int hb_t32_split8_async(hb_ctx* ctx, const void* src, uint64_t src_stride, uint32_t rows,
                         uint32_t row_words, void* hi, void* lo);
 
+/* ----------------------------------------------------- row format -- */
+
+/* The DMA engine's row format for MXINT8 tokens (DMA_LD / DMA_ST of kind
+ * ROW and ROW_INDEXED, tools/iss/dma_engine.cpp:96-279; docs/design.md "Row
+ * format"): a token is tok blocks of 32 int8, then its tok scale bytes,
+ * zero-padded to 16 bytes ((2 tok + (tok > 16 ? 2 : 1)) * 16 bytes); tokens
+ * 4q..4q+3 make quad q of the DDR A words hb_linear takes ([quads][tok] x
+ * 144 B: bytes 32j.. token j's block, 128 + j its scale, 132..143 zero).
+ *
+ * hb_row_load replaces LoadRows: rows x row_words tokens, row r at byte
+ * r * row_stride of src; or, with index != NULL (ROW_INDEXED, device
+ * memory), token e at byte 16 * index[e] of src, 0xFFFFFFFF a zero token
+ * (scale bytes 127).  hb_row_store replaces StoreRows (ROW only): the
+ * inverse, each token's pad bytes written zero.  The reference's checks
+ * return HB_EBADCMD with its texts ("a DMA transfer with R rows of W
+ * words", "row format with tok = T", "row format with N tokens, not a
+ * multiple of 4", "row format with N tokens of B bytes per row");
+ * buffers must be 16-byte aligned and row_stride whole 16-byte beats, at
+ * least a row (HB_EINVAL).  FP32 tokens (FBUF) are plain fp32 rows at this
+ * level and need no conversion. */
+int hb_row_load(hb_ctx* ctx, const void* src, uint64_t row_stride, uint32_t rows,
+                uint32_t row_words, uint32_t tok, const uint32_t* index, void* out);
+int hb_row_load_async(hb_ctx* ctx, const void* src, uint64_t row_stride, uint32_t rows,
+                      uint32_t row_words, uint32_t tok, const uint32_t* index, void* out);
+int hb_row_store(hb_ctx* ctx, const void* words, uint32_t rows, uint32_t row_words, uint32_t tok,
+                 void* dst, uint64_t row_stride);
+int hb_row_store_async(hb_ctx* ctx, const void* words, uint32_t rows, uint32_t row_words,
+                       uint32_t tok, void* dst, uint64_t row_stride);
+
 /* --------------------------------------------------- row programs -- */
 
 /* The VEC row programs over row-major tensors in device memory: what

@@ -490,6 +490,39 @@ def time_row_programs(hb, torch, ctx, stream, steps=10):
     return out
 
 
+def time_row_format(hb, torch, ctx, stream, tokens=262144, tok=30, steps=10):
+    """hb_row_load / hb_row_store of `tokens` MXINT8 tokens of tok blocks (the
+    SmolVLA width 960: 976 bytes each, past the last-level cache);
+    algorithmic bytes = the tokens read + the A words written (or the
+    reverse)."""
+    dev = "cuda:0"
+    size = hb.row_token_bytes(tok)
+    src = torch.randint(0, 256, (tokens * size,), dtype=torch.uint8, device=dev)
+    words = torch.empty((tokens // 4 * tok, 144), dtype=torch.uint8, device=dev)
+    nbytes = float(tokens * size + words.numel())
+    out = {"workload": f"{tokens} tokens of {tok} blocks ({tokens * size / 1e6:.0f} MB of tokens, "
+                       f"{words.numel() / 1e6:.0f} MB of A words)"}
+    for name, call in (
+            ("load", lambda: hb.row_load(src, tokens, 1, tok, words, ctx=ctx, sync=False)),
+            ("store", lambda: hb.row_store(words, tokens, 1, tok, src, ctx=ctx, sync=False))):
+        for _ in range(2):
+            call()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(steps):
+            call()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 4), "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
+                                                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                                      "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    del src, words
+    return out
+
+
 def time_split_kernels(hb, torch, ctx, stream, rows=200000, row_words=10, steps=10):
     """HBM rate of SPLIT8 and T32_SPLIT8 over a K / V matrix of rows x
     row_words MXINT8 words (rows * row_words * 144 B, larger than the
@@ -792,6 +825,7 @@ def main():
         # attention over them
         out["attention_operands"] = time_split_kernels(hb, torch, ctx, stream)
         out["row_programs"] = time_row_programs(hb, torch, ctx, stream)
+        out["row_format"] = time_row_format(hb, torch, ctx, stream)
         att = {"workload": "SmolVLA expert attention: 16 layers x 15 heads, QK^T (mask, scale), "
                            "softmax + MXINT8, PV in W8 over SPLIT8 / T32_SPLIT8 operands, 50 rows "
                            "per element"}

@@ -159,14 +159,17 @@ __global__ __launch_bounds__(64 * kT32Waves) void T32Split8Kernel(const uint8_t*
 // 96-279): an MXINT8 token is tok blocks of 32 bytes, then its tok scale
 // bytes, zero-padded to 16 bytes; tokens 4q..4q+3 are the quad q of DDR A
 // words [q][block] (bytes 32j.. token j's block, 128 + j its scale).  One
-// thread per (token, block): two 16-byte loads and stores and a scale byte.
+// thread per (quad, block, token j), j fastest: four neighbouring threads
+// fill one word, and a token's blocks come from threads 4 apart, so both
+// the token side and the word side are read and written in runs.
 __global__ __launch_bounds__(256) void RowLoadKernel(const uint8_t* src, uint64_t stride,
                                                      uint32_t row_words, uint32_t tok,
                                                      uint32_t token_bytes, const uint32_t* index,
                                                      uint32_t units, uint8_t* out) {
   const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (uint64_t)units * tok) return;
-  const uint32_t u = (uint32_t)(i / tok), w = (uint32_t)(i % tok), j = u % 4;
+  const uint32_t j = (uint32_t)(i % 4), w = (uint32_t)((i / 4) % tok);
+  const uint32_t u = (uint32_t)(i / (4ull * tok)) * 4 + j;
   u32x4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
   uint8_t scale = 127;  // a null entry: a zero token
   const uint8_t* t = nullptr;
@@ -193,7 +196,8 @@ __global__ __launch_bounds__(256) void RowStoreKernel(const uint8_t* words, uint
                                                       uint64_t stride) {
   const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (uint64_t)units * tok) return;
-  const uint32_t u = (uint32_t)(i / tok), w = (uint32_t)(i % tok), j = u % 4;
+  const uint32_t j = (uint32_t)(i % 4), w = (uint32_t)((i / 4) % tok);
+  const uint32_t u = (uint32_t)(i / (4ull * tok)) * 4 + j;
   const uint8_t* word = words + ((uint64_t)(u / 4) * tok + w) * kDdrWord;
   uint8_t* t = dst + (uint64_t)(u / row_words) * stride + (uint64_t)(u % row_words) * token_bytes;
   *reinterpret_cast<u32x4*>(t + 32 * w) = *reinterpret_cast<const u32x4*>(word + 32 * j);

@@ -50,6 +50,7 @@ EXPORTS = (
     "hb_linear_batched_async", "hb_encode_mxint8", "hb_split8", "hb_split8_async",
     "hb_t32_split8", "hb_t32_split8_async", "hb_rows", "hb_rows_async",
     "hb_row_load", "hb_row_load_async", "hb_row_store", "hb_row_store_async",
+    "hb_gacc", "hb_gacc_async",
 )
 
 
@@ -90,6 +91,12 @@ class _RowsDesc(C.Structure):
                 ("aux", C.c_uint32), ("imm", C.c_uint32), ("x", C.c_void_p),
                 ("gamma", C.c_void_p), ("beta", C.c_void_p), ("tbuf", C.c_void_p),
                 ("y", C.c_void_p), ("q_out", C.c_void_p)]
+
+
+class _GaccDesc(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("list", C.c_void_p), ("list_stride", C.c_uint64),
+                ("quads", C.c_uint32), ("slots", C.c_uint32), ("blocks", C.c_uint32),
+                ("w_stride", C.c_uint32), ("accumulate", C.c_uint32), ("out", C.c_void_p)]
 
 
 class _LinearDesc(C.Structure):
@@ -174,6 +181,8 @@ def lib():
             "hb_linear_async": (i, [vp, C.POINTER(_LinearDesc)]),
             "hb_linear_batched_async": (i, [vp, C.POINTER(_LinearDesc), u32]),
             "hb_encode_mxint8": (i, [vp, vp, u32, u32, vp]),
+            "hb_gacc": (i, [vp, C.POINTER(_GaccDesc)]),
+            "hb_gacc_async": (i, [vp, C.POINTER(_GaccDesc)]),
             "hb_row_load": (i, [vp, vp, C.c_uint64, u32, u32, u32, vp, vp]),
             "hb_row_load_async": (i, [vp, vp, C.c_uint64, u32, u32, u32, vp, vp]),
             "hb_row_store": (i, [vp, vp, u32, u32, u32, vp, C.c_uint64]),
@@ -411,6 +420,18 @@ def linear_batched(descs, ctx: Context | None = None) -> None:
     ctx = ctx or default_context()
     arr = (_LinearDesc * len(descs))(*descs)
     _check(lib().hb_linear_batched_async(ctx.handle, arr, len(descs)))
+
+
+def gacc(base, lst, quads: int, slots: int, blocks: int, w_stride: int, out,
+         list_stride: int = 0, accumulate: bool = False, ctx: Context | None = None,
+         sync: bool = True) -> None:
+    """hb_gacc: the DMA engine's gather-accumulate (dma_engine.cpp:596-656)
+    over `quads` quads' lists, into out fp32 [quads * 4][32 * blocks]."""
+    ctx = ctx or default_context()
+    d = _GaccDesc(_ptr(base), _ptr(lst), list_stride, quads, slots, blocks, w_stride,
+                  1 if accumulate else 0, _ptr(out))
+    fn = lib().hb_gacc if sync else lib().hb_gacc_async
+    _check(fn(ctx.handle, C.byref(d)))
 
 
 def row_token_bytes(tok: int) -> int:

@@ -934,9 +934,43 @@ int RowStore(hb_ctx* ctx, const void* words, uint32_t rows, uint32_t row_words, 
   return HB_OK;
 }
 
+int Gacc(hb_ctx* ctx, const hb_gacc_desc* d, bool sync) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!d || !d->base || !d->list || !d->out) return Fail(HB_EINVAL, "null GACC argument");
+  // the reference's checks in its order (dma_engine.cpp Execute, Gather)
+  if (d->slots == 0 || d->blocks == 0)
+    return Fail(HB_EBADCMD, "a DMA transfer with %u rows of %u words", d->slots, d->blocks);
+  if (d->blocks > 8) return Fail(HB_EBADCMD, "GACC with %u blocks per token", d->blocks);
+  if (d->slots > 2047) return Fail(HB_EBADCMD, "GACC with %u slots", d->slots);
+  if (d->quads < 1) return Fail(HB_EINVAL, "GACC over no quads");
+  if (reinterpret_cast<uintptr_t>(d->list) % 16 != 0 || d->list_stride % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(d->base) % 16 != 0)
+    return Fail(HB_EINVAL, "GACC lists and base must be 16-byte aligned");
+  if (d->quads > 1 && d->list_stride < 16 + 128ull * d->slots)
+    return Fail(HB_EINVAL, "GACC list stride %llu is shorter than a list of %u slots",
+                (unsigned long long)d->list_stride, d->slots);
+  hb::GaccArgs a{};
+  a.base = static_cast<const uint8_t*>(d->base);
+  a.list = static_cast<const uint8_t*>(d->list);
+  a.list_stride = d->list_stride;
+  a.quads = d->quads;
+  a.slots = d->slots;
+  a.blocks = d->blocks;
+  a.w_stride = d->w_stride;
+  a.accumulate = d->accumulate ? 1u : 0u;
+  a.out = d->out;
+  const hipError_t err = hb::LaunchGacc(a, ctx->stream);
+  if (err != hipSuccess) return HipFail(err, "GACC launch");
+  if (sync) HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int hb_gacc(hb_ctx* ctx, const hb_gacc_desc* d) { return Gacc(ctx, d, true); }
+int hb_gacc_async(hb_ctx* ctx, const hb_gacc_desc* d) { return Gacc(ctx, d, false); }
 
 int hb_row_load(hb_ctx* ctx, const void* src, uint64_t row_stride, uint32_t rows,
                 uint32_t row_words, uint32_t tok, const uint32_t* index, void* out) {

@@ -140,6 +140,14 @@ hipError_t LaunchRowLoad(const uint8_t* src, uint64_t stride, uint32_t rows, uin
                         hipStream_t stream);
 hipError_t LaunchRowStore(const uint8_t* words, uint32_t rows, uint32_t row_words, uint32_t tok,
                          uint32_t token_bytes, uint8_t* dst, uint64_t stride, hipStream_t stream);
+struct GaccArgs {
+  const uint8_t* base;  // byte 0 of the 16-byte unit addresses
+  const uint8_t* list;  // quad 0's list
+  uint64_t list_stride;
+  uint32_t quads, slots, blocks, w_stride, accumulate;
+  float* out;           // [quads * 4][32 * blocks]
+};
+hipError_t LaunchGacc(const GaccArgs& a, hipStream_t stream);
 hipError_t LaunchT32Split8(const uint8_t* src, uint64_t stride, uint32_t rows, uint32_t row_words,
                            uint8_t* hi, uint8_t* lo, hipStream_t stream);
 

@@ -523,6 +523,61 @@ def time_row_format(hb, torch, ctx, stream, tokens=262144, tok=30, steps=10):
     return out
 
 
+def time_gacc(hb, torch, ctx, stream, frames=(1, 16), slots=52, blocks=8, cameras=6,
+              feature_rows=100000, steps=5):
+    """GACC at the SparseDrive-S head's deformable aggregation shape: 900
+    anchors (225 quads) per frame, 256 channels (8 blocks), per camera a list
+    of 52 slots (13 points x 4 levels, 4 bilinear corners per token), the 6
+    cameras chained through the accumulators; random rows of a 100,000-row
+    feature pool, 10% null entries.  Reported per frame batch: ms for the 6
+    chained commands and the gathered rows per second."""
+    dev, out = "cuda:0", {}
+    row_bytes = hb.row_token_bytes(blocks)
+    rng = np.random.default_rng(5)
+    for f in frames:
+        quads = 225 * f
+        w_words = (slots + 7) // 8
+        w_bytes, list_bytes = blocks * w_words * 128, 16 + 128 * slots
+        w_base = feature_rows * row_bytes
+        list_base = w_base + quads * w_bytes
+        size = list_base + cameras * quads * list_bytes
+        img = torch.randint(0, 256, (size,), dtype=torch.uint8, device=dev)
+        img[w_base:list_base] = torch.randint(0x39000000 // 256, 0x3C000000 // 256,
+                                              ((list_base - w_base) // 4,), device=dev,
+                                              dtype=torch.int32).mul(256).view(torch.uint8)
+        hdr = np.zeros((cameras * quads, 16), np.uint8)
+        hdr[:, :4] = ((w_base + (np.arange(cameras * quads) % quads) * w_bytes) // 16
+                      ).astype(np.uint32).view(np.uint8).reshape(-1, 4)
+        rows = rng.integers(0, feature_rows, (cameras * quads, slots * 16))
+        entries = (rows * row_bytes // 16).astype(np.uint64)
+        entries[rng.random(entries.shape) < 0.1] = 0xFFFFFFFF
+        bw = np.full(entries.shape, 0x3E800000, np.uint64)
+        lists = np.concatenate([hdr, (entries | (bw << np.uint64(32))).view(np.uint8)], axis=1)
+        img[list_base:] = torch.from_numpy(lists.reshape(-1)).to(dev)
+        acc = torch.zeros((quads * 4, 32 * blocks), dtype=torch.float32, device=dev)
+
+        def run():
+            for c in range(cameras):
+                hb.gacc(img, img[list_base + c * quads * list_bytes:], quads, slots, blocks,
+                        w_words * 8, acc, list_stride=list_bytes, accumulate=c > 0, ctx=ctx,
+                        sync=False)
+        run()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(steps):
+            run()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        gathered = float((entries != 0xFFFFFFFF).sum())
+        out[f"frames={f}"] = {"quads": quads, "ms": round(ms, 4),
+                              "rows_per_s": round(gathered / (ms * 1e-3), 0),
+                              "gathered_bytes_per_s": round(gathered * row_bytes / (ms * 1e-3), 0)}
+        del img, acc
+    return out
+
+
 def time_split_kernels(hb, torch, ctx, stream, rows=200000, row_words=10, steps=10):
     """HBM rate of SPLIT8 and T32_SPLIT8 over a K / V matrix of rows x
     row_words MXINT8 words (rows * row_words * 144 B, larger than the
@@ -826,6 +881,7 @@ def main():
         out["attention_operands"] = time_split_kernels(hb, torch, ctx, stream)
         out["row_programs"] = time_row_programs(hb, torch, ctx, stream)
         out["row_format"] = time_row_format(hb, torch, ctx, stream)
+        out["gacc_sparsedrive"] = time_gacc(hb, torch, ctx, stream)
         att = {"workload": "SmolVLA expert attention: 16 layers x 15 heads, QK^T (mask, scale), "
                            "softmax + MXINT8, PV in W8 over SPLIT8 / T32_SPLIT8 operands, 50 rows "
                            "per element"}

@@ -944,8 +944,8 @@ int Gacc(hb_ctx* ctx, const hb_gacc_desc* d, bool sync) {
   if (d->slots > 2047) return Fail(HB_EBADCMD, "GACC with %u slots", d->slots);
   if (d->quads < 1) return Fail(HB_EINVAL, "GACC over no quads");
   if (reinterpret_cast<uintptr_t>(d->list) % 16 != 0 || d->list_stride % 16 != 0 ||
-      reinterpret_cast<uintptr_t>(d->base) % 16 != 0)
-    return Fail(HB_EINVAL, "GACC lists and base must be 16-byte aligned");
+      reinterpret_cast<uintptr_t>(d->base) % 16 != 0 || reinterpret_cast<uintptr_t>(d->out) % 16 != 0)
+    return Fail(HB_EINVAL, "GACC lists, base and out must be 16-byte aligned");
   if (d->quads > 1 && d->list_stride < 16 + 128ull * d->slots)
     return Fail(HB_EINVAL, "GACC list stride %llu is shorter than a list of %u slots",
                 (unsigned long long)d->list_stride, d->slots);

@@ -62,7 +62,8 @@ def build_image(rng, quads, slots, blocks, feature_rows, null_frac=0.15):
     return ddr, list_base, list_bytes, w_stride
 
 
-@pytest.mark.parametrize("quads,slots,blocks", [(1, 12, 3), (64, 20, 8), (7, 3, 1), (5, 100, 2)])
+@pytest.mark.parametrize("quads,slots,blocks", [(1, 12, 3), (64, 20, 8), (7, 3, 1), (5, 100, 2),
+                                                 (600, 9, 8), (512, 5, 3)])
 def test_gacc_matches_the_oracle(gpu, quads, slots, blocks):
     rng = np.random.default_rng(quads * 1000 + slots + blocks)
     ddr, list_base, list_bytes, w_stride = build_image(rng, quads, slots, blocks, 40)

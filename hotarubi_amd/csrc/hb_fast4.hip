@@ -25,9 +25,12 @@
 // One barrier per step; the LDS stage producers fill in iteration s (step
 // s + 2) was read into registers in iteration s - 1 (step 0: before the
 // loop, behind its own barrier), so two stages suffice.
-// Epilogue: the consumers park the tile in LDS (row-major, padded pitch),
-// then all 8 waves store whole rows with 16-byte stores; dword stores
-// straight from the MFMA layout drain several times slower.
+// Epilogue: each consumer wave passes its outputs, one 32 x 32 MFMA tile at
+// a time, through a 4 KB LDS block of its own and stores rows of 4 columns
+// per lane with 16-byte stores (dword stores straight from the MFMA layout
+// drain several times slower).  No barrier is involved: the producers go on
+// with the next tile's loads, and the tile's out-of-window flag reaches the
+// consumers through the ordinary per-step barriers.
 #include <utility>
 
 #include "hb_device.h"
@@ -47,8 +50,6 @@ constexpr int kBM = 128, kBN = 256;
 constexpr int kP = 256;    // producer threads
 constexpr int kU = 4;      // raw register sets per producer thread = loop unroll (even)
 constexpr uint32_t kSafeLo = 70, kSafeHi = 179;
-
-constexpr int kOutPitch = kBN + 8;  // floats: rows r and r + 4 fall on disjoint LDS banks
 
 // One K-step (two blocks) of operands.  Lane l of an m-tile holds row l % 32
 // and block l / 32; lane l of an n-tile holds column l % 32 and block l / 32.
@@ -155,12 +156,20 @@ __device__ __forceinline__ Schedule TilesOf(uint32_t total) {
 // zeros), and the producers' ring streams straight across tile boundaries:
 // global iteration u (tile u / iters) stages global step u + 2 and loads
 // ahead in bursts, so the next tile's first steps are in LDS when a tile
-// ends, and its epilogue (in LDS outside the stages) overlaps nothing but
-// its own stores.  Out-of-window scale bytes are flagged per tile (bit k % 2).
+// ends.  Both roles pass the same barriers: one per iteration and two
+// before the loop.
+//
+// Out-of-window scale bytes are flagged per tile in lds_unsafe[k % 2]: the
+// producers set it while staging tile k's last step (iteration
+// (k + 1) iters - 3, at least two barriers before the consumers read it
+// after iteration (k + 1) iters - 1), and consumer 0 clears the other slot
+// in tile k's epilogue (tile k - 1's flag, read in its epilogue before
+// barrier k iters; tile k + 1's flag is set no earlier than iteration
+// (k + 1) iters + 1).
 template <bool kMulti>
 __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) Stage lds_stage[2];
-  __shared__ __attribute__((aligned(16))) float lds_out[kBM / 2][kOutPitch];  // half a tile
+  __shared__ __attribute__((aligned(16))) float lds_xpose[4][32 * 32];  // one per consumer
   __shared__ uint32_t lds_unsafe[2];
 
   const Schedule sc = TilesOf(g.gx * g.gy * g.gz);
@@ -181,21 +190,6 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
     tl.z = t / (g.gx * g.gy);
     return tl;
   };
-  // Wave v of 8 stores rows v, v + 8, .. of half `half` of tile k: lane l
-  // the 4 columns 4l .. 4l + 3 (n is a multiple of 8: all in or all out).
-  auto store_half = [&](uint32_t k, uint32_t half, uint32_t v) {
-    const Tile tl = tile_of(k);
-    uint32_t* c = g.c + tl.z * g.c_batch;
-    const uint32_t l = threadIdx.x & 63, col = tl.col0 + 4 * l;
-    if (col >= g.n) return;
-    for (uint32_t r = v; r < kBM / 2; r += 8) {
-      const uint32_t row = tl.row0 + half * (kBM / 2) + r;
-      if (row >= g.m) break;
-      const float4 val = *reinterpret_cast<const float4*>(&lds_out[r][4 * l]);
-      *reinterpret_cast<float4*>(c + (size_t)row * g.n + col) = val;
-    }
-  };
-
   if (!consumer) {
     const uint32_t t = threadIdx.x, lane = t & 63, mt = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t h = lane >> 5;  // the A lane's block within the step
@@ -276,12 +270,15 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
       return bad;
     };
 
-    // Convert cursor: the tile (parity) of the step being staged, for the
-    // out-of-window flags (bit k % 2 of `flags`).
-    uint32_t ck = 0, cs = 0, flags = 0;
+    // Convert cursor: the tile of the step being staged, for its
+    // out-of-window flag, raised with the tile's last step.
+    uint32_t ck = 0, cs = 0;
+    bool bad = false;
     auto stage = [&](const Raw& rw, Stage& st) {
-      if (store(rw, st) && ck < sc.count) flags |= 1u << (ck & 1);
+      bad |= store(rw, st) && ck < sc.count;
       if (++cs == iters) {
+        if (bad) lds_unsafe[ck & 1] = 1;
+        bad = false;
         cs = 0;
         ++ck;
       }
@@ -299,24 +296,13 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
     }
     __syncthreads();  // global steps 0 and 1 staged
     __syncthreads();  // the consumers hold step 0: its stage may be refilled
-    for (uint32_t k = 0; k < sc.count; ++k) {
-      for (uint32_t s = 0; s < iters; s += kU) {
+    for (uint32_t u = 0; u < sc.count * iters; u += kU) {
 #pragma unroll
-        for (int i = 0; i < kU; ++i) {  // global iteration u stages step u + 2
-          stage(ring[(i + 2) % kU], lds_stage[i % 2]);
-          load(ring[(i + 2) % kU]);
-          __syncthreads();
-        }
+      for (int i = 0; i < kU; ++i) {  // global iteration u + i stages step u + i + 2
+        stage(ring[(i + 2) % kU], lds_stage[i % 2]);
+        load(ring[(i + 2) % kU]);
+        __syncthreads();
       }
-      // epilogue of tile k (all tile k steps are staged; its flag is final)
-      if (flags & (1u << (k & 1))) lds_unsafe[k & 1] = 1;
-      flags &= ~(1u << (k & 1));
-      __syncthreads();  // E0: flags in
-      __syncthreads();  // E1: rows 0-63 in LDS
-      store_half(k, 0, t >> 6);
-      __syncthreads();  // E2: half 0 read out
-      __syncthreads();  // E3: rows 64-127 in LDS
-      store_half(k, 1, t >> 6);
     }
     return;
   }
@@ -387,13 +373,14 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
   __syncthreads();  // global steps 0 and 1 staged; the flags are clear
   read(lds_stage[0], x);
   __syncthreads();  // step 0 is in registers before producers refill its stage
+  float* const xp = lds_xpose[cw];
   for (uint32_t k = 0; k < sc.count; ++k) {
     const Tile tl = tile_of(k);
     const uint8_t* a = g.a + tl.z * g.a_batch;
     const uint8_t* w0 = g.w[0] + tl.z * g.w_batch;
     uint32_t* c = g.c + tl.z * g.c_batch;
+    bool init_unsafe = false;  // this wave's outputs start from an exponent > 252
     if (g.acc) {  // uniform: start from C
-      bool unsafe = false;
 #pragma unroll
       for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -402,11 +389,10 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
           uint32_t init = 0;
           if (row < g.m && col < g.n) {
             init = c[(size_t)row * g.n + col];
-            unsafe |= ExpField(init) > 252u;
+            init_unsafe |= ExpField(init) > 252u;
           }
           acc[j][r] = __uint_as_float(init);
         }
-      if (unsafe) lds_unsafe[k & 1] = 1;  // read after E0 of this tile
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
@@ -418,38 +404,56 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
         iteration(y, x, 0);
       }
     }
-    __syncthreads();  // E0: the producers' flags for tile k are in
-    const bool slow = lds_unsafe[k & 1] != 0;
-    // Half `half` of the tile (rows 64 half ..) belongs to the waves with
-    // wm == half.  Adding +0 maps -0 to +0 (and a denormal sum, in the
-    // kernel's flush-to-zero mode, to +0).
-    auto park = [&](uint32_t half) {
-      if (wm != half) return;
-      if (slow) {  // a scale byte left the window: every output exactly
-        for (uint32_t j = 0; j < 8; ++j)
-          for (uint32_t r = 0; r < 16; ++r) {
-            const uint32_t row = tl.row0 + trow(j / 4, r), col = tl.col0 + tcol(j % 4);
-            if (row >= g.m || col >= g.n) continue;
-            const uint32_t init = g.acc ? c[(size_t)row * g.n + col] : 0u;
-            lds_out[trow(j / 4, r) - 64 * half][tcol(j % 4)] =
-                __uint_as_float(SlowLinear(g, a, w0, w0, init, row, col));
-          }
-        return;
+    // Epilogue, this wave's 64 x 128 outputs only.
+    const bool slow = __builtin_amdgcn_readfirstlane(
+        lds_unsafe[k & 1] != 0 || __builtin_amdgcn_ballot_w64(init_unsafe) != 0);
+    if (tid == 0) lds_unsafe[(k + 1) & 1] = 0;
+    if (slow) {  // a scale byte or an initial C left the window: every output exactly
+      for (uint32_t j = 0; j < 8; ++j)
+        for (uint32_t r = 0; r < 16; ++r) {
+          const uint32_t row = tl.row0 + trow(j / 4, r), col = tl.col0 + tcol(j % 4);
+          if (row >= g.m || col >= g.n) continue;
+          uint32_t* out = c + (size_t)row * g.n + col;
+          *out = SlowLinear(g, a, w0, w0, g.acc ? *out : 0u, row, col);
+        }
+      continue;
+    }
+    // Each MFMA tile goes through the wave's LDS block: output r of lane l
+    // (block row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32) is written at
+    // physical row p(row) = row ^ ((row >> 2) & 1), so the two half-waves of a
+    // write (rows row and row + 4) and the 16-lane groups of a read (two
+    // physical rows) use disjoint banks; read q gives lane l the 4 columns
+    // 4 (l % 8) .. of physical row l / 8 + 8 q.  LDS accesses of one wave
+    // execute in order, so a wave-scope fence orders the lanes' accesses.
+    // Adding +0 maps -0 to +0 (and a denormal sum, in the kernel's
+    // flush-to-zero mode, to +0).
+    Unroll<8>([&](auto jj) {
+      constexpr int kJ = decltype(jj)::value;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t row = 8 * (r / 4) + 4 * (lane >> 5) + (r & 3);
+        xp[(row ^ ((row >> 2) & 1)) * 32 + (lane & 31)] = acc[kJ][r] + 0.0f;
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          lds_out[trow(j / 4, r) - 64 * half][tcol(j % 4)] = acc[j][r] + 0.0f;
-    };
-    park(0);
-    __syncthreads();  // E1: rows 0-63 in LDS
-    if (tid == 0) lds_unsafe[k & 1] = 0;  // every consumer wave has read it
-    store_half(k, 0, 4 + cw);
-    __syncthreads();  // E2: half 0 read out
-    park(1);
-    __syncthreads();  // E3: rows 64-127 in LDS
-    store_half(k, 1, 4 + cw);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const float4* rd = reinterpret_cast<const float4*>(xp) + (lane >> 3) * 8 + (lane & 7);
+      const float4 v0 = rd[0], v1 = rd[64], v2 = rd[128], v3 = rd[192];  // q = 0 .. 3
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // n is a multiple of 8: the lane's 4 columns are all in or all out
+      const uint32_t col = tl.col0 + (4 * wn + kJ % 4) * 32 + 4 * (lane & 7);
+      const uint32_t prow = lane >> 3, row = tl.row0 + (2 * wm + kJ / 4) * 32 + (prow ^ ((prow >> 2) & 1));
+      float4* out = reinterpret_cast<float4*>(c + (size_t)row * g.n + col);
+      const size_t q_step = (size_t)2 * g.n;  // 8 rows, in float4 units
+      if (col < g.n) {
+        if (row < g.m) out[0] = v0;
+        if (row + 8 < g.m) out[q_step] = v1;
+        if (row + 16 < g.m) out[2 * q_step] = v2;
+        if (row + 24 < g.m) out[3 * q_step] = v3;
+      }
+    });
   }
 }
 

@@ -12,8 +12,9 @@ Extra fields (skipped with --quick): the same workload in exact mode (bitwise
 equal to the NPU), the M sweep {1, 16, 1024} in fast mode, the W8 layer
 M=64 K=960 N=2560 with per-channel scale (MULP) and bias (ADDP), the
 SigLIP-style W8 encoder set (M=2048), the SparseDrive-S stage-1 3x3 conv
-GEMM (MXFP4, M=67584 K=576 N=64), each in fast and exact mode, and the
-SmolVLA action-expert step (its GEMM chain) at batch 1 and 32.
+GEMM (MXFP4, M=67584 K=576 N=64), each in fast and exact mode, the
+SmolVLA action-expert step (its GEMM chain) and the SmolVLA LM prefix (its
+16 MXFP4 decoder layers' GEMMs) at batch 1 and 32.
 
     python bench.py [--steps K] [--warmup W] [--mode exact|fast] [--layers L]
                     [--quick] [--no-cpu] [--copy-probe MIB]
@@ -327,6 +328,40 @@ class ExpertStep(Chain):
                  ops=[(hb.EP_ADDP, self.vec(self.WIDTH, 0.1))])
         self.add(self.ACT, self.KB, hid, self.w8(self.ACT, self.KB), self.f32(self.ACT),
                  ops=[(hb.EP_ADDP, self.vec(self.ACT, 0.1))])
+        torch.cuda.synchronize()
+
+
+class PrefixStep(Chain):
+    """The SmolVLA language-model prefix as the GEMM chain the reference
+    compiler emits for it (tools/compiler/smolvla_lm.cpp:86-100, 118-255): 16
+    decoder layers of hidden 960 (K 960), 15 query / 5 KV heads of 64,
+    SiLU-gated MLP of 2560, every linear MXFP4, over the prefix's 141 tokens
+    per batch element (rows padded to whole quads).  Per layer: q, k, v
+    requantized to MXINT8 (RoPE is outside this path); o with the residual
+    add; up; gate with ACT_MUL(up) and requantize; down with the residual
+    add.  RMSNorm and attention are outside this chain: their outputs are
+    synthetic MXINT8 tensors of the right shape."""
+
+    HIDDEN, KB, KV, INTER, KBI, LAYERS, TOKENS = 960, 30, 320, 2560, 80, 16, 141
+
+    def __init__(self, hb, torch, batch, mode):
+        super().__init__(hb, torch, self.TOKENS * batch, mode, 23 + batch)
+        tb = self.table("silu")
+        x = [self.f32(self.HIDDEN) for _ in range(3)]
+        for _ in range(self.LAYERS):
+            a1, ao, a2 = self.a_words(self.KB), self.a_words(self.KB), self.a_words(self.KB)
+            for n in (self.HIDDEN, self.KV, self.KV):
+                self.add(n, self.KB, a1, [self.w_words(n, self.KB)], self.f32(n),
+                         q=self.a_words(n // 32))
+            self.add(self.HIDDEN, self.KB, ao, [self.w_words(self.HIDDEN, self.KB)], x[1],
+                     ops=[(hb.EP_ADD, x[0])])
+            up = self.f32(self.INTER)
+            self.add(self.INTER, self.KB, a2, [self.w_words(self.INTER, self.KB)], up)
+            h = self.a_words(self.KBI)
+            self.add(self.INTER, self.KB, a2, [self.w_words(self.INTER, self.KB)],
+                     self.f32(self.INTER), ops=[(hb.EP_ACT_MUL, up)], q=h, tbuf=tb)
+            self.add(self.HIDDEN, self.KBI, h, [self.w_words(self.HIDDEN, self.KBI)], x[2],
+                     ops=[(hb.EP_ADD, x[1])])
         torch.cuda.synchronize()
 
 
@@ -758,7 +793,7 @@ def main():
     ap.add_argument("--layers", type=int, default=256)
     ap.add_argument("--m", type=int, default=128)
     ap.add_argument("--quick", action="store_true", help="headline only, no extra fields")
-    ap.add_argument("--only", choices=["attention"], default=None,
+    ap.add_argument("--only", choices=["attention", "smolvla"], default=None,
                     help="headline plus this group of extra fields only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
@@ -869,10 +904,24 @@ def main():
             out[key] = rec
         ctx.set_stream(stream.cuda_stream)
 
+    if not args.quick and args.only in (None, "smolvla"):
         # SmolVLA action-expert step (GEMM chain), B = 1 and 32
         out["smolvla_expert_step_ms"] = {f"B={b}": time_expert_step(hb, torch, ctx, b, mode)
                                          for b in (1, 32)}
         ctx.set_stream(stream.cuda_stream)
+        # SmolVLA LM prefix (16 MXFP4 decoder layers' GEMMs over 141 tokens per element)
+        prefix = {"workload": "SmolVLA LM prefix GEMM chain: 16 layers x {q 960, k 320, v 320 "
+                              "(requantize), o 960 (+residual), up 2560, gate 2560 (ACT_MUL, "
+                              "requantize), down 960 (+residual)}, MXFP4, 141 tokens per element"}
+        for b in (1, 32):
+            wk = PrefixStep(hb, torch, b, mode)
+            t = time_chain(torch, ctx, wk, steps=5)
+            best = min(t["eager_ms"], t.get("graph_ms", t["eager_ms"]))
+            tops, roof = chain_summary(wk, best, "fp6_fp4")
+            prefix[f"B={b}"] = {**t, "tops": tops, "roofline": roof}
+            del wk
+        ctx.set_stream(stream.cuda_stream)
+        out["smolvla_prefix_ms"] = prefix
 
     if not args.quick and args.only in (None, "attention"):
         # attention operands built on device (SPLIT8 / T32_SPLIT8), the row

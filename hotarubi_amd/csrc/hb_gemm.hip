@@ -671,9 +671,12 @@ void ExactGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy) {
 
 namespace {
 // A single layer with fewer tiles than this spreads its work: K splits in
-// fast mode (to about kTargetWorkgroups workgroups, at least two K-steps
-// each) and the element-parallel deferred epilogue.
-constexpr uint32_t kSmallGrid = 128, kTargetWorkgroups = 256;
+// fast mode (to about kTargetWorkgroups workgroups, at least kMinSplitSteps
+// K-steps each) and the element-parallel deferred epilogue.  Measured on the
+// SmolVLA chains (M = 141 and 1,600): 128 workgroups of at least 4 steps beat
+// 256 of 2 by 9-13% (the split sums written and read again cost more than the
+// parallelism gains); 32 workgroups, or no split, lost 50-70% at M = 141.
+constexpr uint32_t kSmallGrid = 128, kTargetWorkgroups = 128, kMinSplitSteps = 4;
 }  // namespace
 
 hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace& ws,
@@ -703,9 +706,9 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
     uint32_t nblocks = 0;
     for (uint32_t p = 0; p < args.n_pieces; ++p) nblocks += args.piece_kb[p];
     const uint32_t steps = (nblocks + 1) / 2;
-    const uint32_t want = kTargetWorkgroups / (gx * gy);
+    const uint32_t want = kTargetWorkgroups > gx * gy ? kTargetWorkgroups / (gx * gy) : 1u;
     uint32_t per = (steps + want - 1) / want;
-    per = per < 2 ? 2 : per;
+    per = per < kMinSplitSteps ? kMinSplitSteps : per;
     args.splits = (steps + per - 1) / per;
     args.split_steps = per;
   }

@@ -93,3 +93,25 @@ def test_batched_pieces_onto_ops_requantize(gpu, slow):
         want, wq = oracle_linear(m, n, kb, d[1], d[2], d[3], ops, pieces=pieces, onto=onto[i],
                                  quantize=True)
         check_fast(got[i], want, gq[i], wq)
+
+
+def test_unaligned_output_of_a_streaming_layer(gpu):
+    """C 4 bytes past a 16-byte boundary: a batched MXFP4 layer of 128 rows
+    that would take the streaming kernel (16-byte stores) is still correct."""
+    rng = np.random.default_rng(320)
+    layers, m, n, k = 2, 128, 256, 320
+    data = [make_layer(rng, m, n, k, False) for _ in range(layers)]
+    kb, modes = data[0][0], data[0][3]
+    a_all = dev(np.stack([d[1] for d in data]))
+    w_all = dev(np.stack([d[2][0] for d in data]))
+    flat = torch.zeros((layers * m * n + 1,), dtype=torch.float32, device=DEV)
+    c_all = flat[1:].view(layers, m, n)
+    descs = [hb.linear_desc(m, n, kb, a_all[i], [w_all[i]], modes, c_all[i], mode=hb.FAST)
+             for i in range(layers)]
+    torch.cuda.synchronize()
+    say("unaligned C", dict(layers=layers, m=m, n=n))
+    hb.linear_batched(descs, gpu)
+    got = host(c_all).view(np.uint32)
+    for i, d in enumerate(data):
+        want, _ = oracle_linear(m, n, kb, d[1], d[2], d[3])
+        check_fast(got[i], want)

@@ -13,6 +13,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -33,9 +34,29 @@ DEVICE_FLAGS = [
 
 
 def build(asm: bool = False, verbose: bool = False) -> str:
+    """Compile each source to an object (in parallel), then link the library."""
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    cmd = [HIPCC, *DEVICE_FLAGS, "-fPIC", "-shared", "-I", os.path.join(ROOT, "include"),
-           "-o", LIB + ".tmp", *srcs]
+    objdir = os.path.join(ROOT, "_build", "obj")
+    os.makedirs(objdir, exist_ok=True)
+    objs = [os.path.join(objdir, os.path.splitext(os.path.basename(s))[0] + ".o") for s in srcs]
+
+    def compile_one(src_obj):
+        src, obj = src_obj
+        cmd = [HIPCC, *DEVICE_FLAGS, "-fPIC", "-c", "-I", os.path.join(ROOT, "include"),
+               "-o", obj, src]
+        if verbose:
+            print(" ".join(cmd))
+        return subprocess.run(cmd, capture_output=True, text=True)
+
+    jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(jobs) as pool:
+        results = list(pool.map(compile_one, zip(srcs, objs)))
+    for src, r in zip(srcs, results):
+        if r.stderr and (verbose or r.returncode != 0):
+            sys.stderr.write(r.stderr)
+        if r.returncode != 0:
+            raise subprocess.CalledProcessError(r.returncode, f"hipcc {os.path.basename(src)}")
+    cmd = [HIPCC, "--offload-arch=gfx950", "-fPIC", "-shared", "-o", LIB + ".tmp", *objs]
     if verbose:
         print(" ".join(cmd))
     subprocess.run(cmd, check=True)

@@ -93,6 +93,11 @@ int CheckGemm(const hb_gemm_cmd* c) {
   if (!(c->kb >= 1 && c->kb <= c->a_stride))
     return Fail(HB_EBADCMD, "GEMM kb = %u is not in [1, a_stride = %u]", c->kb, c->a_stride);
   if (c->n8 < 1) return Fail(HB_EBADCMD, "GEMM n8 = 0");
+  // The instruction's n8 field is 8 bits wide (isa.hpp:83), so a decoded
+  // command never exceeds 255.  The aliasing kernel relies on it: with m <= 992
+  // an FBUF word then has at most ceil(248 * 255 / 4096) = 16 writers.
+  if (c->n8 > 255)
+    return Fail(HB_EINVAL, "GEMM n8 = %u does not fit the instruction's 8-bit field", c->n8);
   return HB_OK;
 }
 
@@ -634,7 +639,7 @@ int hb_ctx_destroy(hb_ctx* ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->d_flag) (void)hipFree(ctx->d_flag);
-  if (ctx->ws.ptr) (void)hipFree(ctx->ws.ptr);
+  hb::FreeWorkspace(ctx->ws);
   if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return HB_OK;

@@ -249,20 +249,30 @@ __device__ __forceinline__ uint32_t ScaleCoefficientBits(uint32_t c, uint32_t sc
   return sign | ((uint32_t)exponent << 23) | (c & 0x7FFFFFu);
 }
 
+constexpr uint32_t kUnitMask = 0x0FFFFFFFu;
+
 template <uint32_t kCh>
 __global__ __launch_bounds__(64) void GaccKernel(GaccArgs a) {
   const uint32_t channels = a.blocks * 32, waves = (channels / kCh + 63) / 64;
   const uint32_t quad = blockIdx.x / (4 * waves), t = (blockIdx.x / waves) % 4;
-  const uint32_t lane = (blockIdx.x % waves) * 64 + threadIdx.x;  // channel group
-  if (kCh * lane >= channels) return;
+  // Every lane of the wave stays to the end: the entry staging below is a
+  // wave-wide LDS exchange (lane i writes slot i), so a lane past the last
+  // channel keeps staging but gathers, computes and stores nothing (it
+  // addresses channel 0's row bytes and w column instead of its own).
+  const uint32_t lane_c = (blockIdx.x % waves) * 64 + threadIdx.x;  // channel group
+  const bool live_lane = kCh * lane_c < channels;
+  const uint32_t lane = live_lane ? lane_c : 0u;
   const uint32_t b = kCh * lane / 32;
   const uint8_t* list = a.list + (uint64_t)quad * a.list_stride;
-  const uint64_t w_area = (uint64_t)(*reinterpret_cast<const uint32_t*>(list)) * 16u;
+  // unit addresses keep their low 28 bits (UnitAddress, dma_engine.cpp:60, 546-548)
+  const uint64_t w_area =
+      (uint64_t)(*reinterpret_cast<const uint32_t*>(list) & kUnitMask) * 16u;
   const uint8_t* wcol = a.base + w_area + (uint64_t)b * a.w_stride * 16u + 4u * (t * 8);
   float* out = a.out + ((uint64_t)quad * 4 + t) * channels + kCh * lane;
   uint32_t acc[kCh];
 #pragma unroll
-  for (uint32_t v = 0; v < kCh; ++v) acc[v] = a.accumulate ? __float_as_uint(out[v]) : 0u;
+  for (uint32_t v = 0; v < kCh; ++v)
+    acc[v] = a.accumulate && live_lane ? __float_as_uint(out[v]) : 0u;
   const uint64_t* entries = reinterpret_cast<const uint64_t*>(list + 16) + t * 4;
   __shared__ uint64_t staged[64][4];
   constexpr uint32_t kSlots = 4;
@@ -289,7 +299,8 @@ __global__ __launch_bounds__(64) void GaccKernel(GaccArgs a) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const bool live = (uint32_t)e[i][k] != 0xFFFFFFFFu;
-        const uint8_t* row = a.base + (uint64_t)(live ? (uint32_t)e[i][k] : 0u) * 16u;
+        const uint8_t* row =
+            a.base + (uint64_t)(live ? (uint32_t)e[i][k] & kUnitMask : 0u) * 16u;
         if constexpr (kCh == 4)
           q[i][k] = live ? *reinterpret_cast<const uint32_t*>(row + 4 * lane) : 0u;
         else
@@ -312,6 +323,7 @@ __global__ __launch_bounds__(64) void GaccKernel(GaccArgs a) {
       }
     }
   }
+  if (!live_lane) return;
 #pragma unroll
   for (uint32_t v = 0; v < kCh; ++v) out[v] = __uint_as_float(acc[v]);
 }

@@ -679,6 +679,28 @@ namespace {
 constexpr uint32_t kSmallGrid = 128, kTargetWorkgroups = 128, kMinSplitSteps = 4;
 }  // namespace
 
+hipError_t GrowWorkspace(Workspace& ws, size_t bytes) {
+  if (ws.bytes >= bytes) return hipSuccess;
+  // at least double, so a run of growing shapes retires few buffers
+  size_t want = ws.bytes * 2 > bytes ? ws.bytes * 2 : bytes;
+  want = (want + 0xFFFFF) & ~(size_t)0xFFFFF;
+  if (ws.ptr != nullptr && ws.n_retired == sizeof ws.retired / sizeof ws.retired[0])
+    return hipErrorOutOfMemory;  // (64 doublings: unreachable in practice)
+  float* p = nullptr;
+  const hipError_t err = hipMalloc(&p, want);
+  if (err != hipSuccess) return err;
+  if (ws.ptr != nullptr) ws.retired[ws.n_retired++] = ws.ptr;
+  ws.ptr = p;
+  ws.bytes = want;
+  return hipSuccess;
+}
+
+void FreeWorkspace(Workspace& ws) {
+  if (ws.ptr != nullptr) (void)hipFree(ws.ptr);
+  for (uint32_t i = 0; i < ws.n_retired; ++i) (void)hipFree(ws.retired[i]);
+  ws = Workspace{};
+}
+
 hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace& ws,
                         hipStream_t stream) {
   GemmArgs args = in;
@@ -717,17 +739,8 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   const bool defer = small && (args.splits > 1 || (!fastk && (args.n_ops > 0 || args.q_out != nullptr)));
   if (!defer) return fastk ? LaunchLinearFast(args, batch, stream) : LaunchTiles<true>(args, batch, stream);
 
-  const size_t bytes = WorkspaceBytes(args);
-  if (ws.bytes < bytes) {
-    hipError_t err = hipStreamSynchronize(stream);  // the old buffer may be in use
-    if (err != hipSuccess) return err;
-    if (ws.ptr != nullptr) (void)hipFree(ws.ptr);
-    ws.ptr = nullptr;
-    ws.bytes = 0;
-    err = hipMalloc(&ws.ptr, bytes);
-    if (err != hipSuccess) return err;
-    ws.bytes = bytes;
-  }
+  const hipError_t grown = GrowWorkspace(ws, WorkspaceBytes(args));
+  if (grown != hipSuccess) return grown;
   args.ws = ws.ptr;
   const hipError_t err = fastk ? LaunchLinearFast(args, args.splits, stream)  // z = split
                              : LaunchTiles<true>(args, 1, stream);

@@ -79,11 +79,20 @@ __device__ __forceinline__ uint32_t* SplitFlags(const GemmArgs& g) {
   return reinterpret_cast<uint32_t*>(g.ws + (size_t)g.splits * g.quads * 4 * g.n);
 }
 
-// Device scratch owned by a context, grown on demand.
+// Device scratch owned by a context, grown on demand.  A buffer, once
+// handed to a kernel, is never freed before the context is destroyed: work
+// still queued, and HIP graphs captured earlier, keep the address they were
+// given.  Growing allocates a larger buffer and retires the old one.
 struct Workspace {
   float* ptr = nullptr;
   size_t bytes = 0;
+  float* retired[64] = {};  // superseded buffers, freed with the context
+  uint32_t n_retired = 0;
 };
+// Make ws at least `bytes` long (hipMalloc; no stream synchronization).
+hipError_t GrowWorkspace(Workspace& ws, size_t bytes);
+// Free the current and every retired buffer.
+void FreeWorkspace(Workspace& ws);
 
 // Workgroup -> tile mapping.  The hardware deals workgroups round-robin over
 // the 8 XCDs, each with its own L2; remapping puts consecutive logical tiles
@@ -110,7 +119,7 @@ hipError_t LaunchGemmInstr(const GemmArgs& args, hipStream_t stream);
 hipError_t LaunchGemmInstrAliased(const GemmArgs& args, hipStream_t stream);
 // Linear layer: picks the kernel, and for a single small layer (few tiles)
 // K splits (fast mode) and/or the deferred element-parallel epilogue, in
-// which case it may grow `ws` (synchronizing the stream first).
+// which case it may grow `ws` (GrowWorkspace).
 hipError_t LaunchLinear(const GemmArgs& args, uint32_t batch, bool fast, Workspace& ws,
                         hipStream_t stream);
 // Fast path (hb_fast.hip): block-scaled f8f6f4 MFMA for one FP4 plane or

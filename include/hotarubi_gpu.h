@@ -141,7 +141,9 @@ int hb_onchip_device_ptr(hb_onchip* onchip, int mem, void** device);
 int hb_gemm_decode(const uint8_t word[16], hb_gemm_cmd* out);
 /* Encode as EncodeGemm (tools/compiler/isa.cpp:89-103), wait bits 0. */
 int hb_gemm_encode(const hb_gemm_cmd* cmd, uint8_t word[16]);
-/* The preconditions of ExecuteGemm (gemm_array.cpp:113-119). */
+/* The preconditions of ExecuteGemm (gemm_array.cpp:113-119), HB_EBADCMD with
+ * the reference's texts; and n8 <= 255, the width of the instruction's n8
+ * field (isa.hpp:83), HB_EINVAL otherwise. */
 int hb_gemm_check(const hb_gemm_cmd* cmd);
 /* Words the instruction reads and writes, one byte per word (1 = touched):
  * reads_abuf[8192], reads_wbuf[2048], reads_fbuf[4096], writes_fbuf[4096];
@@ -244,8 +246,13 @@ typedef struct hb_linear_desc {
 } hb_linear_desc;
 
 /* A single small layer (fewer than 128 output tiles) may grow the context's
- * workspace on its first call of a larger shape (hipMalloc after a stream
- * synchronize); warm a shape up before capturing it in a graph. */
+ * workspace on its first call of a larger shape (a hipMalloc, with no stream
+ * synchronization).  A workspace buffer is never freed before
+ * hb_ctx_destroy, so work already queued and HIP graphs captured earlier
+ * stay valid when a later call grows it; a graph is valid until its context
+ * is destroyed.  Warm a shape up before capturing it in a graph (the
+ * allocation itself is not capturable), and do not replay two graphs that
+ * use one context's workspace concurrently. */
 int hb_linear(hb_ctx* ctx, const hb_linear_desc* desc);
 int hb_linear_async(hb_ctx* ctx, const hb_linear_desc* desc);
 /* `count` independent layers in one launch (e.g. the same projection of

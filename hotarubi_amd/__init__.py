@@ -35,10 +35,11 @@ ABUF, WBUF, FBUF, PBUF, TBUF = range(5)
 DEPTH = {ABUF: 8192, WBUF: 2048, FBUF: 4096, PBUF: 512, TBUF: 1024}
 WORD_BYTES = {ABUF: 132, WBUF: 144, FBUF: 128, PBUF: 128, TBUF: 8}
 EXACT, FAST = 0, 1
+PANELS = 2  # hb_linear_desc.flags bit: the W planes are weight panels
 EP_ADDP, EP_MULP, EP_SCALE, EP_COPY, EP_RELU, EP_ACT, EP_ACT_MUL = 3, 4, 5, 6, 7, 8, 9
 EP_ADD = 0x100
 MAX_PIECES, MAX_OPS = 16, 8
-ABI_VERSION = 2  # HB_ABI_VERSION of the structs mirrored below
+ABI_VERSION = 3  # HB_ABI_VERSION of the structs mirrored below
 
 #: every symbol include/hotarubi_gpu.h declares
 EXPORTS = (
@@ -50,7 +51,7 @@ EXPORTS = (
     "hb_linear_batched_async", "hb_encode_mxint8", "hb_split8", "hb_split8_async",
     "hb_t32_split8", "hb_t32_split8_async", "hb_rows", "hb_rows_async",
     "hb_row_load", "hb_row_load_async", "hb_row_store", "hb_row_store_async",
-    "hb_gacc", "hb_gacc_async",
+    "hb_gacc", "hb_gacc_async", "hb_panel_bytes", "hb_pack_weights", "hb_unpack_weights",
 )
 
 
@@ -193,6 +194,9 @@ def lib():
             "hb_split8_async": (i, [vp, vp, C.c_uint64, u32, u32, vp, vp]),
             "hb_t32_split8": (i, [vp, vp, C.c_uint64, u32, u32, vp, vp]),
             "hb_t32_split8_async": (i, [vp, vp, C.c_uint64, u32, u32, vp, vp]),
+            "hb_panel_bytes": (C.c_uint64, [u32, u32]),
+            "hb_pack_weights": (i, [vp, vp, u32, u32, vp]),
+            "hb_unpack_weights": (i, [vp, vp, u32, u32, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -359,7 +363,7 @@ def _ptr(t) -> int | None:
 
 
 def linear_desc(m, n, kb_total, a, planes, modes, c, pieces=None, onto=False, ops=(),
-                tbuf=None, q_out=None, mode=EXACT, a_stride=0) -> _LinearDesc:
+                tbuf=None, q_out=None, mode=EXACT, a_stride=0, panels=False) -> _LinearDesc:
     """Build an hb_linear_desc from device buffers (torch tensors or addresses).
 
     planes/modes: [w] with [0] (FP4) or [w_hi, w_lo] with [1, 2] (W8).
@@ -399,7 +403,7 @@ def linear_desc(m, n, kb_total, a, planes, modes, c, pieces=None, onto=False, op
             d.ops[i].x2 = _ptr(arg)
     d.tbuf = _ptr(tbuf)
     d.q_out = _ptr(q_out)
-    d.flags = mode
+    d.flags = mode | (PANELS if panels else 0)
     return d
 
 
@@ -471,6 +475,23 @@ def rows(entry: int, x, rows: int, cols: int, aux: int, imm: int = 0, gamma=None
                   _ptr(y), _ptr(q_out))
     fn = lib().hb_rows if sync else lib().hb_rows_async
     _check(fn(ctx.handle, C.byref(d)))
+
+
+def panel_bytes(n: int, kb_total: int) -> int:
+    """Bytes of one weight plane in the panel layout (hb_panel_bytes)."""
+    return int(lib().hb_panel_bytes(n, kb_total))
+
+
+def pack_weights(w, n: int, kb_total: int, panels, ctx: Context | None = None) -> None:
+    """hb_pack_weights: DDR words [n/8][kb_total] x 144 B -> weight panels."""
+    ctx = ctx or default_context()
+    _check(lib().hb_pack_weights(ctx.handle, _ptr(w), n, kb_total, _ptr(panels)))
+
+
+def unpack_weights(panels, n: int, kb_total: int, w, ctx: Context | None = None) -> None:
+    """hb_unpack_weights: weight panels -> DDR words, bit for bit."""
+    ctx = ctx or default_context()
+    _check(lib().hb_unpack_weights(ctx.handle, _ptr(panels), n, kb_total, _ptr(w)))
 
 
 def split8(src, rows: int, row_words: int, hi, lo, src_stride: int | None = None,

@@ -468,12 +468,19 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g, bool* mixed) {
     a_end = std::max(a_end, (quads - 1) * a_row + std::max<uint64_t>(pc.kb_offset, pc.a_word) + pc.kb);
     if (PieceShift(*d, p) != PieceShift(*d, 0)) *mixed = true;
   }
-  if (a_end * hb::kDdrWord > (1ull << 32) || (uint64_t)(d->n / 8) * d->kb_total * hb::kDdrWord > (1ull << 32))
+  const bool panels = (d->flags & HB_LINEAR_PANELS) != 0;
+  const uint64_t w_bytes =
+      panels ? hb::PanelBytes(d->n, d->kb_total) : (uint64_t)(d->n / 8) * d->kb_total * hb::kDdrWord;
+  if (a_end * hb::kDdrWord > (1ull << 32) || w_bytes > (1ull << 32))
     return Fail(HB_EINVAL, "A or W spans more than 4 GiB");
   if (!d->a || !d->c) return Fail(HB_EINVAL, "null A or C");
   if (d->n_ops > HB_MAX_EP_OPS) return Fail(HB_EINVAL, "n_ops = %u", d->n_ops);
   if (d->q_out && d->n % 32 != 0) return Fail(HB_EINVAL, "quantized output needs n %% 32 == 0");
-  if (d->flags > HB_LINEAR_FAST) return Fail(HB_EINVAL, "flags = %u", d->flags);
+  if (d->flags & ~(uint32_t)(HB_LINEAR_FAST | HB_LINEAR_PANELS))
+    return Fail(HB_EINVAL, "flags = %u", d->flags);
+  for (uint32_t l = 0; panels && l < d->n_planes; ++l)
+    if (reinterpret_cast<uintptr_t>(d->w[l]) % 16 != 0)
+      return Fail(HB_EINVAL, "weight panels must be 16-byte aligned");
   std::memset(g, 0, sizeof *g);
   for (uint32_t o = 0; o < d->n_ops; ++o) {
     const hb_ep_op& op = d->ops[o];
@@ -520,6 +527,8 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g, bool* mixed) {
   g->modes[0] = d->modes[0];
   g->modes[1] = d->n_planes > 1 ? d->modes[1] : d->modes[0];
   g->total_steps = (uint32_t)steps;
+  g->w_panels = panels ? 1u : 0u;
+  g->w_steps = (d->kb_total + 1) / 2;
   g->acc = d->onto ? 1u : 0u;
   g->tbuf = d->tbuf;
   g->q_out = static_cast<uint8_t*>(d->q_out);
@@ -574,7 +583,8 @@ int LinearBatched(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
     }
   }
   if (mixed) return LinearChain(ctx, d, count);
-  hipError_t err = hb::LaunchLinear(g, count, d[0].flags == HB_LINEAR_FAST, ctx->ws, ctx->stream);
+  hipError_t err = hb::LaunchLinear(g, count, (d[0].flags & HB_LINEAR_FAST) != 0, ctx->ws,
+                                    ctx->stream);
   if (err != hipSuccess) return HipFail(err, "linear launch");
   return HB_OK;
 }
@@ -834,6 +844,39 @@ int hb_linear(hb_ctx* ctx, const hb_linear_desc* d) {
 int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
   if (int rc = Enter(ctx)) return rc;
   return LinearBatched(ctx, d, count);
+}
+
+uint64_t hb_panel_bytes(uint32_t n, uint32_t kb_total) {
+  if (n < 8 || n % 8 != 0 || kb_total < 1) return 0;
+  return hb::PanelBytes(n, kb_total);
+}
+
+namespace {
+int PanelConvert(hb_ctx* ctx, const void* src, uint32_t n, uint32_t kb_total, void* dst,
+                 bool pack) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!src || !dst) return Fail(HB_EINVAL, "null weights");
+  if (n < 8 || n % 8 != 0 || kb_total < 1)
+    return Fail(HB_EINVAL, "weights n = %u, kb_total = %u: need n %% 8 == 0, kb_total >= 1", n,
+                kb_total);
+  if (reinterpret_cast<uintptr_t>(src) % 16 != 0 || reinterpret_cast<uintptr_t>(dst) % 16 != 0)
+    return Fail(HB_EINVAL, "weights must be 16-byte aligned");
+  const uint8_t* s = static_cast<const uint8_t*>(src);
+  uint8_t* d = static_cast<uint8_t*>(dst);
+  const hipError_t err = pack ? hb::LaunchPackPanels(s, n, kb_total, d, ctx->stream)
+                              : hb::LaunchUnpackPanels(s, n, kb_total, d, ctx->stream);
+  if (err != hipSuccess) return HipFail(err, pack ? "pack launch" : "unpack launch");
+  HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+}  // namespace
+
+int hb_pack_weights(hb_ctx* ctx, const void* w, uint32_t n, uint32_t kb_total, void* panels) {
+  return PanelConvert(ctx, w, n, kb_total, panels, true);
+}
+
+int hb_unpack_weights(hb_ctx* ctx, const void* panels, uint32_t n, uint32_t kb_total, void* w) {
+  return PanelConvert(ctx, panels, n, kb_total, w, false);
 }
 
 int hb_encode_mxint8(hb_ctx* ctx, const float* x, uint32_t rows, uint32_t cols, void* out) {

@@ -199,19 +199,22 @@ __device__ __forceinline__ uint32_t ScaleByteOf(uint32_t emax) { return emax == 
 __device__ __forceinline__ uint32_t SlowLinear(const GemmArgs& g, const uint8_t* a,
                                                const uint8_t* w0, const uint8_t* w1, uint32_t acc,
                                                uint32_t row, uint32_t col) {
-  const uint32_t quad = row >> 2, t = row & 3, grp = col >> 3, cl = col & 7;
+  const uint32_t quad = row >> 2, t = row & 3;
+  const WLaneOff wo = WLane(g, col);
   for (uint32_t p = 0; p < g.n_pieces; ++p)
     for (uint32_t l = 0; l < g.n_planes; ++l)
       for (uint32_t b = 0; b < g.piece_kb[p]; ++b) {
         const uint32_t blk = g.piece_off[p] + b, mode = g.modes[l];
         const uint8_t* aw = a + ((size_t)quad * g.a_row + blk) * kDdrWord;
-        const uint8_t* ww = (l ? w1 : w0) + ((size_t)grp * g.kb_total + blk) * kDdrWord;
+        const uint8_t* wp = l ? w1 : w0;
+        const uint8_t* codes = wp + wo.codes + WBlockCodes(g, blk);
+        const uint32_t wscale = wp[wo.scale + WBlockScale(g, blk) + wo.shift / 8];
         int32_t sum = 0;
         for (uint32_t k = 0; k < 32; ++k) {
-          const uint32_t byte = ww[cl * 16 + (k >> 1)];
+          const uint32_t byte = codes[k >> 1];
           sum += (int32_t)(int8_t)aw[t * 32 + k] * WeightValue((k & 1) ? (byte >> 4) : byte, mode);
         }
-        acc = AddBits(acc, BlockValue(sum, aw[128 + t], ww[128 + cl], mode));
+        acc = AddBits(acc, BlockValue(sum, aw[128 + t], wscale, mode));
       }
   return acc;
 }

@@ -172,9 +172,11 @@ __device__ __forceinline__ Offsets<kWLoads> ThreadOffsets(const GemmArgs& g, uin
   for (int k = 0; k < kWLoads; ++k) {
     const uint32_t col = (t + kP * k) % 256;
     const uint32_t grp = min(g0 + (col >> 3), g.groups - 1), cl = col & 7;
-    o.w[k] = grp * word_row + cl * 16;
-    o.w_scale[k] = grp * word_row + 128 + (cl & 4);
+    const WLaneOff wo = WLane(g, grp * 8 + cl);  // DDR words or panels
+    o.w[k] = wo.codes;
+    o.w_scale[k] = wo.scale;
   }
+  (void)word_row;
   return o;
 }
 
@@ -188,8 +190,9 @@ __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, con
                                         uint32_t nblocks, Raw<kWLoads>& rw) {
   const uint32_t h = (t & 63) >> 5;
   const uint32_t step = s0 + min(live_step, steps - 1);  // steps of this split start at s0
-  const uint32_t ub0 = BlockOf<kMulti>(g, 2 * step) * kDdrWord;
-  const uint32_t ub1 = BlockOf<kMulti>(g, min(2 * step + 1, nblocks - 1)) * kDdrWord;
+  const uint32_t blk0 = BlockOf<kMulti>(g, 2 * step);
+  const uint32_t blk1 = BlockOf<kMulti>(g, min(2 * step + 1, nblocks - 1));
+  const uint32_t ub0 = blk0 * kDdrWord, ub1 = blk1 * kDdrWord;
   if constexpr (kAWave) {
     // the lane's block: a step's two blocks need not be in memory order (a
     // piece list), so each lane addresses its own from the layer base
@@ -210,11 +213,12 @@ __device__ __forceinline__ void LoadRaw(const GemmArgs& g, const uint8_t* a, con
   for (int k = 0; k < kWLoads; ++k) {
     const uint32_t u = t + kP * k;
     const int plane = (kP * k) / 512;  // constant after unrolling
-    const uint8_t* wb = (plane ? w1 : w0) + ((u >> 8) & 1 ? ub1 : ub0);  // wave-uniform
-    const u32x4 v = *reinterpret_cast<const u32x4*>(wb + o.w[k]);
+    const uint8_t* wp = plane ? w1 : w0;
+    const uint32_t blk = (u >> 8) & 1 ? blk1 : blk0;  // wave-uniform
+    const u32x4 v = *reinterpret_cast<const u32x4*>(wp + WBlockCodes(g, blk) + o.w[k]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) rw.w[k][i] = v[i];
-    rw.sw[k] = *reinterpret_cast<const uint32_t*>(wb + o.w_scale[k]);
+    rw.sw[k] = *reinterpret_cast<const uint32_t*>(wp + WBlockScale(g, blk) + o.w_scale[k]);
   }
 }
 
@@ -287,7 +291,7 @@ __device__ __forceinline__ u32x6 PlaneW8(const uint32_t* x, bool lo) {
 
 template <int kMT, int kP, int kWLoads, bool kW8, bool kAWave>
 __device__ __forceinline__ bool StoreRaw(const Raw<kWLoads>& rw, Lds<kMT, kW8>& l, int st,
-                                         uint32_t t) {
+                                         uint32_t t, const GemmArgs& g, uint32_t g0) {
   const uint32_t lane = t & 63;
   constexpr int kTM = Fmt<kW8>::kTM, kTN = Fmt<kW8>::kTN, kWP = Fmt<kW8>::kWPlanes;
   bool bad = false;
@@ -306,7 +310,9 @@ __device__ __forceinline__ bool StoreRaw(const Raw<kWLoads>& rw, Lds<kMT, kW8>& 
     const uint32_t u = t + kP * k, col = u % 256, half = (u >> 8) & 1;
     const int plane = (kP * k) / 512;  // constant after unrolling
     const uint32_t nt = col >> 5, slot = (col & 31) + 32 * half;
-    const uint32_t ew = __builtin_amdgcn_ubfe(rw.sw[k], 8 * (col & 3), 8);  // column cl % 4
+    // the scale byte's place in its dword, for the column ThreadOffsets loaded
+    const uint32_t shift = WLane(g, min(g0 + (col >> 3), g.groups - 1) * 8 + (col & 7)).shift;
+    const uint32_t ew = __builtin_amdgcn_ubfe(rw.sw[k], shift, 8);
     if constexpr (kW8) {
       const u32x6 wc = PlaneW8(rw.w[k], plane != 0);
 #pragma unroll
@@ -503,7 +509,7 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
     for (int i = 0; i < kU; ++i) load(ring[i], i);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      unsafe |= StoreRaw<kMT, kP, kWLoads, kW8, kAWave>(ring[i], lds, i, t);
+      unsafe |= StoreRaw<kMT, kP, kWLoads, kW8, kAWave>(ring[i], lds, i, t, g, g0);
       load(ring[i], i + kU);
     }
 #pragma unroll
@@ -516,7 +522,8 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < kU; ++i) {  // iteration step + i converts step + i + 2
         if (step + i >= steps) break;  // uniform; the consumers stop at the same step
-        unsafe |= StoreRaw<kMT, kP, kWLoads, kW8, kAWave>(ring[(i + 2) % kU], lds, (i + 2) % kU, t);
+        unsafe |= StoreRaw<kMT, kP, kWLoads, kW8, kAWave>(ring[(i + 2) % kU], lds, (i + 2) % kU, t, g,
+                                                          g0);
         load(ring[(i + 2) % kU], step + i + 2 + kU);
         __syncthreads();
       }

@@ -462,7 +462,8 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
 bool Fp4Eligible(const GemmArgs& args, uint32_t tile_rows) {
   // C is stored 16 bytes at a time
   const bool aligned = reinterpret_cast<uintptr_t>(args.c) % 16 == 0 && args.c_batch % 4 == 0;
-  return args.n_planes == 1 && args.modes[0] == kModeFp4 && tile_rows == kBM && aligned &&
+  return !args.w_panels && args.n_planes == 1 && args.modes[0] == kModeFp4 && tile_rows == kBM &&
+         aligned &&
          args.n_ops == 0 && args.q_out == nullptr && args.ws == nullptr && args.splits <= 1;
 }
 

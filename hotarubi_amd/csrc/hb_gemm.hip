@@ -162,8 +162,12 @@ __device__ __forceinline__ Offsets ThreadOffsets(const GemmArgs& g, const Lane<T
   const uint32_t wstride = kLinear ? g.kb_total * kDdrWord : 0u;
   o.a = quad * astride + t * 32 + ln.aofs;
   o.a_scale = quad * astride + 128 + t;
-  o.w = grp * wstride + cl * 16 + ln.wofs;
-  o.w_scale = grp * wstride + 128 + cl;
+  if (kLinear) {  // DDR words or panels (g.w_panels)
+    const WLaneOff wo = WLane(g, grp * 8 + cl);
+    o.w = wo.codes + ln.wofs;
+    o.w_scale = wo.scale + wo.shift / 8;
+  }
+  (void)wstride;
   if (!kLinear) {  // keep the quad / group for the wrapping on-chip addresses
     o.a = (quad << 16) | (t * 32 + ln.aofs);
     o.a_scale = (quad << 16) | (128 + t);
@@ -198,11 +202,10 @@ __device__ __forceinline__ void LoadBlock(const GemmArgs& g, const uint8_t* a, c
   const uint8_t* w = s.l ? w1 : w0;
   if (kLinear) {
     const uint8_t* ab = a + (size_t)blk * kDdrWord;  // uniform
-    const uint8_t* wb = w + (size_t)blk * kDdrWord;  // uniform
     LoadDwords<T::kA4>(ab + o.a, st.a);
     st.sa = ab[o.a_scale];
-    LoadDwords<T::kW4>(wb + o.w, st.w);
-    st.sw = wb[o.w_scale];
+    LoadDwords<T::kW4>(w + WBlockCodes(g, blk) + o.w, st.w);  // uniform base + lane offset
+    st.sw = w[WBlockScale(g, blk) + o.w_scale];
   } else {
     const uint8_t* aw = AWord<false>(g, a, o.a >> 16, blk);
     const uint8_t* ww = WWord<false>(g, w, o.w >> 16, blk);
@@ -291,6 +294,7 @@ template <bool kLinear>
 __device__ __forceinline__ uint32_t SlowOutput(const GemmArgs& g, const uint8_t* a,
                                                const uint8_t* w0, const uint8_t* w1, uint32_t acc,
                                                uint32_t row, uint32_t col) {
+  if (kLinear) return SlowLinear(g, a, w0, w1, acc, row, col);
   const uint32_t quad = row >> 2, t = row & 3, grp = col >> 3, cl = col & 7;
   for (uint32_t p = 0; p < g.n_pieces; ++p) {
     for (uint32_t l = 0; l < g.n_planes; ++l) {
@@ -723,6 +727,8 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   args.gy = gy;
   const bool small = batch == 1 && gx * gy < kSmallGrid;
   args.fast_ep = fastk ? 1u : 0u;
+  if (fastk && !small && StreamEligible(args)) return LaunchStream(args, batch, stream);
+  if (fastk && !small && PanelEligible(args)) return LaunchPanel(args, batch, stream);
   if (small && fastk) {
     // as many splits as fit in one round of kTargetWorkgroups workgroups
     uint32_t nblocks = 0;

@@ -68,7 +68,54 @@ struct GemmArgs {
   // epilogue arithmetic of a fast-mode layer: FP32 hardware operations
   // instead of the VEC lane formulas (EpApplyFast)
   uint32_t fast_ep;
+  // W planes in the panel layout (HB_LINEAR_PANELS) instead of DDR words;
+  // w_steps = ceil(kb_total / 2), the steps of a panel
+  uint32_t w_panels, w_steps;
 };
+
+// Weight panels (hb_pack_weights): one plane of n columns x kb_total
+// blocks as ceil(n / 64) panels of 64 columns, each ceil(kb_total / 2)
+// steps of 2 blocks; chunk (panel p, step s) is kPanelChunk bytes at
+// (p * steps + s) * kPanelChunk: the 16-byte column-blocks (the DDR word's
+// 16 bytes of one column: element 2j in the low nibble of byte j) at
+// (b * 64 + c) * 16 for block 2s + b and column 64p + c, then the scale
+// bytes at 2048 + 2 (b * 32 + c % 32) + c / 32.  Columns past n and blocks
+// past kb_total are zero codes with scale byte 127.
+constexpr uint32_t kPanelCols = 64, kPanelChunk = 2176, kPanelScales = 2048;
+
+// Byte offsets of W data relative to a plane's base, split into a part that
+// depends on the column only (per lane) and one on the block only (uniform):
+// column col's 16 code bytes of block blk are at codes + BlockCodes(blk),
+// the aligned dword holding its scale byte at scale + BlockScale(blk), the
+// byte at bit `shift` of that dword.
+struct WLaneOff {
+  uint32_t codes, scale, shift;
+};
+__host__ __device__ __forceinline__ WLaneOff WLane(const GemmArgs& g, uint32_t col) {
+  WLaneOff o;
+  if (g.w_panels) {
+    const uint32_t base = (col / kPanelCols) * g.w_steps * kPanelChunk, c = col % kPanelCols;
+    o.codes = base + c * 16;
+    o.scale = base + kPanelScales + 4 * ((c % 32) / 2);
+    o.shift = 8 * (2 * (c % 2) + c / 32);
+  } else {
+    const uint32_t base = (col / 8) * g.kb_total * kDdrWord, cl = col % 8;
+    o.codes = base + cl * 16;
+    o.scale = base + 128 + (cl & 4);
+    o.shift = 8 * (cl & 3);
+  }
+  return o;
+}
+__host__ __device__ __forceinline__ uint32_t WBlockCodes(const GemmArgs& g, uint32_t blk) {
+  return g.w_panels ? (blk / 2) * kPanelChunk + (blk % 2) * (kPanelCols * 16) : blk * kDdrWord;
+}
+__host__ __device__ __forceinline__ uint32_t WBlockScale(const GemmArgs& g, uint32_t blk) {
+  return g.w_panels ? (blk / 2) * kPanelChunk + (blk % 2) * kPanelCols : blk * kDdrWord;
+}
+// Bytes of one plane.
+inline uint64_t PanelBytes(uint32_t n, uint32_t kb_total) {
+  return (uint64_t)((n + kPanelCols - 1) / kPanelCols) * ((kb_total + 1) / 2) * kPanelChunk;
+}
 
 // Byte size of the deferred-epilogue workspace of `args` (sums and flags).
 inline size_t WorkspaceBytes(const GemmArgs& args) {
@@ -133,6 +180,18 @@ hipError_t LaunchLinearFast(const GemmArgs& args, uint32_t batch, hipStream_t st
 // (no ops, no requantize, no K splits); `args` carries the tile grid.
 bool Fp4Eligible(const GemmArgs& args, uint32_t tile_rows);
 hipError_t LaunchFp4(const GemmArgs& args, hipStream_t stream);
+// Streaming kernel over weight panels (hb_panel.hip): fast MXFP4, plain
+// layers of more than 64 rows, one piece over every block.
+bool PanelEligible(const GemmArgs& args);
+hipError_t LaunchPanel(const GemmArgs& args, uint32_t batch, hipStream_t stream);
+// Streaming kernel over weight panels with a global-to-LDS ring (hb_stream.hip).
+bool StreamEligible(const GemmArgs& args);
+hipError_t LaunchStream(const GemmArgs& args, uint32_t batch, hipStream_t stream);
+// DDR words <-> panels of one plane (hb_panel.hip).
+hipError_t LaunchPackPanels(const uint8_t* w, uint32_t n, uint32_t kb_total, uint8_t* out,
+                            hipStream_t stream);
+hipError_t LaunchUnpackPanels(const uint8_t* in, uint32_t n, uint32_t kb_total, uint8_t* w,
+                              hipStream_t stream);
 // Fast path for layers of at most 64 rows (hb_skinny.hip): split-K over the
 // waves of a workgroup, W streamed into registers.
 hipError_t LaunchLinearSkinny(const GemmArgs& args, uint32_t batch, hipStream_t stream);

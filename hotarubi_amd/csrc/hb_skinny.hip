@@ -171,17 +171,24 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
   // The lane's row within a quad (r16 % 4) and column within a group (r16 %
   // 8) are the same in every tile, so the scale dword's offset from the data
   // and the scale byte's position are per lane, not per tile.
+  // W: DDR words or panels (WLane); a column past the layer reads the last
+  // group's column at the same position (its outputs are not stored).
   const uint32_t ashift = 8 * (r16 & 3), as_delta = 128 - (r16 & 3) * 32;
-  const uint32_t cl = r16 & 7, wshift = 8 * (cl & 3), ws_delta = 128 + (cl & 4) - cl * 16;
-  uint32_t a_off[kMT], w_off[kNT];
+  uint32_t a_off[kMT], w_off[kNT], ws_off[kNT], wshift[kNT];
 #pragma unroll
   for (int mi = 0; mi < kMT; ++mi) {
     const uint32_t quad = min((mi * 16 + r16) >> 2, g.quads - 1);
     a_off[mi] = quad * a_row + (r16 & 3) * 32;
   }
 #pragma unroll
-  for (int nj = 0; nj < kNT; ++nj)
-    w_off[nj] = min((col0 + nj * 16 + r16) >> 3, g.groups - 1) * word_row + cl * 16;
+  for (int nj = 0; nj < kNT; ++nj) {
+    const uint32_t col = min((col0 + nj * 16 + r16) >> 3, g.groups - 1) * 8 + (r16 & 7);
+    const WLaneOff wo = WLane(g, col);
+    w_off[nj] = wo.codes;
+    ws_off[nj] = wo.scale;
+    wshift[nj] = wo.shift;
+  }
+  (void)word_row;
 
   // Loads of chunk ch (its lane's block); a chunk at or past c_end, or a
   // block past the end, reloads a valid block and adds zero.
@@ -189,7 +196,8 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t idx = 4 * ch + kq;
     rw.nib = (ch < c_end && idx < nblocks) ? 0x0F0F0F0Fu : 0u;
-    const uint32_t blk = SkinnyBlockOf<kMulti>(g, min(idx, nblocks - 1)) * kDdrWord;
+    const uint32_t ublk = SkinnyBlockOf<kMulti>(g, min(idx, nblocks - 1));
+    const uint32_t blk = ublk * kDdrWord, wbc = WBlockCodes(g, ublk), wbs = WBlockScale(g, ublk);
 #pragma unroll
     for (int mi = 0; mi < kMT; ++mi) {
       const uint8_t* p = a + blk + a_off[mi];
@@ -206,11 +214,11 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
     for (int nj = 0; nj < kNT; ++nj)
 #pragma unroll
       for (int pl = 0; pl < kWP; ++pl) {
-        const uint8_t* wb = (pl ? w1 : w0) + blk;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(wb + w_off[nj]);
+        const uint8_t* wp = pl ? w1 : w0;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(wp + wbc + w_off[nj]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) rw.w[nj][pl][i] = v[i];
-        rw.sw[nj][pl] = *reinterpret_cast<const uint32_t*>(wb + w_off[nj] + ws_delta);
+        rw.sw[nj][pl] = *reinterpret_cast<const uint32_t*>(wp + wbs + ws_off[nj]);
       }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -227,10 +235,10 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
     uint32_t sb[kNT];
 #pragma unroll
     for (int nj = 0; nj < kNT; ++nj) {
-      const uint32_t ewh = __builtin_amdgcn_ubfe(rw.sw[nj][0], wshift, 8);
+      const uint32_t ewh = __builtin_amdgcn_ubfe(rw.sw[nj][0], wshift[nj], 8);
       unsafe |= ewh - kSafeLo > kSafeHi - kSafeLo;
       if constexpr (kW8) {
-        const uint32_t ewl = __builtin_amdgcn_ubfe(rw.sw[nj][1], wshift, 8);
+        const uint32_t ewl = __builtin_amdgcn_ubfe(rw.sw[nj][1], wshift[nj], 8);
         unsafe |= ewl - kSafeLo > kSafeHi - kSafeLo;
         sb[nj] = (ewh - 1u) | ((ewl - 5u) << 8);
 #pragma unroll

@@ -452,3 +452,47 @@ def linear(m, n, kb_total, a_words, planes, modes, pieces=None, c=None, onto=Fal
     if rc:
         raise ValueError(last_error())
     return cc, q_out
+
+
+# ------------------------------------------------------- weight panels --
+# The GPU-native panel layout of a weight plane (this build's format, no
+# reference counterpart): restated here in numpy so the device packer is
+# checked byte for byte.  Pinned by the round trip through unpack_panels and
+# by the linear layer over panels equalling the one over the DDR words.
+
+PANEL_COLS, PANEL_CHUNK = 64, 2176
+
+
+def panel_bytes(n: int, kb: int) -> int:
+    return ((n + PANEL_COLS - 1) // PANEL_COLS) * ((kb + 1) // 2) * PANEL_CHUNK
+
+
+def pack_panels(w_words, n: int, kb: int) -> np.ndarray:
+    """DDR words [n/8][kb][144] -> panels: per (panel p, step s) a chunk of
+    2176 bytes: column-block (block 2s+b, column 64p+c) at (b*64 + c)*16,
+    its scale byte at 2048 + 2*(b*32 + c%32) + c//32; padding columns and
+    blocks are zero codes with scale 127."""
+    P, S = (n + PANEL_COLS - 1) // PANEL_COLS, (kb + 1) // 2
+    wd = np.asarray(w_words, np.uint8).reshape(n // 8, kb, 144)
+    codes = np.zeros((P * PANEL_COLS, 2 * S, 16), np.uint8)
+    scales = np.full((P * PANEL_COLS, 2 * S), 127, np.uint8)
+    codes[:n, :kb] = wd[:, :, :128].reshape(n // 8, kb, 8, 16).transpose(0, 2, 1, 3).reshape(n, kb, 16)
+    scales[:n, :kb] = wd[:, :, 128:136].transpose(0, 2, 1).reshape(n, kb)
+    c = codes.reshape(P, PANEL_COLS, S, 2, 16).transpose(0, 2, 3, 1, 4).reshape(P, S, 2048)
+    # scale (b, c) -> 2 * (b * 32 + c % 32) + c // 32, c = 32 * hi + lo
+    sc = scales.reshape(P, 2, 32, S, 2).transpose(0, 3, 4, 2, 1).reshape(P, S, 128)
+    return np.concatenate([c, sc], axis=2).reshape(-1)
+
+
+def unpack_panels(panels, n: int, kb: int) -> np.ndarray:
+    """Inverse of pack_panels: DDR words [n/8 * kb][144], bytes 136..143 zero."""
+    P, S = (n + PANEL_COLS - 1) // PANEL_COLS, (kb + 1) // 2
+    ch = np.asarray(panels, np.uint8).reshape(P, S, PANEL_CHUNK)
+    codes = ch[:, :, :2048].reshape(P, S, 2, PANEL_COLS, 16).transpose(0, 3, 1, 2, 4) \
+        .reshape(P * PANEL_COLS, 2 * S, 16)
+    scales = ch[:, :, 2048:].reshape(P, S, 2, 32, 2).transpose(0, 4, 3, 1, 2) \
+        .reshape(P * PANEL_COLS, 2 * S)
+    w = np.zeros((n // 8, kb, 144), np.uint8)
+    w[:, :, :128] = codes[:n, :kb].reshape(n // 8, 8, kb, 16).transpose(0, 2, 1, 3).reshape(n // 8, kb, 128)
+    w[:, :, 128:136] = scales[:n, :kb].reshape(n // 8, 8, kb).transpose(0, 2, 1)
+    return w.reshape(-1, 144)

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     assert set(syms) == set(hb.EXPORTS)
     for s in syms:
         assert hasattr(lib, s), s
-    assert lib.hb_abi_version() == hb.ABI_VERSION == 2
+    assert lib.hb_abi_version() == hb.ABI_VERSION == 3
 
 
 def test_product_does_not_link_the_oracle():

@@ -60,33 +60,58 @@ def w8_planes(rng, n, kb):
     return list(helpers.w8_planes_from_int8(rng.integers(-127, 128, (n, kb * 32)))), [1, 2]
 
 
-def batched_layers(gpu, m, n, kb, layers, check, mode, all_codes=False, seed=0):
+def to_panels(gpu, w_d, n, kb):
+    """Device DDR words -> device weight panels (hb_pack_weights)."""
+    out = torch.empty((hb.panel_bytes(n, kb),), dtype=torch.uint8, device=DEV)
+    hb.pack_weights(w_d, n, kb, out, ctx=gpu)
+    return out
+
+
+def batched_layers(gpu, m, n, kb, layers, check, mode, all_codes=False, seed=0, panels=False,
+                   onto=False, bad_scales=False):
     """`layers` MXFP4 layers of one shape in one batched launch; the oracle
-    checks the layers in `check`."""
+    checks the layers in `check`.  panels: the weights go through
+    hb_pack_weights and the layers read the panels.  onto: start from C.
+    bad_scales: a few weight scale bytes outside the fast path's window (those
+    tiles are recomputed with the exact fold)."""
     rng = np.random.default_rng(seed)
-    a_host, w_host = [], []
+    a_host, w_host, c0 = [], [], []
     for i in range(layers):
         if all_codes:
             a = helpers.random_a_words(rng, m, kb)
         else:
             a = helpers.activations(rng, m, kb * 32)[1]
         a_host.append(a)
-        w_host.append(mxfp4_planes(rng, n, kb)[0][0])
+        w = mxfp4_planes(rng, n, kb)[0][0]
+        if bad_scales:
+            w.reshape(-1, 144)[::53, 128 + (i % 8)] = 200
+        w_host.append(w)
+        c0.append(helpers.random_fp32_words(rng, (m, n), 118, 128) if onto else None)
     a_d, w_d = dev(np.stack(a_host)), dev(np.stack(w_host))
-    c_d = torch.zeros((layers, m, n), dtype=torch.float32, device=DEV)
-    descs = [hb.linear_desc(m, n, kb, a_d[i], [w_d[i]], [0], c_d[i], mode=mode)
+    if panels:
+        pb = hb.panel_bytes(n, kb)
+        w_p = torch.empty((layers, pb), dtype=torch.uint8, device=DEV)
+        for i in range(layers):
+            hb.pack_weights(w_d[i], n, kb, w_p[i], ctx=gpu)
+        w_d = w_p
+    c_d = dev(np.stack(c0).view(np.float32)) if onto else \
+        torch.zeros((layers, m, n), dtype=torch.float32, device=DEV)
+    descs = [hb.linear_desc(m, n, kb, a_d[i], [w_d[i]], [0], c_d[i], mode=mode, panels=panels,
+                            onto=onto)
              for i in range(layers)]
     torch.cuda.synchronize()
-    say("batched", dict(m=m, n=n, kb=kb, layers=layers, mode=mode, all_codes=all_codes))
+    say("batched", dict(m=m, n=n, kb=kb, layers=layers, mode=mode, all_codes=all_codes,
+                        panels=panels, onto=onto, bad_scales=bad_scales))
     hb.linear_batched(descs, gpu)
     got = host(c_d).view(np.uint32)
     for i in check:
-        want, _ = helpers.oracle_linear_mt(m, n, kb, a_host[i], [w_host[i]], [0])
+        want, _ = helpers.oracle_linear_mt(m, n, kb, a_host[i], [w_host[i]], [0], onto=c0[i])
         if mode == hb.EXACT:
             assert np.array_equal(got[i], want), i
         else:
             helpers.check_fast(got[i], want,
-                               bound=helpers.block_abs_sums(m, n, kb, a_host[i], [w_host[i]], [0]))
+                               bound=None if onto or bad_scales else
+                               helpers.block_abs_sums(m, n, kb, a_host[i], [w_host[i]], [0]))
 
 
 @pytest.mark.parametrize("layers,check", [(2, (0, 1)), (80, (0, 1, 37, 63, 79))])
@@ -116,10 +141,13 @@ def test_all_int8_codes_skinny(gpu, m):
 
 
 def single_layer(gpu, m, n, kb, w8, mode, ops_fn=None, quantize=False, tbuf=None,
-                 all_codes=False, seed=0, bound=False):
+                 all_codes=False, seed=0, bound=False, panels=False, pieces=None):
     rng = np.random.default_rng(seed)
     a = helpers.random_a_words(rng, m, kb) if all_codes else helpers.activations(rng, m, kb * 32)[1]
     planes, modes = w8_planes(rng, n, kb) if w8 else mxfp4_planes(rng, n, kb)
+    w_dev = [dev(p) for p in planes]
+    if panels:
+        w_dev = [to_panels(gpu, w, n, kb) for w in w_dev]
     ops = ops_fn(rng, m, n) if ops_fn else []
     dev_ops = [(k, dev(v.view(np.float32)) if isinstance(v, np.ndarray) else v) for k, v in ops]
     c_d = torch.zeros((m, n), dtype=torch.float32, device=DEV)
@@ -128,20 +156,21 @@ def single_layer(gpu, m, n, kb, w8, mode, ops_fn=None, quantize=False, tbuf=None
     tb_d = dev(tbuf.view(np.int64)) if tbuf is not None else None
     torch.cuda.synchronize()
     say("layer", dict(m=m, n=n, kb=kb, w8=w8, mode=mode, ops=[o[0] for o in ops],
-                      quantize=quantize, all_codes=all_codes))
-    hb.linear(gpu, a=dev(a), planes=[dev(p) for p in planes], modes=modes, c=c_d, m=m, n=n,
-              kb_total=kb, ops=dev_ops, tbuf=tb_d, q_out=q_d, mode=mode)
+                      quantize=quantize, all_codes=all_codes, panels=panels, pieces=pieces))
+    hb.linear(gpu, a=dev(a), planes=w_dev, modes=modes, c=c_d, m=m, n=n,
+              kb_total=kb, ops=dev_ops, tbuf=tb_d, q_out=q_d, mode=mode, panels=panels,
+              pieces=pieces)
     got = host(c_d).view(np.uint32)
     gq = host(q_d) if quantize else None
     want, wq = helpers.oracle_linear_mt(m, n, kb, a, planes, modes, ops=ops, tbuf=tbuf,
-                                        quantize=quantize)
+                                        quantize=quantize, pieces=pieces)
     if mode == hb.EXACT:
         assert np.array_equal(got, want)
         if quantize:
             assert np.array_equal(gq, wq)
     else:
         helpers.check_fast(got, want, gq, wq,
-                           bound=helpers.block_abs_sums(m, n, kb, a, planes, modes)
+                           bound=helpers.block_abs_sums(m, n, kb, a, planes, modes, pieces)
                            if bound else None)
 
 

@@ -8,26 +8,30 @@
 // v_mfma_scale_f32_32x32x64_f8f6f4 (tools/iss/gemm_array.cpp:84-110).
 //
 // Data flow.  Every operand byte of the K loop reaches LDS by the CU's
-// direct global-to-LDS loads (global_load_lds_dwordx4 / _dword), through a
-// ring of kD steps: per step, each wave's A rows (its 32 rows x 2 blocks: 32
-// code bytes and the scale dword per lane) and the tile's W chunks (5
-// panels x 2176 bytes, spread over the 4 waves, 16 bytes per lane).  The
-// loads hold no registers while in flight, so kD - 1 = 5 steps (about 100 KB
-// per CU) stream ahead of the matrix cores.
+// direct global-to-LDS loads (global_load_lds_dwordx4: lane l's 16 bytes
+// land at M0 + 16 l), through a ring of kD steps.  A step is one table of
+// 20 x 64 pieces of 16 bytes, 5 loads per wave:
+//   A codes   [h][row][32 bytes]: row r's 32 codes of block 2s + h, the
+//             two 16-byte halves of its 32 bytes in the 144-byte word;
+//   A scales  [h][quad][16 bytes]: bytes 128..143 of quad's word of block
+//             2s + h (the 4 rows' E8M0 bytes first);
+//   W chunks  the tile's 5 panels' chunks of step s, 2176 bytes each;
+// so each quad's A words of the step (288 contiguous bytes) and each W
+// chunk are read whole, and the A layout in LDS is row-major: a lane's two
+// 16-byte reads of its row are conflict-free.  The loads hold no registers
+// while in flight, so kD - 2 = 5 steps (100 KB per CU) stream ahead of the
+// matrix cores.
 //   Wave w owns rows 32w..32w+31 of the tile (one m-tile) and all 10
 // n-tiles: it converts only its own A rows (one (row, block) per lane per
-// step), so converted A never passes through LDS; only W is shared, read
-// by each wave from the ring (its B operands, 1 KiB per n-tile).  The
-// conversion of step u + 1 runs on the VALU while the matrix cores run
-// step u.
+// step), so converted A never passes through LDS; W is shared, read by each
+// wave from the ring (its B operands, 1 KiB per n-tile).  The conversion of
+// step u + 1 runs on the VALU while the matrix cores run step u.  C leaves
+// through a 4 KiB LDS block per wave, as 16-byte stores.
 //
-// Synchronisation: one barrier per step.  In iteration u a wave waits for
-// its own loads of step u + 1 (the load counter, counted by hand: the loads
-// are issued from inline asm, which the compiler's own waits do not see),
-// then the barrier (every wave's loads of steps u, u + 1 are in LDS, and
-// every wave has finished reading ring slot u - 1), then it refills slot
-// u - 1 with step u + kD - 1.  Loads past the last step repeat a valid
-// address, so every wave issues the same number of loads every step.
+// Synchronisation: one barrier per step, with the load counter counted by
+// hand (the loads are issued from inline asm, which the compiler's own
+// waits do not see).  Loads past the last step repeat a valid address, so
+// every wave issues the same number of loads every step.
 #include <utility>
 
 #include "hb_device.h"
@@ -48,17 +52,21 @@ constexpr int kBM = 32 * kWaves;                       // tile rows
 constexpr int kTP = 5;                                 // panels per tile
 constexpr int kBN = kTP * (int)kPanelCols;             // tile columns
 constexpr int kNT = 2 * kTP;                           // 32-column n-tiles
-constexpr int kD = 6;                                  // ring depth, steps
-constexpr uint32_t kChunkPieces = kPanelChunk / 16;    // 136 16-byte pieces per chunk
-constexpr uint32_t kPieces = kTP * kChunkPieces;       // W pieces per step
-constexpr int kWRounds = (kPieces + 255) / 256;        // W loads per wave per step
-constexpr uint32_t kABytes = 2304;                     // per wave: 2 x 1 KiB codes, 256 B scales
-constexpr uint32_t kSlotA = kWaves * kABytes;
-constexpr uint32_t kSlotW = kWRounds * 256 * 16;
-constexpr uint32_t kSlot = kSlotA + kSlotW;
-constexpr int kOps = 3 + kWRounds;                     // loads per wave per step
+constexpr int kD = 7;                                  // ring depth, steps
+// the step's table of 16-byte pieces
+constexpr uint32_t kChunkPieces = kPanelChunk / 16;    // 136 per W chunk
+constexpr uint32_t kWPieces = kTP * kChunkPieces;      // 680
+constexpr uint32_t kACodes = 2 * kBM * 32;             // 8192 bytes: [h][row][32]
+constexpr uint32_t kAScales = 2 * (kBM / 4) * 16;      // 1024 bytes: [h][quad][16]
+constexpr uint32_t kAPieces = (kACodes + kAScales) / 16;                  // 576
+constexpr int kALoads = (int)(kAPieces / 64);                             // 9
+constexpr int kWLoads = (int)((kWPieces + 63) / 64);                      // 11
+constexpr int kOps = (kALoads + kWLoads) / kWaves;     // loads per wave per step
+constexpr uint32_t kSlotW = kACodes + kAScales;        // W chunks' offset in a slot
+constexpr uint32_t kSlot = kSlotW + kWLoads * 1024;
 constexpr uint32_t kSafeLo = 70, kSafeHi = 179;
-static_assert((kD - 3) * kOps < 64, "load counter range");
+static_assert(kAPieces % 64 == 0 && (kALoads + kWLoads) % kWaves == 0, "piece table");
+static_assert(kD * kOps < 64, "load counter range");
 static_assert(kSlot % 16 == 0, "16-byte slots");
 
 template <typename Fn, int... kI>
@@ -70,8 +78,8 @@ __device__ __forceinline__ void Unroll(Fn&& f) {
   UnrollImpl(f, std::make_integer_sequence<int, kN>{});
 }
 
-// Direct loads into LDS: lane l's 16 (or 4) bytes at base + voff land at LDS
-// byte lds + 16 l (4 l).  lds is wave-uniform (M0).
+// Direct load into LDS: lane l's 16 bytes at base + voff land at LDS byte
+// lds + 16 l.  lds is wave-uniform (M0).
 // (base and lds are made wave-uniform values in scalar registers.)
 __device__ __forceinline__ uint64_t UniformAddress(const uint8_t* p) {
   // (the builtin returns int: widen through uint32_t, not by sign extension)
@@ -82,11 +90,6 @@ __device__ __forceinline__ uint64_t UniformAddress(const uint8_t* p) {
 }
 __device__ __forceinline__ void Dma16(const uint8_t* base, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(voff), "s"(UniformAddress(base)), "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
-}
-__device__ __forceinline__ void Dma4(const uint8_t* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
                :: "v"(voff), "s"(UniformAddress(base)), "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
@@ -143,17 +146,21 @@ __device__ __forceinline__ Schedule TilesOf(uint32_t total) {
   return sc;
 }
 
-// One step's operands for this lane: the B operands of the tile's 10
-// n-tiles (t: panel t / 2, columns 32 (t % 2) ..) with the panels' scale
-// bytes (bytes 0, 1 of sw[q]: n-tiles 2q, 2q + 1), and the converted A
-// planes h, r/2 with their scale bytes (ea - 1 | (ea - 5) << 8); abad: the
-// lane's A scale byte left the window.
+// Operand set of parity p (steps v = p mod 2) for this lane: step v's B
+// operands of the tile's 10 n-tiles (t: panel t / 2, columns 32 (t % 2) ..)
+// and the panels' scale bytes (bytes 0, 1 of sw[q]: n-tiles 2q, 2q + 1);
+// step v's A, converted: planes h and r/2 (FP6 E2M3 codes) with their scale
+// bytes (ea - 1 | (ea - 5) << 8) and abad, the lane's A scale byte left the
+// window; and the raw A codes and scale dword of a later step of the same
+// parity, loaded ahead of their conversion.
 struct Ops {
   u32x4 b[kNT];
   uint32_t sw[kTP];
   u32x6 h, r;
   int sa;
   uint32_t abad;
+  u32x4 x0, x1;
+  uint32_t sd;
 };
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -165,7 +172,7 @@ void StreamKernel(GemmArgs g) {
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t steps = g.w_steps, nblocks = g.kb_total;
-  const uint32_t total = sc.count * steps;
+  const uint32_t esteps = steps + (steps & 1);  // an odd count gets one all-zero step
   const uint32_t n_panels = (g.n + kPanelCols - 1) / kPanelCols;
   const uint32_t ring = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_ring));
 
@@ -183,26 +190,53 @@ void StreamKernel(GemmArgs g) {
     return tl;
   };
 
-  // Per-lane constants of the loads.  A: row r of the tile, block h of the
-  // step.  W: piece i = (round * 4 + w) * 64 + lane of the step's kPieces
-  // (panel i / 136 of the tile, byte (i % 136) * 16 of its chunk); pieces
-  // past kPieces (padding of the last round) repeat piece 0's panel.
+  // This lane's row r of the tile and block h of the step, in the MFMAs.
   const uint32_t r = w * 32 + (lane & 31), h = lane >> 5;
-  uint32_t wq[kWRounds], woff[kWRounds];
+  // step s of a tile holds live A for this lane iff 2 s < nbh (kept in a
+  // register: a reload of the argument inside the loop would wait for every
+  // outstanding LDS read)
+  uint32_t nbh = nblocks - h;
+  asm volatile("" : "+v"(nbh));
+
+  // The lane's pieces: load k of wave w is load i = kOps w + k of the table
+  // (A for i < kALoads, else W), piece p = 64 i' + lane of its part.
+  //   A: pcol = the piece's bytes in its quad's word, plus 144 h for block
+  //      2s + h; pq = its quad (relative to the tile);
+  //   W: pcol = its bytes in the tile's step-s chunks (panel-relative),
+  //      pq = its panel; pieces past the last chunk repeat piece 0.
+  uint32_t pcol[kOps], pq[kOps];
 #pragma unroll
-  for (int k = 0; k < kWRounds; ++k) {
-    const uint32_t i = (k * kWaves + w) * 64 + lane;
-    wq[k] = i < kPieces ? i / kChunkPieces : 0u;
-    woff[k] = i < kPieces ? (i % kChunkPieces) * 16 : 0u;
+  for (int k = 0; k < kOps; ++k) {
+    const uint32_t i = w * kOps + k;
+    if (i < (uint32_t)kALoads) {
+      const uint32_t pp = i * 64 + lane;
+      if (pp < kACodes / 16) {  // [h][row][half]
+        const uint32_t ph = pp / (kACodes / 32), row = (pp / 2) % kBM;
+        pq[k] = row / 4;
+        pcol[k] = ph * kDdrWord + (row % 4) * 32 + (pp % 2) * 16;
+      } else {                  // [h][quad]
+        const uint32_t q = pp - kACodes / 16;
+        pq[k] = q % (kBM / 4);
+        pcol[k] = (q / (kBM / 4)) * kDdrWord + 128;
+      }
+    } else {
+      const uint32_t pp = (i - kALoads) * 64 + lane;
+      pq[k] = pp < kWPieces ? pp / kChunkPieces : 0u;
+      pcol[k] = pp < kWPieces ? (pp % kChunkPieces) * 16 : 0u;
+    }
   }
 
   // Load cursor: the next global step to load (tile dk, step ds, slot
-  // dslot), with the tile's bases cached.  Past the last step: the last
-  // step again, so every wave issues kOps loads per step.
+  // dslot), with the tile's bases cached.  The padding step and steps past
+  // the last tile load the tile's last step again, so every wave issues
+  // kOps loads per step, all in bounds.  A's block 2s + h is clamped to the
+  // layer's last (a block past it is not live).
   uint32_t dk = 0, ds = 0, dslot = 0, dcached = ~0u;
   const uint8_t* da = nullptr;
   const uint8_t* dw = nullptr;
-  uint32_t da_lane = 0, dw_lane[kWRounds];
+  uint32_t dbase[kOps], alim[kOps];
+#pragma unroll
+  for (int k = 0; k < kOps; ++k) alim[k] = (nblocks - 1) * kDdrWord + pcol[k] % kDdrWord;
   auto issue_next = [&]() __attribute__((always_inline)) {
     const uint32_t k = min(dk, sc.count - 1);
     if (k != dcached) {  // uniform: once per tile
@@ -210,69 +244,71 @@ void StreamKernel(GemmArgs g) {
       const Tile tl = tile_of(k);
       da = g.a + tl.z * g.a_batch;
       dw = g.w[0] + tl.z * g.w_batch;
-      const uint32_t quad = min(tl.row0 / 4 + (r >> 2), g.quads - 1);
-      da_lane = quad * g.a_row * kDdrWord + (r & 3) * 32;
 #pragma unroll
-      for (int k2 = 0; k2 < kWRounds; ++k2)
-        dw_lane[k2] = min(tl.p0 + wq[k2], n_panels - 1) * steps * kPanelChunk + woff[k2];
+      for (int k2 = 0; k2 < kOps; ++k2) {
+        const bool is_a = w * kOps + k2 < (uint32_t)kALoads;
+        dbase[k2] = is_a ? min(tl.row0 / 4 + pq[k2], g.quads - 1) * g.a_row * kDdrWord
+                         : min(tl.p0 + pq[k2], n_panels - 1) * steps * kPanelChunk + pcol[k2];
+      }
     }
-    const uint32_t s = dk < sc.count ? ds : steps - 1;
-    const uint32_t blk = min(2 * s + h, nblocks - 1);
+    const uint32_t s = dk < sc.count ? min(ds, steps - 1) : steps - 1;
     const uint32_t slot = ring + dslot * kSlot;
-    const uint32_t abase = __builtin_amdgcn_readfirstlane(slot + w * kABytes);
-    const uint32_t aw = da_lane + blk * kDdrWord;
-    Dma16(da, aw, abase);
-    Dma16(da, aw + 16, abase + 1024);
-    Dma4(da, aw + 128 - (r & 3) * 32, abase + 2048);
 #pragma unroll
-    for (int k2 = 0; k2 < kWRounds; ++k2)
-      Dma16(dw, dw_lane[k2] + s * kPanelChunk,
-            __builtin_amdgcn_readfirstlane(slot + kSlotA + (k2 * kWaves + w) * 1024));
-    if (++ds == steps) {
+    for (int k2 = 0; k2 < kOps; ++k2) {
+      const uint32_t i = w * kOps + k2;
+      const bool is_a = i < (uint32_t)kALoads;  // uniform
+      const uint32_t off = is_a ? dbase[k2] + min(s * (2 * kDdrWord) + pcol[k2], alim[k2])
+                                : dbase[k2] + s * kPanelChunk;
+      const uint32_t lds = is_a ? slot + i * 1024 : slot + kSlotW + (i - kALoads) * 1024;
+      Dma16(is_a ? da : dw, off, __builtin_amdgcn_readfirstlane(lds));
+    }
+    if (++ds == esteps) {
       ds = 0;
       ++dk;
     }
     dslot = dslot + 1 == kD ? 0u : dslot + 1;
   };
 
-  // Read step (k, s)'s operands from ring slot `slot`: the B operands and
-  // W scale dwords, and this lane's A (converted).
-  auto fetch = [&](Ops& o, uint32_t slot, uint32_t k, uint32_t s) __attribute__((always_inline)) {
-    const uint8_t* base = lds_ring + slot * kSlot;
-    const uint8_t* wslot = base + kSlotA;
+  // Reads from ring slot `slot`: the W chunks' B operands and scale dwords;
+  // this lane's raw A.
+  auto read_w = [&](Ops& o, uint32_t slot) __attribute__((always_inline)) {
+    const uint8_t* wslot = lds_ring + slot * kSlot + kSlotW;
 #pragma unroll
     for (int q = 0; q < kTP; ++q) {
       const uint8_t* chunk = wslot + q * kPanelChunk;
-      o.sw[q] = *reinterpret_cast<const uint32_t*>(chunk + kPanelScales + 4 * (lane >> 1));
 #pragma unroll
       for (int t = 0; t < 2; ++t)
         o.b[2 * q + t] = *reinterpret_cast<const u32x4*>(
             chunk + ((lane >> 5) * kPanelCols + t * 32 + (lane & 31)) * 16);
+      o.sw[q] = *reinterpret_cast<const uint32_t*>(chunk + kPanelScales + 4 * (lane >> 1));
     }
-    const uint8_t* abuf = base + w * kABytes;
-    const u32x4 x0 = *reinterpret_cast<const u32x4*>(abuf + lane * 16);
-    const u32x4 x1 = *reinterpret_cast<const u32x4*>(abuf + 1024 + lane * 16);
-    const uint32_t sd = *reinterpret_cast<const uint32_t*>(abuf + 2048 + lane * 4);
-    const bool live = k < sc.count && 2 * s + h < nblocks;
-    const uint32_t x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+  };
+  auto read_a = [&](Ops& o, uint32_t slot) __attribute__((always_inline)) {
+    const uint8_t* abuf = lds_ring + slot * kSlot;
+    o.x0 = *reinterpret_cast<const u32x4*>(abuf + (h * kBM + r) * 32);
+    o.x1 = *reinterpret_cast<const u32x4*>(abuf + (h * kBM + r) * 32 + 16);
+    o.sd = *reinterpret_cast<const uint32_t*>(abuf + kACodes + (h * (kBM / 4) + r / 4) * 16);
+  };
+  // Convert the raw A held in o, of step (k, s).
+  auto convert = [&](Ops& o, uint32_t k, uint32_t s) __attribute__((always_inline)) {
+    const bool live = k < sc.count && 2 * s < nbh;
+    const uint32_t x[8] = {o.x0[0], o.x0[1], o.x0[2], o.x0[3], o.x1[0], o.x1[1], o.x1[2], o.x1[3]};
     SplitA(x, live ? 0xFFFFFFFFu : 0u, o.h, o.r);
-    const uint32_t ea = __builtin_amdgcn_ubfe(sd, 8 * (r & 3), 8);
+    const uint32_t ea = __builtin_amdgcn_ubfe(o.sd, 8 * (r & 3), 8);
     o.sa = (int)(((ea - 5u) << 8) | ((ea - 1u) & 0xFFu));
     o.abad = live && ea - kSafeLo > kSafeHi - kSafeLo ? 1u : 0u;
   };
 
   float* const xp = lds_xpose[w];
   f32x16 acc[kNT];
-  uint32_t bad = 0;        // this wave's tile saw a scale byte outside the window
-  bool init_unsafe = false;
   Tile tl{};
   uint32_t row_w = 0, live_nt = 0;
+  bool init_unsafe = false;
   // Start tile k: its geometry and the accumulators (+0, or C).
   auto begin_tile = [&](uint32_t k) __attribute__((always_inline)) {
     tl = tile_of(k);
     row_w = tl.row0 + w * 32;
     live_nt = min((uint32_t)kNT, (g.n - min(tl.col0, g.n) + 31) / 32);
-    bad = 0;
     init_unsafe = false;
     if (g.acc) {  // uniform: start from C (a compiler-visible load: drain the ring's first)
       WaitVm<0>();
@@ -296,7 +332,7 @@ void StreamKernel(GemmArgs g) {
     }
   };
   // Finish the current tile: exact recompute if flagged, else store C.
-  auto end_tile = [&]() __attribute__((always_inline)) {
+  auto end_tile = [&](uint32_t bad) __attribute__((always_inline)) {
     const uint8_t* a = g.a + tl.z * g.a_batch;
     const uint8_t* w0 = g.w[0] + tl.z * g.w_batch;
     uint32_t* c = g.c + tl.z * g.c_batch;
@@ -347,73 +383,90 @@ void StreamKernel(GemmArgs g) {
     });
   };
 
-  // Prologue: steps 0 .. kD - 2 in flight; steps 0, 1 landed; step 0 read.
+  // Prologue: steps 0 .. kD - 1 in flight (every slot); steps 0, 1 landed:
+  // step 0's operands read and converted, step 1's raw A read.
 #pragma unroll
-  for (int v = 0; v < kD - 1; ++v) issue_next();
-  WaitVm<(kD - 3) * kOps>();
+  for (int v = 0; v < kD; ++v) issue_next();
+  WaitVm<(kD - 2) * kOps>();
   __syncthreads();
   Ops o0, o1;
-  fetch(o0, 0, 0, 0);
-  begin_tile(0);
+  read_w(o0, 0);
+  read_a(o0, 0);
+  read_a(o1, 1);
+  convert(o0, 0, 0);
 
-  // Iteration u (tile k, step s, ring slot u % kD): wait for this wave's
-  // loads of step u + 1, barrier, refill slot u - 1 with step u + kD - 1,
-  // read step u + 1's operands into the other register set while the
-  // matrix cores run step u.
-  uint32_t u = 0, k = 0, s = 0, slot = 0;
-  auto iteration = [&](const Ops& cur, Ops& nxt) __attribute__((always_inline)) {
+  // Step u = (tile k, step s), ring slot u mod kD, operands in `use` (the
+  // set of u's parity): wait for this wave's loads of step u + 2, barrier
+  // (every wave's loads of step u + 2 landed; every wave done reading slot
+  // u: step u's W was read in step u - 1, its A in step u - 2), refill slot
+  // u with step u + kD; read step u + 1's W into `oth` and step u + 2's raw
+  // A into `use`; convert step u + 1's raw A (read in step u - 1, held in
+  // `oth`) while the matrix cores run step u's 20 MFMAs.
+  uint32_t slot = 0;
+  auto iteration = [&](Ops& use, Ops& oth, uint32_t k, uint32_t s, uint32_t& bad)
+      __attribute__((always_inline)) {
     WaitVm<(kD - 3) * kOps>();
     WaitLds();
     __syncthreads();
     issue_next();
-    const uint32_t nslot = slot + 1 == kD ? 0u : slot + 1;
-    const bool wrap = s + 1 == steps;
-    fetch(nxt, nslot, wrap ? k + 1 : k, wrap ? 0u : s + 1);
+    const uint32_t s1 = slot + 1 == kD ? 0u : slot + 1;
+    const uint32_t s2 = s1 + 1 == kD ? 0u : s1 + 1;
+    read_w(oth, s1);
+    read_a(use, s2);
+    const bool last = s + 1 == esteps;
+    convert(oth, last ? k + 1 : k, last ? 0u : s + 1);
+    slot = s1;
     // the window checks (a panel past the layer repeats the last one's bytes)
-    uint32_t wb = cur.abad;
+    uint32_t wb = use.abad;
 #pragma unroll
     for (int q = 0; q < kTP; ++q) {
-      const uint32_t sq = cur.sw[q] >> (16 * (lane & 1));
+      const uint32_t sq = use.sw[q] >> (16 * (lane & 1));
       wb |= (uint32_t)((sq & 0xFFu) - kSafeLo > kSafeHi - kSafeLo) |
             (uint32_t)(((sq >> 8) & 0xFFu) - kSafeLo > kSafeHi - kSafeLo);
     }
     bad |= wb;
-    const i32x8 ah = {(int)cur.h[0], (int)cur.h[1], (int)cur.h[2], (int)cur.h[3],
-                      (int)cur.h[4], (int)cur.h[5], 0, 0};
-    const i32x8 ar = {(int)cur.r[0], (int)cur.r[1], (int)cur.r[2], (int)cur.r[3],
-                      (int)cur.r[4], (int)cur.r[5], 0, 0};
+    const i32x8 ah = {(int)use.h[0], (int)use.h[1], (int)use.h[2], (int)use.h[3],
+                      (int)use.h[4], (int)use.h[5], 0, 0};
+    const i32x8 ar = {(int)use.r[0], (int)use.r[1], (int)use.r[2], (int)use.r[3],
+                      (int)use.r[4], (int)use.r[5], 0, 0};
     // plane h over the n-tiles, then plane r (branch-free: n-tiles past the
     // layer compute outputs that are not stored)
     Unroll<kNT>([&](auto t_c) {
       constexpr int kT = decltype(t_c)::value;
-      const i32x8 bt = {(int)cur.b[kT][0], (int)cur.b[kT][1], (int)cur.b[kT][2], (int)cur.b[kT][3],
-                        0, 0, 0, 0};
+      const i32x8 bt = {(int)use.b[kT][0], (int)use.b[kT][1], (int)use.b[kT][2],
+                        (int)use.b[kT][3], 0, 0, 0, 0};
       acc[kT] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          ah, bt, acc[kT], 2, 4, 0, cur.sa, kT % 2,
-          (int)(cur.sw[kT / 2] >> (16 * (lane & 1))));
+          ah, bt, acc[kT], 2, 4, 0, use.sa, kT % 2, (int)(use.sw[kT / 2] >> (16 * (lane & 1))));
     });
     Unroll<kNT>([&](auto t_c) {
       constexpr int kT = decltype(t_c)::value;
-      const i32x8 bt = {(int)cur.b[kT][0], (int)cur.b[kT][1], (int)cur.b[kT][2], (int)cur.b[kT][3],
-                        0, 0, 0, 0};
+      const i32x8 bt = {(int)use.b[kT][0], (int)use.b[kT][1], (int)use.b[kT][2],
+                        (int)use.b[kT][3], 0, 0, 0, 0};
       acc[kT] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          ar, bt, acc[kT], 2, 4, 1, cur.sa, kT % 2,
-          (int)(cur.sw[kT / 2] >> (16 * (lane & 1))));
+          ar, bt, acc[kT], 2, 4, 1, use.sa, kT % 2, (int)(use.sw[kT / 2] >> (16 * (lane & 1))));
     });
-    ++u;
-    slot = nslot;
-    if (wrap) {  // uniform: the tile's last step
-      end_tile();
-      s = 0;
-      if (++k < sc.count) begin_tile(k);
-    } else {
-      ++s;
-    }
+    // the step's MFMAs and the conversion are issued here, before the next
+    // barrier, so they overlap the next step's loads and LDS reads
+    // issue order: the LDS reads, then each MFMA followed by a share of the
+    // step's vector ALU work, which runs while the MFMA does
+    __builtin_amdgcn_sched_group_barrier(0x100, 17, 0);
+    Unroll<2 * kNT>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    });
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) asm volatile("" : "+a"(acc[t]));
+    asm volatile("" : "+v"(oth.h), "+v"(oth.r), "+v"(oth.sa), "+v"(oth.abad));
   };
-  while (u < total) {
-    iteration(o0, o1);
-    if (u >= total) break;
-    iteration(o1, o0);
+
+  for (uint32_t k = 0; k < sc.count; ++k) {
+    begin_tile(k);
+    uint32_t bad = 0;  // this wave's tile saw a scale byte outside the window
+    for (uint32_t s = 0; s < esteps; s += 2) {
+      iteration(o0, o1, k, s, bad);
+      iteration(o1, o0, k, s + 1, bad);
+    }
+    end_tile(bad);
   }
   WaitVm<0>();  // no load into LDS outlives the workgroup
 }

@@ -52,6 +52,7 @@ EXPORTS = (
     "hb_t32_split8", "hb_t32_split8_async", "hb_rows", "hb_rows_async",
     "hb_row_load", "hb_row_load_async", "hb_row_store", "hb_row_store_async",
     "hb_gacc", "hb_gacc_async", "hb_panel_bytes", "hb_pack_weights", "hb_unpack_weights",
+    "hb_linear_noalloc_async",
 )
 
 
@@ -181,6 +182,7 @@ def lib():
             "hb_linear": (i, [vp, C.POINTER(_LinearDesc)]),
             "hb_linear_async": (i, [vp, C.POINTER(_LinearDesc)]),
             "hb_linear_batched_async": (i, [vp, C.POINTER(_LinearDesc), u32]),
+            "hb_linear_noalloc_async": (i, [vp, C.POINTER(_LinearDesc), u32]),
             "hb_encode_mxint8": (i, [vp, vp, u32, u32, vp]),
             "hb_gacc": (i, [vp, C.POINTER(_GaccDesc)]),
             "hb_gacc_async": (i, [vp, C.POINTER(_GaccDesc)]),
@@ -424,6 +426,17 @@ def linear_batched(descs, ctx: Context | None = None) -> None:
     ctx = ctx or default_context()
     arr = (_LinearDesc * len(descs))(*descs)
     _check(lib().hb_linear_batched_async(ctx.handle, arr, len(descs)))
+
+
+def linear_noalloc(descs, ctx: Context | None = None) -> None:
+    """hb_linear_noalloc_async: hb_linear_batched_async without any device
+    allocation (the K-split scratch is a fixed per-device array)."""
+    ctx = ctx or default_context()
+    arr = (_LinearDesc * len(descs))(*descs)
+    _check(lib().hb_linear_noalloc_async(ctx.handle, arr, len(descs)))
+
+
+NOALLOC_SCRATCH_BYTES = 8 << 20  # HB_NOALLOC_SCRATCH_BYTES
 
 
 def gacc(base, lst, quads: int, slots: int, blocks: int, w_stride: int, out,

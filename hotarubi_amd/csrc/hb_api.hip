@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -33,9 +34,18 @@ struct hb_onchip {
   uint32_t* temp = nullptr;  // one VEC pass: up to 511 quads x 255 words x 32 values
 };
 
+// Scratch of hb_linear_noalloc_async: one array per device (the code
+// object's copy on that device), never freed.  In host code `scratch` only
+// names the symbol; its device address comes from hipGetSymbolAddress.
+static __device__ __align__(256) uint8_t scratch[HB_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_error;
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch`, per device
 
 int Fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -56,6 +66,20 @@ int HipFail(hipError_t err, const char* what) {
     hipError_t e_ = (call);                           \
     if (e_ != hipSuccess) return HipFail(e_, #call);  \
   } while (0)
+
+// The scratch array's address on `device` (the current device), looked up
+// once per device.
+int ScratchSetUp(int device) {
+  if (device < 0 || device >= kMaxDevices) return Fail(HB_EINVAL, "device %d", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device] != nullptr) return HB_OK;
+  void* p = nullptr;
+  const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (err != hipSuccess) return HipFail(err, "scratch address");
+  if (p == nullptr) return Fail(HB_EDEVICE, "scratch address is null");
+  g_scratch_ptr[device] = p;
+  return HB_OK;
+}
 
 constexpr uint32_t kVecTempWords = 511u * 255u;
 
@@ -540,9 +564,12 @@ uint64_t Diff(const T* a, const T* b) {
   return (uint64_t)(reinterpret_cast<const uint8_t*>(b) - reinterpret_cast<const uint8_t*>(a));
 }
 
-int LinearChain(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count);
+int LinearChain(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count, hb::FixedScratch* fixed);
 
-int LinearBatched(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
+// `fixed`: run without allocating, in that buffer (null: the context's
+// workspace).
+int LinearBatched(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count,
+                  hb::FixedScratch* fixed = nullptr) {
   if (!d || count < 1) return Fail(HB_EINVAL, "no layers");
   hb::GemmArgs g;
   bool mixed = false;
@@ -582,9 +609,12 @@ int LinearBatched(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
       if (!same) return Fail(HB_EINVAL, "layer %u differs in shape, schedule, ops or stride", i);
     }
   }
-  if (mixed) return LinearChain(ctx, d, count);
+  if (mixed) return LinearChain(ctx, d, count, fixed);
   hipError_t err = hb::LaunchLinear(g, count, (d[0].flags & HB_LINEAR_FAST) != 0, ctx->ws,
-                                    ctx->stream);
+                                    ctx->stream, fixed);
+  if (err == hipErrorOutOfMemory && fixed != nullptr && fixed->need > fixed->bytes)
+    return Fail(HB_ENOMEM, "layer needs %zu bytes of K-split scratch; the no-allocation entry point holds %zu",
+                fixed->need, fixed->bytes);
   if (err != hipSuccess) return HipFail(err, "linear launch");
   return HB_OK;
 }
@@ -594,7 +624,7 @@ int LinearBatched(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
 // offset.  The fold is pieces-outer, so starting each run from the previous
 // one's C folds in the same order; the ops and the requantize go with the
 // last run.  The descriptors were validated as a whole.
-int LinearChain(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
+int LinearChain(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count, hb::FixedScratch* fixed) {
   std::vector<hb_linear_desc> part(d, d + count);
   for (uint32_t p0 = 0, p1; p0 < d[0].n_pieces; p0 = p1) {
     for (p1 = p0 + 1; p1 < d[0].n_pieces && PieceShift(d[0], p1) == PieceShift(d[0], p0);) ++p1;
@@ -610,7 +640,7 @@ int LinearChain(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
         x.q_out = nullptr;
       }
     }
-    if (int rc = LinearBatched(ctx, part.data(), count)) return rc;
+    if (int rc = LinearBatched(ctx, part.data(), count, fixed)) return rc;
   }
   return HB_OK;
 }
@@ -629,6 +659,7 @@ int hb_ctx_create(int device, hb_ctx** out) {
   HB_HIP(hipGetDeviceCount(&count));
   if (device < 0 || device >= count) return Fail(HB_EINVAL, "device %d of %d", device, count);
   HB_HIP(hipSetDevice(device));
+  if (int rc = ScratchSetUp(device)) return rc;
   hb_ctx* ctx = new (std::nothrow) hb_ctx;
   if (!ctx) return Fail(HB_ENOMEM, "context");
   ctx->device = device;
@@ -844,6 +875,18 @@ int hb_linear(hb_ctx* ctx, const hb_linear_desc* d) {
 int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
   if (int rc = Enter(ctx)) return rc;
   return LinearBatched(ctx, d, count);
+}
+
+int hb_linear_noalloc_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
+  if (int rc = Enter(ctx)) return rc;
+  void* p = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (ctx->device >= 0 && ctx->device < kMaxDevices) p = g_scratch_ptr[ctx->device];
+  }
+  if (p == nullptr) return Fail(HB_EDEVICE, "no scratch on device %d", ctx->device);
+  hb::FixedScratch fixed{p, HB_NOALLOC_SCRATCH_BYTES, 0};
+  return LinearBatched(ctx, d, count, &fixed);
 }
 
 uint64_t hb_panel_bytes(uint32_t n, uint32_t kb_total) {

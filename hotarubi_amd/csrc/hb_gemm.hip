@@ -706,7 +706,7 @@ void FreeWorkspace(Workspace& ws) {
 }
 
 hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace& ws,
-                        hipStream_t stream) {
+                        hipStream_t stream, FixedScratch* fixed) {
   GemmArgs args = in;
   args.ws = nullptr;
   args.splits = 1;
@@ -745,9 +745,15 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   const bool defer = small && (args.splits > 1 || (!fastk && (args.n_ops > 0 || args.q_out != nullptr)));
   if (!defer) return fastk ? LaunchLinearFast(args, batch, stream) : LaunchTiles<true>(args, batch, stream);
 
-  const hipError_t grown = GrowWorkspace(ws, WorkspaceBytes(args));
-  if (grown != hipSuccess) return grown;
-  args.ws = ws.ptr;
+  if (fixed != nullptr) {  // no allocation: the caller's buffer, or an error
+    fixed->need = WorkspaceBytes(args);
+    if (fixed->need > fixed->bytes || fixed->ptr == nullptr) return hipErrorOutOfMemory;
+    args.ws = static_cast<float*>(fixed->ptr);
+  } else {
+    const hipError_t grown = GrowWorkspace(ws, WorkspaceBytes(args));
+    if (grown != hipSuccess) return grown;
+    args.ws = ws.ptr;
+  }
   const hipError_t err = fastk ? LaunchLinearFast(args, args.splits, stream)  // z = split
                              : LaunchTiles<true>(args, 1, stream);
   if (err != hipSuccess) return err;

@@ -167,8 +167,15 @@ hipError_t LaunchGemmInstrAliased(const GemmArgs& args, hipStream_t stream);
 // Linear layer: picks the kernel, and for a single small layer (few tiles)
 // K splits (fast mode) and/or the deferred element-parallel epilogue, in
 // which case it may grow `ws` (GrowWorkspace).
+// A fixed scratch buffer in place of the context's growable workspace:
+// the launch never allocates; *need reports the bytes a layer needs.
+struct FixedScratch {
+  void* ptr;
+  size_t bytes;
+  size_t need;
+};
 hipError_t LaunchLinear(const GemmArgs& args, uint32_t batch, bool fast, Workspace& ws,
-                        hipStream_t stream);
+                        hipStream_t stream, FixedScratch* fixed = nullptr);
 // Fast path (hb_fast.hip): block-scaled f8f6f4 MFMA for one FP4 plane or
 // the W8 planes (hi, lo), in that order.
 bool FastEligible(const GemmArgs& args);

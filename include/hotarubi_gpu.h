@@ -111,10 +111,12 @@ const char* hb_last_error(void);
 int hb_ctx_create(int device, hb_ctx** out);
 int hb_ctx_destroy(hb_ctx* ctx);
 /* Order the context's work on an existing hipStream_t from now on (NULL is
- * the null stream); the context's own stream, if any, is released.  A
- * context reuses one device workspace across calls (small layers split
- * their K range and finish in a separate element-parallel epilogue), so
- * work issued on an earlier stream must be complete before the switch. */
+ * the null stream); the context's own stream, if any, is synchronized and
+ * destroyed (so make the first switch before any graph capture: a capture
+ * does not allow either).  A context reuses one device workspace across
+ * calls (small layers split their K range and finish in a separate
+ * element-parallel epilogue), so work issued on an earlier stream must be
+ * complete before the switch. */
 int hb_ctx_set_stream(hb_ctx* ctx, void* hip_stream);
 int hb_ctx_synchronize(hb_ctx* ctx);
 
@@ -269,6 +271,20 @@ int hb_linear_async(hb_ctx* ctx, const hb_linear_desc* desc);
  * stride from one layer to the next; otherwise HB_EINVAL. */
 int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* descs,
                             uint32_t count);
+/* hb_linear_batched_async without any device allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc).  The partial sums of a small layer's K splits and its slow
+ * flags, which hb_linear keeps in the context's growable workspace, go to a
+ * fixed per-device scratch array of HB_NOALLOC_SCRATCH_BYTES instead
+ * (resolved when a context is created on the device, held until the
+ * process ends).  A layer that needs more returns HB_ENOMEM, naming the
+ * size; every other argument rule is hb_linear_batched_async's.  All calls
+ * on one GPU share that GPU's array and leave their partials in it:
+ * calls that overlap in time on one GPU (different streams or contexts)
+ * race, so serialize them. */
+#define HB_NOALLOC_SCRATCH_BYTES (8u << 20)
+int hb_linear_noalloc_async(hb_ctx* ctx, const hb_linear_desc* descs, uint32_t count);
 
 /* --------------------------------------------------- weight panels -- */
 

@@ -77,6 +77,9 @@ int ScratchSetUp(int device) {
   const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
   if (err != hipSuccess) return HipFail(err, "scratch address");
   if (p == nullptr) return Fail(HB_EDEVICE, "scratch address is null");
+  // the split kernel's tile counters start at zero (each launch puts back
+  // what it used)
+  HB_HIP(hipMemset(p, 0, hb::kSplitCounterBytes));
   g_scratch_ptr[device] = p;
   return HB_OK;
 }

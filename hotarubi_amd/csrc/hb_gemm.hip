@@ -683,7 +683,8 @@ namespace {
 constexpr uint32_t kSmallGrid = 128, kTargetWorkgroups = 128, kMinSplitSteps = 4;
 }  // namespace
 
-hipError_t GrowWorkspace(Workspace& ws, size_t bytes) {
+hipError_t GrowWorkspace(Workspace& ws, size_t bytes, hipStream_t stream) {
+  bytes += kSplitCounterBytes;
   if (ws.bytes >= bytes) return hipSuccess;
   // at least double, so a run of growing shapes retires few buffers
   size_t want = ws.bytes * 2 > bytes ? ws.bytes * 2 : bytes;
@@ -691,8 +692,13 @@ hipError_t GrowWorkspace(Workspace& ws, size_t bytes) {
   if (ws.ptr != nullptr && ws.n_retired == sizeof ws.retired / sizeof ws.retired[0])
     return hipErrorOutOfMemory;  // (64 doublings: unreachable in practice)
   float* p = nullptr;
-  const hipError_t err = hipMalloc(&p, want);
+  hipError_t err = hipMalloc(&p, want);
   if (err != hipSuccess) return err;
+  err = hipMemsetAsync(p, 0, kSplitCounterBytes, stream);  // the split counters start at zero
+  if (err != hipSuccess) {
+    (void)hipFree(p);
+    return err;
+  }
   if (ws.ptr != nullptr) ws.retired[ws.n_retired++] = ws.ptr;
   ws.ptr = p;
   ws.bytes = want;
@@ -717,9 +723,30 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   // Split-K over the waves of one workgroup pays where a workgroup can hold
   // every row and still many columns: up to 16 rows, or a single MXFP4 layer
   // of up to 64 rows (which otherwise needs K splits and a second launch).
-  if (fastk && (args.quads * 4 <= 16 ||
-                (args.quads * 4 <= 64 && batch == 1 && args.n_planes == 1)))
-    return LaunchLinearSkinny(args, batch, stream);
+  // A single small layer: one launch, K split over workgroups (the last
+  // split of each tile finishes it).  Workspace: the counters, then the
+  // partial sums.
+  if (fastk && SplitEligible(args, batch)) {
+    const size_t part = SplitPlan(args);
+    args.fast_ep = 1u;
+    if (part > 0) {
+      float* base = nullptr;
+      if (fixed != nullptr) {
+        fixed->need = kSplitCounterBytes + part;
+        if (fixed->need > fixed->bytes || fixed->ptr == nullptr) return hipErrorOutOfMemory;
+        base = static_cast<float*>(fixed->ptr);
+      } else {
+        const hipError_t grown = GrowWorkspace(ws, part, stream);
+        if (grown != hipSuccess) return grown;
+        base = ws.ptr;
+      }
+      args.ws = base;
+    }
+    return LaunchSplitLinear(args, stream);
+  }
+  // Batched layers of up to 16 rows: split-K over the waves of one
+  // workgroup, which holds every row.
+  if (fastk && args.quads * 4 <= 16) return LaunchLinearSkinny(args, batch, stream);
   uint32_t gx, gy;
   if (fastk) FastGrid(args, &gx, &gy, &args.tile_rows);
   else ExactGrid(args, &gx, &gy);
@@ -745,14 +772,15 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   const bool defer = small && (args.splits > 1 || (!fastk && (args.n_ops > 0 || args.q_out != nullptr)));
   if (!defer) return fastk ? LaunchLinearFast(args, batch, stream) : LaunchTiles<true>(args, batch, stream);
 
+  // (the partial sums start after the split counters)
   if (fixed != nullptr) {  // no allocation: the caller's buffer, or an error
-    fixed->need = WorkspaceBytes(args);
+    fixed->need = kSplitCounterBytes + WorkspaceBytes(args);
     if (fixed->need > fixed->bytes || fixed->ptr == nullptr) return hipErrorOutOfMemory;
-    args.ws = static_cast<float*>(fixed->ptr);
+    args.ws = static_cast<float*>(fixed->ptr) + kSplitCounterBytes / sizeof(float);
   } else {
-    const hipError_t grown = GrowWorkspace(ws, WorkspaceBytes(args));
+    const hipError_t grown = GrowWorkspace(ws, WorkspaceBytes(args), stream);
     if (grown != hipSuccess) return grown;
-    args.ws = ws.ptr;
+    args.ws = ws.ptr + kSplitCounterBytes / sizeof(float);
   }
   const hipError_t err = fastk ? LaunchLinearFast(args, args.splits, stream)  // z = split
                              : LaunchTiles<true>(args, 1, stream);

@@ -118,6 +118,15 @@ inline uint64_t PanelBytes(uint32_t n, uint32_t kb_total) {
 }
 
 // Byte size of the deferred-epilogue workspace of `args` (sums and flags).
+// Every workspace (the context's, and the no-allocation scratch) starts with
+// kSplitCounters tile counters of the single-launch split kernel, zero
+// whenever no launch is in flight (each launch puts back what it used);
+// the rest, from kSplitCounterBytes on, holds a launch's partial sums.
+constexpr uint32_t kSplitCounters = 4096;
+constexpr size_t kSplitCounterBytes = kSplitCounters * sizeof(uint32_t);
+// Partial-sum tiles a single-launch split layer may use (each 32 x 32 FP32
+// plus a flag): keeps its workspace within 8 MiB.
+constexpr uint32_t kSplitMaxPartials = 2040;
 inline size_t WorkspaceBytes(const GemmArgs& args) {
   const size_t sums = (size_t)args.splits * args.quads * 4 * args.n * sizeof(float);
   return sums + (args.splits > 1 ? (size_t)args.splits * args.gx * args.gy * sizeof(uint32_t) : 0);
@@ -137,7 +146,7 @@ struct Workspace {
   uint32_t n_retired = 0;
 };
 // Make ws at least `bytes` long (hipMalloc; no stream synchronization).
-hipError_t GrowWorkspace(Workspace& ws, size_t bytes);
+hipError_t GrowWorkspace(Workspace& ws, size_t bytes, hipStream_t stream);
 // Free the current and every retired buffer.
 void FreeWorkspace(Workspace& ws);
 
@@ -202,6 +211,14 @@ hipError_t LaunchUnpackPanels(const uint8_t* in, uint32_t n, uint32_t kb_total, 
 // Fast path for layers of at most 64 rows (hb_skinny.hip): split-K over the
 // waves of a workgroup, W streamed into registers.
 hipError_t LaunchLinearSkinny(const GemmArgs& args, uint32_t batch, hipStream_t stream);
+// One fast layer of at most kSplitMaxRows rows in one launch: 32 x 32 tiles,
+// K split over workgroups, the last split of a tile finishing it.
+constexpr uint32_t kSplitMaxRows = 160;
+bool SplitEligible(const GemmArgs& args, uint32_t batch);
+// Grid and K split of a split launch (sets gx, gy, splits, split_steps) and
+// the workspace bytes it needs past the counters (0: no partials).
+size_t SplitPlan(GemmArgs& args);
+hipError_t LaunchSplitLinear(const GemmArgs& args, hipStream_t stream);
 // Exact tile kernel grid for a linear layer (column tiles, row tiles).
 void ExactGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy);
 // Deferred epilogue (hb_vec.hip): reads args.ws, writes C and q_out.

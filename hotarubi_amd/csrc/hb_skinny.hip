@@ -355,6 +355,276 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
   }
 }
 
+// ---------------------------------------------------------------------------
+// One small layer in one launch (HB_LINEAR_FAST, a single layer of at most
+// kSplitMaxRows rows).  A workgroup is one wave and computes a 32 x 32
+// output tile over a range of K steps (64 K values: two blocks per step)
+// with v_mfma_scale_f32_32x32x64_f8f6f4: lane l's A operand is 32 values of
+// row l % 32 and block l / 32 of the step, its B operand 32 values of
+// column l % 32 and the same block (formats and scale bytes as above).
+// The K ranges ("splits") of a tile meet in the workspace: each split
+// writes its 32 x 32 sums (element e of lane l at e * 64 + l) and its window
+// flag, then counts itself on the tile's counter; the split that counts
+// last adds the partials in split order, so the sum does not depend on
+// which split that is, runs the epilogue and the requantize, stores C, and
+// puts the counter back to zero for the next launch.  A tile of one split
+// finishes in place.  Per split about 3.4 KB of operands per step (MXFP4),
+// so a workgroup moves a few 10 KB: small layers are latency-bound, and
+// this spreads them over many CUs in one launch instead of two.
+template <bool kW8>
+struct RawSplit {
+  uint32_t a[8], sa;
+  uint32_t w[kW8 ? 2 : 1][4], sw[kW8 ? 2 : 1];
+  uint32_t nib;  // 0x0F0F0F0F, or 0 for a block past the range (adds zero)
+};
+
+template <bool kW8, bool kMulti>
+__global__ __launch_bounds__(64) void SplitKernel(GemmArgs g) {
+  constexpr int kWP = kW8 ? 2 : 1;
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  const uint32_t lane = threadIdx.x;
+  const uint32_t tiles = g.gx * g.gy;
+  const uint32_t tile = blockIdx.x % tiles, split = blockIdx.x / tiles;
+  const uint32_t col0 = (tile % g.gx) * 32, row0 = (tile / g.gx) * 32;
+  const uint32_t r32 = lane & 31, hb = lane >> 5;
+  const uint8_t* a = g.a;
+  const uint8_t* w0 = g.w[0];
+  const uint8_t* w1 = kW8 ? g.w[1] : w0;
+
+  uint32_t nblocks = 0;
+  for (uint32_t p = 0; p < g.n_pieces; ++p) nblocks += g.piece_kb[p];
+  const uint32_t steps = (nblocks + 1) / 2;
+  const uint32_t s_begin = split * g.split_steps, s_end = min(s_begin + g.split_steps, steps);
+
+  // the lane's A row and W column (a row or column past the layer reads
+  // the last one's bytes; its outputs are not stored)
+  const uint32_t quad = min((row0 + r32) >> 2, g.quads - 1);
+  const uint32_t a_off = quad * g.a_row * kDdrWord + (r32 & 3) * 32;
+  const uint32_t ashift = 8 * (r32 & 3), as_delta = 128 - (r32 & 3) * 32;
+  const WLaneOff wo = WLane(g, min((col0 + r32) >> 3, g.groups - 1) * 8 + (r32 & 7));
+
+  auto load = [&](RawSplit<kW8>& rw, uint32_t st) __attribute__((always_inline)) {
+    const uint32_t idx = 2 * st + hb;
+    rw.nib = (st < s_end && idx < nblocks) ? 0x0F0F0F0Fu : 0u;
+    const uint32_t ublk = SkinnyBlockOf<kMulti>(g, min(idx, nblocks - 1));
+    const uint8_t* p = a + (size_t)ublk * kDdrWord + a_off;
+    const u32x4 v0 = *reinterpret_cast<const u32x4*>(p);
+    const u32x4 v1 = *reinterpret_cast<const u32x4*>(p + 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      rw.a[i] = v0[i];
+      rw.a[4 + i] = v1[i];
+    }
+    rw.sa = *reinterpret_cast<const uint32_t*>(p + as_delta);
+    const uint32_t wbc = WBlockCodes(g, ublk), wbs = WBlockScale(g, ublk);
+#pragma unroll
+    for (int pl = 0; pl < kWP; ++pl) {
+      const uint8_t* wp = pl ? w1 : w0;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(wp + wbc + wo.codes);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rw.w[pl][i] = v[i];
+      rw.sw[pl] = *reinterpret_cast<const uint32_t*>(wp + wbs + wo.scale);
+    }
+  };
+
+  f32x16 acc = {};
+  bool unsafe = false;
+  auto compute = [&](const RawSplit<kW8>& rw) __attribute__((always_inline)) {
+    const uint32_t ewh = __builtin_amdgcn_ubfe(rw.sw[0], wo.shift, 8);
+    unsafe |= ewh - kSafeLo > kSafeHi - kSafeLo;
+    i32x8 b[kWP];
+    uint32_t sb = ewh;
+    if constexpr (kW8) {
+      const uint32_t ewl = __builtin_amdgcn_ubfe(rw.sw[1], wo.shift, 8);
+      unsafe |= ewl - kSafeLo > kSafeHi - kSafeLo;
+      sb = (ewh - 1u) | ((ewl - 5u) << 8);
+#pragma unroll
+      for (int pl = 0; pl < 2; ++pl) {
+        const u32x6 cw = WPlane(rw.w[pl], pl != 0);
+#pragma unroll
+        for (int i = 0; i < 6; ++i) b[pl][i] = (int)cw[i];
+        b[pl][6] = b[pl][7] = 0;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b[0][i] = (int)rw.w[0][i];
+      b[0][4] = b[0][5] = b[0][6] = b[0][7] = 0;
+    }
+    const uint32_t ea = __builtin_amdgcn_ubfe(rw.sa, ashift, 8);
+    unsafe |= ea - kSafeLo > kSafeHi - kSafeLo;
+    const int sa = (int)((ea - 1u) | ((ea - 5u) << 8));
+    i32x8 ap[2];
+#pragma unroll
+    for (int pa = 0; pa < 2; ++pa) {
+      const u32x6 ca = APlane<kW8>(rw.a, rw.nib, pa != 0);
+#pragma unroll
+      for (int i = 0; i < 6; ++i) ap[pa][i] = (int)ca[i];
+      ap[pa][6] = ap[pa][7] = 0;
+    }
+    UnrollS([&](auto pa_c) {
+      constexpr int pa = decltype(pa_c)::value;
+      UnrollS([&](auto pb_c) {
+        constexpr int pb = decltype(pb_c)::value;
+        acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ap[pa], b[pb], acc, 2, kW8 ? 2 : 4,
+                                                              pa, sa, pb, (int)sb);
+      }, std::make_integer_sequence<int, kWP>{});
+    }, std::make_integer_sequence<int, 2>{});
+  };
+
+  // the lane's outputs: element e is row row0 + 8 (e / 4) + 4 hb + e % 4,
+  // column col0 + r32
+  const uint32_t col = col0 + r32;
+  const bool col_in = col < g.n;
+  auto row_of = [&](int e) { return row0 + 8 * (e / 4) + 4 * hb + (e & 3); };
+  // The epilogue's own operands (the initial C, and the first two ops'
+  // [m][n] operand or column value) are loaded before the K loop, so the
+  // split that finishes the tile does not wait for them at the end.
+  constexpr int kPreOps = 2;
+  f32x16 pre_init = {}, pre_x2[kPreOps] = {};
+  float pre_v[kPreOps] = {};
+  if (g.acc && col_in) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      if (row_of(e) < g.m) pre_init[e] = __uint_as_float(g.c[(size_t)row_of(e) * g.n + col]);
+  }
+#pragma unroll
+  for (int op = 0; op < kPreOps; ++op) {
+    if ((uint32_t)op >= g.n_ops || !col_in) continue;
+    const uint32_t kind = g.op_kind[op];
+    if (kind == kEpAddP || kind == kEpMulP) pre_v[op] = __uint_as_float(g.op_vec[op][col]);
+    if (kind == kEpAdd || kind == kEpActMul) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (row_of(e) < g.m)
+          pre_x2[op][e] = __uint_as_float(g.op_x2[op][(size_t)row_of(e) * g.n + col]);
+    }
+  }
+
+  // K loop: kAhead steps' loads in flight (a split of a small layer has
+  // about that many, so they all go out at once); steps past the range are
+  // neither loaded nor computed.
+  constexpr int kAhead = 4;
+  RawSplit<kW8> ring[kAhead];
+#pragma unroll
+  for (int i = 0; i < kAhead; ++i)
+    if (s_begin + i < s_end) load(ring[i], s_begin + i);
+  for (uint32_t st = s_begin; st < s_end; st += kAhead) {
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) {
+      if (st + i < s_end) compute(ring[i]);
+      if (st + kAhead + i < s_end) load(ring[i], st + kAhead + i);
+    }
+  }
+  bool slow = __builtin_amdgcn_ballot_w64(unsafe) != 0;
+  f32x16 sum;
+  if (g.splits > 1) {
+    float* part = g.ws + kSplitCounterBytes / 4;
+    uint32_t* flags = reinterpret_cast<uint32_t*>(part + (size_t)tiles * g.splits * 1024);
+    uint32_t* counters = reinterpret_cast<uint32_t*>(g.ws);
+    // Partials, flags and the counter are exchanged with device-scope
+    // atomic stores, loads and adds, which the L2 writes through or reads
+    // coherently: a device-scope fence would write back and invalidate the
+    // whole L2 of the XCD in every workgroup.  The stores complete (load
+    // counter at zero) before the count.
+    float* mine = part + ((size_t)tile * g.splits + split) * 1024;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      __hip_atomic_store(&mine[e * 64 + lane], acc[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0)
+      __hip_atomic_store(&flags[tile * g.splits + split], slow ? 1u : 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    uint32_t old = 0;
+    if (lane == 0)
+      old = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != g.splits - 1) return;  // (uniform) another split finishes the tile
+    if (lane == 0)
+      __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    auto partial = [&](uint32_t s) __attribute__((always_inline)) {
+      float* ps = part + ((size_t)tile * g.splits + s) * 1024;
+      f32x16 v;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        v[e] = __hip_atomic_load(&ps[e * 64 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return v;
+    };
+    auto flag = [&](uint32_t s) __attribute__((always_inline)) {
+      return __hip_atomic_load(&flags[tile * g.splits + s], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT) != 0;
+    };
+    sum = partial(0);
+    slow = flag(0);
+    for (uint32_t s = 1; s < g.splits; ++s) {
+      sum += partial(s);
+      slow |= flag(s);
+    }
+  } else {
+    sum = acc;
+  }
+
+  uint32_t* c = g.c;
+  f32x16 y;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const uint32_t row = row_of(e);
+    y[e] = pre_init[e] + sum[e] + 0.0f;
+    if (slow && col_in && (row >> 2) < g.quads)  // a scale byte left the window: exactly
+      y[e] = __uint_as_float(SlowLinear(g, a, w0, w1, __float_as_uint(pre_init[e]), row, col));
+  }
+  const uint64_t* act = g.tbuf != nullptr ? g.tbuf + 512 : nullptr;
+  for (uint32_t op = 0; op < g.n_ops; ++op) {
+    const uint32_t kind = g.op_kind[op];
+    float pv = 0.0f;
+    f32x16 x2 = {};
+    if (op < (uint32_t)kPreOps) {
+#pragma unroll
+      for (int i = 0; i < kPreOps; ++i)
+        if (op == (uint32_t)i) {
+          pv = pre_v[i];
+          x2 = pre_x2[i];
+        }
+    } else if (col_in) {
+      if (kind == kEpAddP || kind == kEpMulP) pv = __uint_as_float(g.op_vec[op][col]);
+      if (kind == kEpAdd || kind == kEpActMul) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (row_of(e) < g.m) x2[e] = __uint_as_float(g.op_x2[op][(size_t)row_of(e) * g.n + col]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) y[e] = EpApplyFast(kind, g.op_imm[op], y[e], x2[e], pv, act);
+  }
+  if (col_in) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t row = row_of(e);
+      if (row < g.m) c[(size_t)row * g.n + col] = __float_as_uint(y[e]);
+    }
+  }
+  if (g.q_out != nullptr) {
+    // one MXINT8 block: the row's 32 columns are the 32 lanes of this half
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t row = row_of(e);
+      const bool in = (row >> 2) < g.quads && col_in;
+      const uint32_t bits = __float_as_uint(y[e]);
+      uint32_t ex = in ? ExpField(bits) : 0u;
+      ex = max(ex, (uint32_t)__shfl_xor((int)ex, 1));
+      ex = max(ex, (uint32_t)__shfl_xor((int)ex, 2));
+      ex = max(ex, (uint32_t)__shfl_xor((int)ex, 4));
+      ex = max(ex, (uint32_t)__shfl_xor((int)ex, 8));
+      ex = max(ex, (uint32_t)__shfl_xor((int)ex, 16));
+      if (in) {
+        uint8_t* word = g.q_out + ((size_t)(row >> 2) * (g.n >> 5) + (col >> 5)) * kDdrWord;
+        word[(row & 3) * 32 + r32] = QuantizeElement(bits, ex);
+        if (r32 == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(ex);
+        if (r32 < 12 && (row & 3) == 0) word[132 + r32] = 0;
+      }
+    }
+  }
+}
+
 template <int kMT, bool kW8, bool kMulti>
 void LaunchS(const GemmArgs& in, uint32_t batch, hipStream_t stream) {
   constexpr int kCols = 16 * NTiles<kMT, kW8>();
@@ -376,6 +646,47 @@ void LaunchRowsS(const GemmArgs& args, uint32_t batch, hipStream_t stream) {
 }
 
 }  // namespace
+
+bool SplitEligible(const GemmArgs& args, uint32_t batch) {
+  return batch == 1 && args.quads * 4 <= kSplitMaxRows;
+}
+
+size_t SplitPlan(GemmArgs& args) {
+  // splits of at least 4 steps, at most 8 per tile (the last split reads
+  // them all), within kSplitMaxPartials partial tiles
+  constexpr uint32_t kMinSteps = 4, kMaxSplits = 8;
+  args.gx = (args.n + 31) / 32;
+  args.gy = (args.quads * 4 + 31) / 32;
+  args.gz = 1;
+  uint32_t nblocks = 0;
+  for (uint32_t p = 0; p < args.n_pieces; ++p) nblocks += args.piece_kb[p];
+  const uint32_t steps = (nblocks + 1) / 2, tiles = args.gx * args.gy;
+  uint32_t per = (steps + kMaxSplits - 1) / kMaxSplits;
+  per = per < kMinSteps ? kMinSteps : per;
+  uint32_t splits = (steps + per - 1) / per;
+  if (tiles > kSplitCounters) splits = 1;
+  while (splits > 1 && tiles * splits > kSplitMaxPartials) {
+    --splits;
+    per = (steps + splits - 1) / splits;
+    splits = (steps + per - 1) / per;
+  }
+  args.splits = splits;
+  args.split_steps = splits > 1 ? per : steps;
+  return splits > 1 ? (size_t)tiles * splits * (1024 * sizeof(float) + sizeof(uint32_t)) : 0;
+}
+
+hipError_t LaunchSplitLinear(const GemmArgs& args, hipStream_t stream) {
+  const dim3 grid(args.gx * args.gy * args.splits), block(64);
+  const bool w8 = args.n_planes == 2, multi = args.n_pieces > 1;
+  if (w8) {
+    if (multi) hipLaunchKernelGGL((SplitKernel<true, true>), grid, block, 0, stream, args);
+    else hipLaunchKernelGGL((SplitKernel<true, false>), grid, block, 0, stream, args);
+  } else {
+    if (multi) hipLaunchKernelGGL((SplitKernel<false, true>), grid, block, 0, stream, args);
+    else hipLaunchKernelGGL((SplitKernel<false, false>), grid, block, 0, stream, args);
+  }
+  return hipGetLastError();
+}
 
 hipError_t LaunchLinearSkinny(const GemmArgs& args, uint32_t batch, hipStream_t stream) {
   const uint32_t rows = args.quads * 4;

@@ -3,8 +3,8 @@ allocation, its K-split scratch a fixed per-device array.  Its results are
 checked bitwise against hb_linear_batched_async's on the same descriptors
 (the same kernels run; only the scratch buffer differs):
 
-  * two calls in a row on small layers that take the K-split path (the
-    second one smaller, so it runs over what the first left in the scratch),
+  * two calls in a row on small layers whose K splits meet in the scratch
+    (the second one smaller, so it runs over what the first left there),
     then an exact-mode layer whose epilogue is deferred through the scratch;
   * batched and skinny layers, which need no scratch;
   * capture in a HIP graph, replayed between eager work (the point of the
@@ -78,7 +78,8 @@ def run_both(gpu, m, n, kb, a, planes, modes, mode, ops=(), layers=1):
 
 def test_two_calls_in_a_row_second_smaller(gpu):
     rng = np.random.default_rng(11)
-    # 141 x 960 x 2560 MXFP4: 8 fast tiles -> 10 K splits, ~5.5 MB of partials
+    # 141 x 960 x 2560 MXFP4: 150 tiles of 32 x 32, 8 K splits each, ~4.9 MB
+    # of partial sums
     m, n, kb = 141, 960, 80
     a, planes, modes = mxfp4_layer(rng, m, n, kb)
     say("call 1", dict(m=m, n=n, kb=kb))
@@ -86,7 +87,7 @@ def test_two_calls_in_a_row_second_smaller(gpu):
     assert np.array_equal(got, ref)
     want, _ = helpers.oracle_linear_mt(m, n, kb, a, planes, modes)
     helpers.check_fast(got[0], want)
-    # smaller: 72 x 512 x 768 W8 (2 tiles -> 3 K splits) over what call 1 left
+    # smaller: 72 x 512 x 768 W8 (48 tiles, 3 K splits) over what call 1 left
     m, n, kb = 72, 512, 24
     a, planes, modes = w8_layer(rng, m, n, kb)
     say("call 2", dict(m=m, n=n, kb=kb))
@@ -168,10 +169,10 @@ def test_graph_capture_of_a_new_shape(gpu):
 
 
 def test_oversize_layer_is_rejected(gpu):
-    # 128 x 16384 x 2048 MXFP4: 64 fast tiles -> 2 K splits, ~16.8 MB of
-    # partial sums, over the 8 MiB array
+    # 256 x 4096 x 2048 MXFP4: 32 tiles of 128 x 256 rows, 4 K splits, ~16.8 MB
+    # of partial sums, over the 8 MiB array
     rng = np.random.default_rng(15)
-    m, n, kb = 128, 16384, 64
+    m, n, kb = 256, 4096, 64
     a = helpers.activations(rng, m, kb * 32)[1]
     w = torch.zeros((n // 8 * kb, 144), dtype=torch.uint8, device=DEV)
     c = torch.zeros((m, n), dtype=torch.float32, device=DEV)

@@ -17,12 +17,15 @@ SmolVLA action-expert step (its GEMM chain) and the SmolVLA LM prefix (its
 16 MXFP4 decoder layers' GEMMs) at batch 1 and 32.
 
     python bench.py [--steps K] [--warmup W] [--mode exact|fast] [--layers L]
-                    [--quick] [--no-cpu] [--copy-probe MIB]
+                    [--quick] [--no-cpu] [--copy-probe MIB] [--settle S]
 
 Prints one JSON line.  The CPU baseline times the oracle (a C restatement of
 the reference's CPU path, single thread) on one layer of the same shape.
 --copy-probe copies MIB MiB on the device three times first (a plain copy of
-known size, to calibrate HBM byte counters under a profiler).
+known size, to calibrate HBM byte counters under a profiler).  --settle runs
+the headline untimed for S seconds before its warmup steps, so the clocks
+have reached their sustained-load state (default 0.5; 0 under a counter
+profiler, which would otherwise sample every one of those launches).
 """
 from __future__ import annotations
 
@@ -153,39 +156,57 @@ def counted_traffic(kernel_tag):
 
 
 class Workload:
-    """L layers of one shape on the device, with their descriptors."""
+    """L layers of one shape on the device, with their descriptors.  Every
+    layer's A is MXINT8 of its own N(0,1) fp32 matrix (hb_encode_mxint8:
+    EncodeMxint8 + PackAbuf, max-abs rule); MXFP4 W has random E2M1 codes and
+    E8M0 exponents uniform in [-10, -2]; W8 W is two nibble planes of random
+    codes (int8 weights uniform over [-128, 127]) sharing the scale byte 133
+    (MXINT8 of int8 values).  All drawn on the device from a seeded
+    generator.  panels: the weights are packed once (hb_pack_weights) and the
+    layers read the panels."""
 
-    def __init__(self, hb, torch, m, n, kb, w8, layers, mode, epilogue=False, seed=1):
+    def __init__(self, hb, torch, ctx, m, n, kb, w8, layers, mode, epilogue=False, seed=1,
+                 panels=False):
         dev = "cuda:0"
         self.m, self.n, self.kb, self.w8, self.layers = m, n, kb, w8, layers
         self.n_vectors = 2 if epilogue else 0
-        a1, w1 = make_inputs(np.random.default_rng(seed), m, n, kb, w8)
-        L = layers
-        self.a = torch.empty((L,) + a1.shape, dtype=torch.uint8, device=dev)
-        self.w = [torch.empty((L,) + p.shape, dtype=torch.uint8, device=dev) for p in w1]
-        for i in range(min(L, 4)):  # four layers from the host generator
-            ai, wi = make_inputs(np.random.default_rng(seed * 100 + i), m, n, kb, w8)
-            self.a[i].copy_(torch.from_numpy(ai))
-            for p in range(len(wi)):
-                self.w[p][i].copy_(torch.from_numpy(wi[p]))
-        if L > 4:  # the rest: same scales, fresh codes drawn on the device
-            g = torch.Generator(device=dev).manual_seed(seed + 5)
-            self.a[4:] = self.a[:1]
-            for p in range(len(self.w)):
-                self.w[p][4:] = self.w[p][:1]
-                self.w[p][4:, :, :128] = torch.randint(0, 256, self.w[p][4:, :, :128].shape,
-                                                       generator=g, device=dev, dtype=torch.uint8)
-            self.a[4:, :, :128] = torch.randint(0, 256, self.a[4:, :, :128].shape, generator=g,
-                                                device=dev, dtype=torch.uint8)
+        self.panels = panels
+        L, quads = layers, (m + 3) // 4
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.a = torch.empty((L, quads * kb, 144), dtype=torch.uint8, device=dev)
+        for i in range(L):
+            x = torch.randn((m, kb * 32), generator=g, device=dev)
+            hb.encode_mxint8(x, m, kb * 32, self.a[i], ctx=ctx)
+            del x
+        planes = 2 if w8 else 1
+        w = [torch.randint(0, 256, (L, n // 8 * kb, 144), generator=g, device=dev,
+                           dtype=torch.uint8) for _ in range(planes)]
+        for p in w:
+            p[:, :, 136:] = 0
+            if w8:
+                p[:, :, 128:136] = 133
+            else:
+                p[:, :, 128:136] = torch.randint(117, 126, (L, n // 8 * kb, 8), generator=g,
+                                                 device=dev, dtype=torch.uint8)
+        if panels:
+            pb = hb.panel_bytes(n, kb)
+            self.w = [torch.empty((L, pb), dtype=torch.uint8, device=dev) for _ in range(planes)]
+            for p in range(planes):
+                for i in range(L):
+                    hb.pack_weights(w[p][i], n, kb, self.w[p][i], ctx=ctx)
+            del w
+        else:
+            self.w = w
         self.c = torch.zeros((L, m, n), dtype=torch.float32, device=dev)
         ops_t = []
         if epilogue:  # per-channel scale ~ U(0.001, 0.02), bias ~ N(0, 0.1)
-            self.scale = torch.rand((L, n), device=dev) * 0.019 + 0.001
-            self.bias = torch.randn((L, n), device=dev) * 0.1
+            self.scale = torch.rand((L, n), generator=g, device=dev) * 0.019 + 0.001
+            self.bias = torch.randn((L, n), generator=g, device=dev) * 0.1
             ops_t = [(hb.EP_MULP, self.scale), (hb.EP_ADDP, self.bias)]
         modes = [1, 2] if w8 else [0]
         self.descs = [hb.linear_desc(m, n, kb, self.a[i], [p[i] for p in self.w], modes,
-                                     self.c[i], ops=[(k, t[i]) for k, t in ops_t], mode=mode)
+                                     self.c[i], ops=[(k, t[i]) for k, t in ops_t], mode=mode,
+                                     panels=panels)
                       for i in range(L)]
         torch.cuda.synchronize()
 
@@ -753,9 +774,23 @@ def chain_summary(work, ms, mfma_class):
     return round(tops, 3), roof
 
 
-def time_steps(hb, torch, ctx, stream, work, steps, warmup):
+def settle(fn, torch, seconds):
+    """Run fn back to back for about `seconds` (untimed), so the GPU's clocks
+    reach the state they keep under sustained load of this kind before a
+    timed region starts (they ramp over a few hundred milliseconds)."""
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+
+
+def time_steps(hb, torch, ctx, stream, work, steps, warmup, settle_s=0.0):
     """Average ms per step over `steps` back-to-back batched launches, timed
-    with events on the stream the kernels run on."""
+    with events on the stream the kernels run on (after `settle_s` seconds of
+    untimed steps and `warmup` more)."""
+    if settle_s > 0:
+        settle(lambda: hb.linear_batched(work.descs, ctx), torch, settle_s)
     for _ in range(warmup):
         hb.linear_batched(work.descs, ctx)
     torch.cuda.synchronize()
@@ -784,6 +819,38 @@ def summarize(work, ms, mfma_class, kernel_tag=None):
     return tops, roof
 
 
+def single_layer_latency(hb, torch, ctx, stream, m, n, kb, launches=50):
+    """Milliseconds per launch of one MXFP4 layer (fast mode, weights in
+    panels), launched back to back on one stream: its one-launch latency,
+    as a chain of dependent layers sees it (a launch starts when the one
+    before it has ended)."""
+    work = Workload(hb, torch, ctx, m, n, kb, False, 1, hb.FAST, seed=9, panels=True)
+    d = work.descs[0]
+    settle(lambda: hb.launch(d, ctx), torch, 0.05)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(launches):
+        hb.launch(d, ctx)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return round(t0.elapsed_time(t1) / launches, 4)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+TOLERANCE = ("fast mode: per element |got - exact| <= 2^-17 * sum over blocks of |block value| "
+             "(measured envelope; the normwise per-row max |got - exact| <= 1e-5 * max |exact| "
+             "holds on N(0,1) data); exact mode: bitwise")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -797,6 +864,8 @@ def main():
                     help="headline plus this group of extra fields only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
+    ap.add_argument("--settle", type=float, default=0.5, metavar="S",
+                    help="seconds of untimed headline steps before the warmup (0: none)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}); nothing in this build "
@@ -821,9 +890,11 @@ def main():
     mode = hb.FAST if fast else hb.EXACT
     n, kb = 960, 80
 
-    work = Workload(hb, torch, args.m, n, kb, False, args.layers, mode)
-    ms = time_steps(hb, torch, ctx, stream, work, args.steps, args.warmup)
-    tag = "Fp4Kernel<false>" if fast else "GemmTileKernel<linear,128,128>"
+    # weights packed into panels once, before timing (fast mode reads them;
+    # the exact kernel reads DDR words)
+    work = Workload(hb, torch, ctx, args.m, n, kb, False, args.layers, mode, panels=fast)
+    ms = time_steps(hb, torch, ctx, stream, work, args.steps, args.warmup, settle_s=args.settle)
+    tag = "StreamKernel" if fast else "GemmTileKernel<linear,128,128>"
     tops, roof = summarize(work, ms, "fp6_fp4" if fast else "bf16",
                            tag if (args.m == 128 and args.layers == 256) else None)
     del work
@@ -840,12 +911,16 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "mxint8 x mxfp4 -> fp32",
-        "data": "synthetic (seeded MXINT8 activations of N(0,1), random E2M1 codes, "
-                "E8M0 exponents -10..-2)",
+        "data": "synthetic, seeded, drawn on the device: each layer's activations MXINT8 of "
+                "its own N(0,1) fp32 matrix (max-abs rule), random E2M1 weight codes, E8M0 "
+                "exponents uniform in -10..-2",
         "config": {"workload": f"MXFP4 linear M={args.m} K={kb * 32} N={n}, "
                                f"{args.layers} distinct layers per step",
                    "mode": args.mode, "layers_per_step": args.layers, "m": args.m,
-                   "k": kb * 32, "n": n},
+                   "k": kb * 32, "n": n,
+                   "weights": "panels (hb_pack_weights, once, untimed)" if fast else "DDR words",
+                   "settle_s": args.settle},
+        "tolerance": TOLERANCE,
         "roofline": roof,
     }
 
@@ -853,30 +928,40 @@ def main():
         extra_steps, extra_warm = 5, 1
         # the same workload in the other mode
         other = hb.EXACT if fast else hb.FAST
-        w2 = Workload(hb, torch, args.m, n, kb, False, args.layers, other)
-        ms2 = time_steps(hb, torch, ctx, stream, w2, extra_steps, extra_warm)
+        w2 = Workload(hb, torch, ctx, args.m, n, kb, False, args.layers, other,
+                      panels=other == hb.FAST)
+        ms2 = time_steps(hb, torch, ctx, stream, w2, extra_steps, extra_warm, settle_s=0.2)
         t2, r2 = summarize(w2, ms2, "bf16" if fast else "fp6_fp4")
         out["exact" if fast else "fast"] = {"value": round(t2, 3), "unit": "TOPS",
                                             "ms_per_step": round(ms2, 4), "roofline": r2}
         del w2
         # M sweep (fast MXFP4), enough layers per step to exceed the caches
         sweep = {}
-        for m, L in ((1, 256), (16, 256), (1024, 64)):
-            ws = Workload(hb, torch, m, n, kb, False, L, hb.FAST, seed=3)
-            mss = time_steps(hb, torch, ctx, stream, ws, extra_steps, extra_warm)
+        # (M=1 and 16 read DDR words: the skinny kernel's per-lane loads
+        # of a batch of layers do better over them than over panels)
+        for m, L, pan in ((1, 256, False), (16, 256, False), (1024, 64, True)):
+            ws = Workload(hb, torch, ctx, m, n, kb, False, L, hb.FAST, seed=3, panels=pan)
+            mss = time_steps(hb, torch, ctx, stream, ws, extra_steps, extra_warm, settle_s=0.2)
             ts, rs = summarize(ws, mss, "fp6_fp4")
             sweep[f"M={m}"] = {"value": round(ts, 3), "unit": "TOPS", "layers": L,
+                               "weights": "panels" if pan else "DDR words",
                                "ms_per_step": round(mss, 4), "roofline": rs}
             del ws
         sweep["M=128"] = {"value": out["value"], "unit": "TOPS", "layers": args.layers,
                           "ms_per_step": out["ms_per_step"], "roofline": roof}
         out["mxfp4_fast_m_sweep"] = sweep
+        # one layer of the same shape, one launch at a time
+        out["mxfp4_fast_single_layer_ms"] = {
+            "workload": f"one MXFP4 layer K={kb * 32} N={n} per launch, launches back to back "
+                        "on one stream, weights in panels",
+            **{f"M={m}": single_layer_latency(hb, torch, ctx, stream, m, n, kb)
+               for m in (1, 16, 128, 1024)}}
         # W8 layer with per-channel scale and bias, fast and exact
         L8 = 128
         w8 = {"workload": f"W8 linear M=64 K=960 N=2560 + MULP + ADDP, {L8} layers per step"}
         for name, md, cls in (("fast", hb.FAST, "int8"), ("exact", hb.EXACT, "bf16")):
-            wk = Workload(hb, torch, 64, 2560, 30, True, L8, md, epilogue=True, seed=4)
-            ms8 = time_steps(hb, torch, ctx, stream, wk, extra_steps, extra_warm)
+            wk = Workload(hb, torch, ctx, 64, 2560, 30, True, L8, md, epilogue=True, seed=4)
+            ms8 = time_steps(hb, torch, ctx, stream, wk, extra_steps, extra_warm, settle_s=0.2)
             t8, r8 = summarize(wk, ms8, cls)
             w8[name] = {"value": round(t8, 3), "unit": "TOPS", "ms_per_step": round(ms8, 4),
                         "roofline": r8}
@@ -947,6 +1032,7 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.m, n, kb)
         out["cpu_baseline_cores"] = cpu_baseline_cores(args.m, n, kb)
+        out["cpu_baseline"]["cpu_model"] = out["cpu_baseline_cores"]["cpu_model"] = cpu_model()
     print(json.dumps(out), flush=True)
     ctx.close()
 

@@ -196,19 +196,30 @@ __device__ __forceinline__ uint32_t ScaleByteOf(uint32_t emax) { return emax == 
 // NPU's ordered fold, tools/iss/gemm_array.cpp:123-147 as emitted per
 // tools/compiler/kernels.cpp:343-395: pieces, then planes, then blocks),
 // starting from acc.
+// kLayout: 0 reads g.w_panels, 1 DDR words, 2 panels (known to the caller).
+template <int kLayout = 0>
 __device__ __forceinline__ uint32_t SlowLinear(const GemmArgs& g, const uint8_t* a,
                                                const uint8_t* w0, const uint8_t* w1, uint32_t acc,
                                                uint32_t row, uint32_t col) {
+  const bool panels = kLayout == 0 ? g.w_panels != 0 : kLayout == 2;
   const uint32_t quad = row >> 2, t = row & 3;
-  const WLaneOff wo = WLane(g, col);
+  const WLaneOff wo = WLane(g, col, panels);
   for (uint32_t p = 0; p < g.n_pieces; ++p)
     for (uint32_t l = 0; l < g.n_planes; ++l)
       for (uint32_t b = 0; b < g.piece_kb[p]; ++b) {
         const uint32_t blk = g.piece_off[p] + b, mode = g.modes[l];
         const uint8_t* aw = a + ((size_t)quad * g.a_row + blk) * kDdrWord;
         const uint8_t* wp = l ? w1 : w0;
-        const uint8_t* codes = wp + wo.codes + WBlockCodes(g, blk);
-        const uint32_t wscale = wp[wo.scale + WBlockScale(g, blk) + wo.shift / 8];
+        const uint8_t* codes;
+        uint32_t wscale;
+        if (panels) {
+          codes = wp + wo.codes + WBlockCodes(g, blk, true);
+          wscale = wp[wo.scale + WBlockScale(g, blk, true) + wo.shift / 8];
+        } else {  // the column's 16 code bytes and its scale byte in the block's word
+          const uint8_t* ww = wp + ((size_t)(col >> 3) * g.kb_total + blk) * kDdrWord;
+          codes = ww + (col & 7) * 16;
+          wscale = ww[128 + (col & 7)];
+        }
         int32_t sum = 0;
         for (uint32_t k = 0; k < 32; ++k) {
           const uint32_t byte = codes[k >> 1];

@@ -91,9 +91,11 @@ constexpr uint32_t kPanelCols = 64, kPanelChunk = 2176, kPanelScales = 2048;
 struct WLaneOff {
   uint32_t codes, scale, shift;
 };
-__host__ __device__ __forceinline__ WLaneOff WLane(const GemmArgs& g, uint32_t col) {
+// `panels` is g.w_panels; kernels that know the layout at compile time pass
+// it as a constant (the other layout's arithmetic then disappears).
+__host__ __device__ __forceinline__ WLaneOff WLane(const GemmArgs& g, uint32_t col, bool panels) {
   WLaneOff o;
-  if (g.w_panels) {
+  if (panels) {
     const uint32_t base = (col / kPanelCols) * g.w_steps * kPanelChunk, c = col % kPanelCols;
     o.codes = base + c * 16;
     o.scale = base + kPanelScales + 4 * ((c % 32) / 2);
@@ -106,11 +108,20 @@ __host__ __device__ __forceinline__ WLaneOff WLane(const GemmArgs& g, uint32_t c
   }
   return o;
 }
+__host__ __device__ __forceinline__ WLaneOff WLane(const GemmArgs& g, uint32_t col) {
+  return WLane(g, col, g.w_panels != 0);
+}
+__host__ __device__ __forceinline__ uint32_t WBlockCodes(const GemmArgs& g, uint32_t blk, bool panels) {
+  return panels ? (blk / 2) * kPanelChunk + (blk % 2) * (kPanelCols * 16) : blk * kDdrWord;
+}
 __host__ __device__ __forceinline__ uint32_t WBlockCodes(const GemmArgs& g, uint32_t blk) {
-  return g.w_panels ? (blk / 2) * kPanelChunk + (blk % 2) * (kPanelCols * 16) : blk * kDdrWord;
+  return WBlockCodes(g, blk, g.w_panels != 0);
+}
+__host__ __device__ __forceinline__ uint32_t WBlockScale(const GemmArgs& g, uint32_t blk, bool panels) {
+  return panels ? (blk / 2) * kPanelChunk + (blk % 2) * kPanelCols : blk * kDdrWord;
 }
 __host__ __device__ __forceinline__ uint32_t WBlockScale(const GemmArgs& g, uint32_t blk) {
-  return g.w_panels ? (blk / 2) * kPanelChunk + (blk % 2) * kPanelCols : blk * kDdrWord;
+  return WBlockScale(g, blk, g.w_panels != 0);
 }
 // Bytes of one plane.
 inline uint64_t PanelBytes(uint32_t n, uint32_t kb_total) {

@@ -1,5 +1,6 @@
-// Skinny fast linear kernel for gfx950 (HB_LINEAR_FAST, at most 64 rows):
-// MXFP4 or W8 weights streamed from HBM straight into the matrix cores.
+// Skinny fast linear kernel for gfx950 (HB_LINEAR_FAST, a batch of layers of
+// at most 16 rows each): MXFP4 or W8 weights streamed from HBM straight into
+// the matrix cores.
 //
 // Matrix cores: v_mfma_scale_f32_16x16x128_f8f6f4.  One lane's A operand is
 // 32 values of one row and one K-block (lane l: row l % 16, block l / 16 of
@@ -8,7 +9,7 @@
 // 128-row fast kernel (A as FP6 planes hi/2, lo/2 with ea-1, ea-5; MXFP4 W
 // untouched; W8 W as FP6 planes with ew-1, ew-5, K in the W8 byte order).
 //
-// Work split: a workgroup holds every row (16 * kMT <= 64) and kCols
+// Work split: a workgroup holds every row (16 * kMT) and kCols
 // columns; its 8 waves take contiguous ranges of 4-block K chunks (split-K).
 // Each lane loads its own A bytes and W column-block (16 B per plane, the
 // WBUF word layout) into registers, converts, and issues the chunk's MFMAs;
@@ -136,7 +137,7 @@ struct RawS {
   uint32_t nib;  // 0x0F0F0F0F, or 0 for a block past the end (adds zero)
 };
 
-template <int kMT, bool kW8, bool kMulti>
+template <int kMT, bool kW8, bool kMulti, bool kPanels>
 __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void SkinnyKernel(GemmArgs g) {
   constexpr int kNT = NTiles<kMT, kW8>(), kCols = 16 * kNT, kWP = kW8 ? 2 : 1;
   constexpr int kRows = 16 * kMT, kOut = kRows * kCols;
@@ -171,10 +172,15 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
   // The lane's row within a quad (r16 % 4) and column within a group (r16 %
   // 8) are the same in every tile, so the scale dword's offset from the data
   // and the scale byte's position are per lane, not per tile.
-  // W: DDR words or panels (WLane); a column past the layer reads the last
-  // group's column at the same position (its outputs are not stored).
+  // W in DDR words: the scale dword's offset from the codes and the scale
+  // byte's position are per lane too (one register per column tile); in
+  // panels (WLane) they differ between the lane's column tiles.  A column
+  // past the layer reads the last group's column at the same position (its
+  // outputs are not stored).
   const uint32_t ashift = 8 * (r16 & 3), as_delta = 128 - (r16 & 3) * 32;
-  uint32_t a_off[kMT], w_off[kNT], ws_off[kNT], wshift[kNT];
+  const uint32_t cl = r16 & 7, wshift_ddr = 8 * (cl & 3), ws_delta = 128 + (cl & 4) - cl * 16;
+  uint32_t a_off[kMT], w_off[kNT];
+  [[maybe_unused]] uint32_t ws_off[kPanels ? kNT : 1], wshift[kPanels ? kNT : 1];
 #pragma unroll
   for (int mi = 0; mi < kMT; ++mi) {
     const uint32_t quad = min((mi * 16 + r16) >> 2, g.quads - 1);
@@ -182,13 +188,16 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
   }
 #pragma unroll
   for (int nj = 0; nj < kNT; ++nj) {
-    const uint32_t col = min((col0 + nj * 16 + r16) >> 3, g.groups - 1) * 8 + (r16 & 7);
-    const WLaneOff wo = WLane(g, col);
-    w_off[nj] = wo.codes;
-    ws_off[nj] = wo.scale;
-    wshift[nj] = wo.shift;
+    const uint32_t grp = min((col0 + nj * 16 + r16) >> 3, g.groups - 1);
+    if constexpr (kPanels) {
+      const WLaneOff wo = WLane(g, grp * 8 + cl);
+      w_off[nj] = wo.codes;
+      ws_off[nj] = wo.scale;
+      wshift[nj] = wo.shift;
+    } else {
+      w_off[nj] = grp * word_row + cl * 16;
+    }
   }
-  (void)word_row;
 
   // Loads of chunk ch (its lane's block); a chunk at or past c_end, or a
   // block past the end, reloads a valid block and adds zero.
@@ -197,7 +206,9 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
     const uint32_t idx = 4 * ch + kq;
     rw.nib = (ch < c_end && idx < nblocks) ? 0x0F0F0F0Fu : 0u;
     const uint32_t ublk = SkinnyBlockOf<kMulti>(g, min(idx, nblocks - 1));
-    const uint32_t blk = ublk * kDdrWord, wbc = WBlockCodes(g, ublk), wbs = WBlockScale(g, ublk);
+    const uint32_t blk = ublk * kDdrWord;
+    const uint32_t wbc = kPanels ? WBlockCodes(g, ublk) : blk;
+    const uint32_t wbs = kPanels ? WBlockScale(g, ublk) : blk;
 #pragma unroll
     for (int mi = 0; mi < kMT; ++mi) {
       const uint8_t* p = a + blk + a_off[mi];
@@ -215,10 +226,14 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
 #pragma unroll
       for (int pl = 0; pl < kWP; ++pl) {
         const uint8_t* wp = pl ? w1 : w0;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(wp + wbc + w_off[nj]);
+        const uint8_t* wc = wp + wbc + w_off[nj];
+        const u32x4 v = *reinterpret_cast<const u32x4*>(wc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) rw.w[nj][pl][i] = v[i];
-        rw.sw[nj][pl] = *reinterpret_cast<const uint32_t*>(wp + wbs + ws_off[nj]);
+        // (DDR words: the scale as an offset from the codes' address, so no
+        // per-tile sum stays live across the K loop)
+        rw.sw[nj][pl] = *reinterpret_cast<const uint32_t*>(
+            kPanels ? wp + wbs + ws_off[kPanels ? nj : 0] : wc + ws_delta);
       }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -235,10 +250,11 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
     uint32_t sb[kNT];
 #pragma unroll
     for (int nj = 0; nj < kNT; ++nj) {
-      const uint32_t ewh = __builtin_amdgcn_ubfe(rw.sw[nj][0], wshift[nj], 8);
+      const uint32_t sh = kPanels ? wshift[kPanels ? nj : 0] : wshift_ddr;
+      const uint32_t ewh = __builtin_amdgcn_ubfe(rw.sw[nj][0], sh, 8);
       unsafe |= ewh - kSafeLo > kSafeHi - kSafeLo;
       if constexpr (kW8) {
-        const uint32_t ewl = __builtin_amdgcn_ubfe(rw.sw[nj][1], wshift[nj], 8);
+        const uint32_t ewl = __builtin_amdgcn_ubfe(rw.sw[nj][1], sh, 8);
         unsafe |= ewl - kSafeLo > kSafeHi - kSafeLo;
         sb[nj] = (ewh - 1u) | ((ewl - 5u) << 8);
 #pragma unroll
@@ -319,7 +335,7 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
     if (in) {
       const uint32_t init = (g.acc && row < g.m) ? c[(size_t)row * g.n + col] : 0u;
       if (slow) {
-        y = SlowLinear(g, a, w0, w1, init, row, col);
+        y = SlowLinear<kPanels ? 2 : 1>(g, a, w0, w1, init, row, col);
       } else {
         float s = __uint_as_float(init);
 #pragma unroll
@@ -632,8 +648,12 @@ void LaunchS(const GemmArgs& in, uint32_t batch, hipStream_t stream) {
   args.gx = (args.groups * 8 + kCols - 1) / kCols;
   args.gy = 1;
   args.gz = batch;
-  hipLaunchKernelGGL((SkinnyKernel<kMT, kW8, kMulti>), dim3(args.gx * args.gz), dim3(kWaves * 64),
-                     0, stream, args);
+  if (args.w_panels)
+    hipLaunchKernelGGL((SkinnyKernel<kMT, kW8, kMulti, true>), dim3(args.gx * args.gz),
+                       dim3(kWaves * 64), 0, stream, args);
+  else
+    hipLaunchKernelGGL((SkinnyKernel<kMT, kW8, kMulti, false>), dim3(args.gx * args.gz),
+                       dim3(kWaves * 64), 0, stream, args);
 }
 
 template <int kMT>
@@ -689,10 +709,10 @@ hipError_t LaunchSplitLinear(const GemmArgs& args, hipStream_t stream) {
 }
 
 hipError_t LaunchLinearSkinny(const GemmArgs& args, uint32_t batch, hipStream_t stream) {
-  const uint32_t rows = args.quads * 4;
-  if (rows <= 16) LaunchRowsS<1>(args, batch, stream);
-  else if (rows <= 32) LaunchRowsS<2>(args, batch, stream);
-  else LaunchRowsS<4>(args, batch, stream);
+  // (layers of up to 16 rows in a batch; one layer of up to kSplitMaxRows
+  // rows runs as a split launch instead)
+  if (args.quads * 4 > 16) return hipErrorInvalidValue;
+  LaunchRowsS<1>(args, batch, stream);
   return hipGetLastError();
 }
 

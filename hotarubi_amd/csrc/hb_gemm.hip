@@ -720,9 +720,6 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   // Fast mode runs MXFP4 and W8 (hi, lo) on the block-scaled matrix cores;
   // any other plane list runs exactly (which meets the fast-mode tolerance).
   const bool fastk = fast && FastEligible(args);
-  // Split-K over the waves of one workgroup pays where a workgroup can hold
-  // every row and still many columns: up to 16 rows, or a single MXFP4 layer
-  // of up to 64 rows (which otherwise needs K splits and a second launch).
   // A single small layer: one launch, K split over workgroups (the last
   // split of each tile finishes it).  Workspace: the counters, then the
   // partial sums.

@@ -6,8 +6,10 @@ panels against the oracle's layer over the same weights as DDR words
 343-395): exact mode bitwise, fast mode within the fast-mode tolerance, on
 every kernel route that reads panels (the panel streaming kernel batched and
 persistent, a partial last panel and odd block counts, from C, out-of-window
-scale bytes; the skinny kernel; the 128-row tile kernel and the K-split path
-with ops, requantize and W8 planes; the exact tile kernel)."""
+scale bytes; the skinny kernel for batches of up to 16 rows; the single-launch
+split kernel for one layer of up to 160 rows, with ops, requantize and W8
+planes; the 128-row tile kernel and its K-split path; the exact tile
+kernel)."""
 from __future__ import annotations
 
 import numpy as np
@@ -103,13 +105,15 @@ def test_w8_ops_requantize(gpu, mode):
                  quantize=True, tbuf=helpers.activation_table("gelu"), seed=509, panels=True)
 
 
+@pytest.mark.parametrize("m", [141, 200])
 @pytest.mark.parametrize("mode", [hb.FAST, hb.EXACT])
-def test_small_layer_split_with_ops(gpu, mode):
-    """141 rows (a few tiles): the K-split path and its epilogue kernel in
-    fast mode, the deferred exact epilogue in exact mode."""
-    single_layer(gpu, 141, 320, 30, False, mode,
+def test_small_layer_split_with_ops(gpu, mode, m):
+    """One small layer with the residual ADD: at 141 rows the single-launch
+    split kernel (fast), at 200 rows the 128-row tile kernel's K splits and
+    the epilogue kernel (fast); the deferred exact epilogue in exact mode."""
+    single_layer(gpu, m, 320, 30, False, mode,
                  lambda r, m, n: [(hb.EP_ADD, helpers.random_fp32_words(r, (m, n), 118, 128))],
-                 seed=510, panels=True)
+                 seed=510 + m, panels=True)
 
 
 @pytest.mark.parametrize("mode", [hb.FAST, hb.EXACT])

@@ -242,8 +242,9 @@ class Chain:
     with E8M0 exponents in [lo, hi]; W8 weights are two nibble planes of
     random codes sharing the scale byte 133 (MXINT8 of int8 values)."""
 
-    def __init__(self, hb, torch, m, mode, seed):
+    def __init__(self, hb, torch, m, mode, seed, w8_panels=False):
         self.hb, self.torch, self.m, self.mode = hb, torch, m, mode
+        self.w8_panels = w8_panels  # W8 layers over W8 panels (packed once, here)
         self.dev = "cuda:0"
         self.g = torch.Generator(device=self.dev).manual_seed(seed)
         self.quads = (m + 3) // 4
@@ -288,8 +289,16 @@ class Chain:
 
     def add(self, n, kb, a, planes, c, ops=(), q=None, onto=False, tbuf=None):
         modes = [1, 2] if len(planes) == 2 else [0]
+        w8p = self.w8_panels and len(planes) == 2
+        if w8p:
+            pan = self.torch.empty((self.hb.w8_panel_bytes(n, kb),), dtype=self.torch.uint8,
+                                   device=self.dev)
+            self.hb.pack_w8(planes[0], planes[1], n, kb, pan)
+            self.keep.append(pan)
+            planes = [pan, pan]
         self.descs.append(self.hb.linear_desc(self.m, n, kb, a, planes, modes, c, ops=ops,
-                                              tbuf=tbuf, q_out=q, onto=onto, mode=self.mode))
+                                              tbuf=tbuf, q_out=q, onto=onto, mode=self.mode,
+                                              w8_panels=w8p))
         self.ops += 2.0 * self.m * n * kb * 32
         vectors = sum(1 for k, _ in ops if k in (self.hb.EP_ADDP, self.hb.EP_MULP))
         out = self.m * n * (1 + 1 / 32) if q is not None else 4 * self.m * n
@@ -675,8 +684,8 @@ class SiglipSet(Chain):
 
     M, D, QKV, FF, LAYERS = 2048, 768, 2304, 3072, 12
 
-    def __init__(self, hb, torch, mode):
-        super().__init__(hb, torch, self.M, mode, 21)
+    def __init__(self, hb, torch, mode, w8_panels=False):
+        super().__init__(hb, torch, self.M, mode, 21, w8_panels)
         tb = self.table("gelu")
         kb, kbf = self.D // 32, self.FF // 32
 
@@ -968,12 +977,15 @@ def main():
             del wk
         out["w8"] = w8
 
-        # SigLIP-style W8 encoder set (12 layers x 4 GEMMs, M=2048) and the
-        # SparseDrive-S stage-1 3x3 im2col GEMM (MXFP4), fast and exact
+        # SigLIP-style W8 encoder set (12 layers x 4 GEMMs, M=2048; fast mode
+        # over W8 panels, the weights' layout for large-M W8 layers, exact
+        # mode over DDR words) and the SparseDrive-S stage-1 3x3 im2col GEMM
+        # (MXFP4), fast and exact
         for key, desc, cls_fast, make in (
                 ("siglip_w8_set", "W8 SigLIP-style encoder: 12 layers x {QKV 768->2304, out "
                  "768->768, up 768->3072 + GELU + requantize, down 3072->768}, M=2048, "
-                 "MULP + ADDP", "int8", lambda md: SiglipSet(hb, torch, md)),
+                 "MULP + ADDP; fast: W8 panels, exact: DDR words", "int8",
+                 lambda md: SiglipSet(hb, torch, md, w8_panels=md == hb.FAST)),
                 ("sparsedrive_stage1_conv_mxfp4", "MXFP4 im2col GEMM M=67584 K=576 N=64 "
                  "(SparseDrive-S stage-1 3x3 conv, 6 cameras)", "fp6_fp4",
                  lambda md: SparseDriveConv(hb, torch, md))):
@@ -984,6 +996,13 @@ def main():
                 tops, roof = chain_summary(wk, t["eager_ms"], cls)
                 rec[name] = {"value": tops, "unit": "TOPS", "ms_per_pass": t["eager_ms"],
                              "gemms": t["gemms"], "m": t["m"], "roofline": roof}
+                del wk
+            if key == "siglip_w8_set":  # the fast set over DDR words, for comparison
+                wk = SiglipSet(hb, torch, hb.FAST)
+                t = time_chain(torch, ctx, wk, steps=5, graph=False)
+                tops, roof = chain_summary(wk, t["eager_ms"], cls_fast)
+                rec["fast_ddr_words"] = {"value": tops, "unit": "TOPS", "ms_per_pass": t["eager_ms"],
+                                         "roofline": roof}
                 del wk
             rec["workload"] = desc
             out[key] = rec

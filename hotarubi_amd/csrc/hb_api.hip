@@ -496,18 +496,30 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g, bool* mixed) {
     if (PieceShift(*d, p) != PieceShift(*d, 0)) *mixed = true;
   }
   const bool panels = (d->flags & HB_LINEAR_PANELS) != 0;
-  const uint64_t w_bytes =
-      panels ? hb::PanelBytes(d->n, d->kb_total) : (uint64_t)(d->n / 8) * d->kb_total * hb::kDdrWord;
+  const bool w8p = (d->flags & HB_LINEAR_W8_PANELS) != 0;
+  const uint64_t w_bytes = w8p ? hb::W8PanelBytes(d->n, d->kb_total)
+                           : panels ? hb::PanelBytes(d->n, d->kb_total)
+                                    : (uint64_t)(d->n / 8) * d->kb_total * hb::kDdrWord;
   if (a_end * hb::kDdrWord > (1ull << 32) || w_bytes > (1ull << 32))
     return Fail(HB_EINVAL, "A or W spans more than 4 GiB");
   if (!d->a || !d->c) return Fail(HB_EINVAL, "null A or C");
   if (d->n_ops > HB_MAX_EP_OPS) return Fail(HB_EINVAL, "n_ops = %u", d->n_ops);
   if (d->q_out && d->n % 32 != 0) return Fail(HB_EINVAL, "quantized output needs n %% 32 == 0");
-  if (d->flags & ~(uint32_t)(HB_LINEAR_FAST | HB_LINEAR_PANELS))
+  if (d->flags & ~(uint32_t)(HB_LINEAR_FAST | HB_LINEAR_PANELS | HB_LINEAR_W8_PANELS) ||
+      (panels && w8p))
     return Fail(HB_EINVAL, "flags = %u", d->flags);
   for (uint32_t l = 0; panels && l < d->n_planes; ++l)
     if (reinterpret_cast<uintptr_t>(d->w[l]) % 16 != 0)
       return Fail(HB_EINVAL, "weight panels must be 16-byte aligned");
+  if (w8p) {
+    if (d->n_planes != 2 || d->modes[0] != 1 || d->modes[1] != 2 || d->w[1] != d->w[0])
+      return Fail(HB_EINVAL, "W8 panels: planes {W8_HI, W8_LO} with w[0] == w[1]");
+    if (reinterpret_cast<uintptr_t>(d->w[0]) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(d->a) % 16 != 0)
+      return Fail(HB_EINVAL, "W8 panels: A and the panels must be 16-byte aligned");
+    if (d->n_pieces != 1 || d->pieces[0].kb_offset != 0 || d->pieces[0].kb != d->kb_total)
+      return Fail(HB_EUNSUPPORTED, "W8 panels take one piece over every block");
+  }
   std::memset(g, 0, sizeof *g);
   for (uint32_t o = 0; o < d->n_ops; ++o) {
     const hb_ep_op& op = d->ops[o];
@@ -555,6 +567,7 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g, bool* mixed) {
   g->modes[1] = d->n_planes > 1 ? d->modes[1] : d->modes[0];
   g->total_steps = (uint32_t)steps;
   g->w_panels = panels ? 1u : 0u;
+  g->w_fp6 = w8p ? 1u : 0u;
   g->w_steps = (d->kb_total + 1) / 2;
   g->acc = d->onto ? 1u : 0u;
   g->tbuf = d->tbuf;
@@ -611,6 +624,8 @@ int LinearBatched(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count,
       }
       if (!same) return Fail(HB_EINVAL, "layer %u differs in shape, schedule, ops or stride", i);
     }
+    if (g.w_fp6 && (g.a_batch % 16 != 0 || g.w_batch % 16 != 0))
+      return Fail(HB_EINVAL, "W8 panels: layers' A and panels must be 16-byte aligned");
   }
   if (mixed) return LinearChain(ctx, d, count, fixed);
   hipError_t err = hb::LaunchLinear(g, count, (d[0].flags & HB_LINEAR_FAST) != 0, ctx->ws,
@@ -923,6 +938,50 @@ int hb_pack_weights(hb_ctx* ctx, const void* w, uint32_t n, uint32_t kb_total, v
 
 int hb_unpack_weights(hb_ctx* ctx, const void* panels, uint32_t n, uint32_t kb_total, void* w) {
   return PanelConvert(ctx, panels, n, kb_total, w, false);
+}
+
+uint64_t hb_w8_panel_bytes(uint32_t n, uint32_t kb_total) {
+  if (n < 8 || n % 8 != 0 || kb_total < 1) return 0;
+  return hb::W8PanelBytes(n, kb_total);
+}
+
+namespace {
+int W8Convert(hb_ctx* ctx, const void* hi, const void* lo, uint32_t n, uint32_t kb_total,
+              const void* in_panels, void* out_panels, void* out_hi, void* out_lo) {
+  if (int rc = Enter(ctx)) return rc;
+  const bool pack = out_panels != nullptr;
+  const void* bufs[3] = {pack ? hi : in_panels, pack ? lo : out_hi, pack ? out_panels : out_lo};
+  for (const void* b : bufs) {
+    if (!b) return Fail(HB_EINVAL, "null weights");
+    if (reinterpret_cast<uintptr_t>(b) % 16 != 0)
+      return Fail(HB_EINVAL, "weights must be 16-byte aligned");
+  }
+  if (n < 8 || n % 8 != 0 || kb_total < 1)
+    return Fail(HB_EINVAL, "weights n = %u, kb_total = %u: need n %% 8 == 0, kb_total >= 1", n,
+                kb_total);
+  if (hb::W8PanelBytes(n, kb_total) > (1ull << 32))
+    return Fail(HB_EINVAL, "W8 panels of more than 4 GiB");
+  const hipError_t err =
+      pack ? hb::LaunchPackW8(static_cast<const uint8_t*>(hi), static_cast<const uint8_t*>(lo),
+                              n, kb_total, static_cast<uint8_t*>(out_panels), ctx->stream)
+           : hb::LaunchUnpackW8(static_cast<const uint8_t*>(in_panels), n, kb_total,
+                                static_cast<uint8_t*>(out_hi), static_cast<uint8_t*>(out_lo),
+                                ctx->stream);
+  if (err != hipSuccess) return HipFail(err, pack ? "W8 pack launch" : "W8 unpack launch");
+  HB_HIP(hipStreamSynchronize(ctx->stream));
+  return HB_OK;
+}
+}  // namespace
+
+int hb_pack_w8(hb_ctx* ctx, const void* w_hi, const void* w_lo, uint32_t n, uint32_t kb_total,
+               void* panels) {
+  return W8Convert(ctx, w_hi, w_lo, n, kb_total, nullptr, panels, nullptr, nullptr);
+}
+
+int hb_unpack_w8(hb_ctx* ctx, const void* panels, uint32_t n, uint32_t kb_total, void* w_hi,
+                 void* w_lo) {
+  if (!panels) return Fail(HB_EINVAL, "null weights");
+  return W8Convert(ctx, nullptr, nullptr, n, kb_total, panels, nullptr, w_hi, w_lo);
 }
 
 int hb_encode_mxint8(hb_ctx* ctx, const float* x, uint32_t rows, uint32_t cols, void* out) {

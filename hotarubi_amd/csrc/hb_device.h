@@ -113,16 +113,17 @@ __device__ __forceinline__ uint32_t EpApply(uint32_t kind, uint32_t imm, uint32_
 // results are +0 as there.  The table interpolation v + s * (frac / 2^16)
 // is one correctly rounded product (frac / 2^16 is exact) and one add, as
 // in the exact path.
+// (Branch-free: the index is computed for every exponent and always lies in
+// the table; exponents from 131 on then take 1.0.)
 __device__ __forceinline__ float ActivationFast(float prod, const uint64_t* t) {
   const uint32_t bits = __float_as_uint(prod), e = ExpField(bits);
-  if (e >= 131u) return 1.0f;
   const uint32_t sig = Significand(bits);
-  uint32_t fixed = 0;
-  if (e == 130u) fixed = sig << 1;
-  else if (e >= 105u) fixed = sig >> (129u - e);
+  const uint32_t sh = e >= 105u && e <= 129u ? 129u - e : 31u;
+  const uint32_t fixed = e == 130u ? sig << 1 : e < 105u || e > 130u ? 0u : sig >> sh;
   const uint64_t entry = t[fixed >> 16];
-  return __uint_as_float((uint32_t)entry) +
-         __uint_as_float((uint32_t)(entry >> 32)) * ((float)(fixed & 0xFFFFu) * (1.0f / 65536.0f));
+  const float v = __uint_as_float((uint32_t)entry) +
+                  __uint_as_float((uint32_t)(entry >> 32)) * ((float)(fixed & 0xFFFFu) * (1.0f / 65536.0f));
+  return e >= 131u ? 1.0f : v;
 }
 
 __device__ __forceinline__ float ActGateFast(float x, const uint64_t* t) {
@@ -149,12 +150,16 @@ __device__ __forceinline__ float EpApplyFast(uint32_t kind, uint32_t imm, float 
   }
 }
 
-// EpApplyFast over 16 values (one MFMA tile of a lane): the kind is
-// resolved once, each case is a straight run.  x2 holds the op's [m][n]
-// operand, p the column's vector value.
+// EpApplyFast over 16 values of a lane: the kind is resolved once, each
+// case is a straight run.  x2 holds the op's [m][n] operand, p the vector
+// value of each element's column (P = float: one column for all 16; P =
+// f32x16_t: one per element).  kSerial keeps the 16 table lookups of an
+// activation from all being in flight at once (for callers short of
+// registers); otherwise their latencies overlap.
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+template <bool kSerial = true, typename P>
 __device__ __forceinline__ void EpApplyFast16(uint32_t kind, uint32_t imm, f32x16_t& y,
-                                              const f32x16_t& x2, float p, const uint64_t* t) {
+                                              const f32x16_t& x2, const P& p, const uint64_t* t) {
   switch (kind) {
     case kEpAddP: y = (y + p) + 0.0f; break;
     case kEpMulP: y = (y + 0.0f) * p + 0.0f; break;
@@ -168,20 +173,18 @@ __device__ __forceinline__ void EpApplyFast16(uint32_t kind, uint32_t imm, f32x1
         y[r] = (prod > 0.0f ? prod : 0.0f) + 0.0f;
       }
       break;
-    // (the fences keep the 16 table lookups from all being in flight at
-    // once, which would cost registers the caller needs)
     case kEpAct:
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         y[r] = ActGateFast(y[r], t);
-        __builtin_amdgcn_sched_barrier(0);
+        if (kSerial) __builtin_amdgcn_sched_barrier(0);
       }
       break;
     case kEpActMul:
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         y[r] = (ActGateFast(y[r], t) + 0.0f) * x2[r] + 0.0f;
-        __builtin_amdgcn_sched_barrier(0);
+        if (kSerial) __builtin_amdgcn_sched_barrier(0);
       }
       break;
     default: break;
@@ -192,15 +195,39 @@ __device__ __forceinline__ void EpApplyFast16(uint32_t kind, uint32_t imm, f32x1
 // emax = largest exponent field (0 -> scale byte 127).
 __device__ __forceinline__ uint32_t ScaleByteOf(uint32_t emax) { return emax == 0 ? 127u : emax; }
 
+// Block blk of column col, plane l of W8 panels (w: the panels): the dot
+// product of the 32 int8 codes at a32 with the plane's nibble values (each
+// decoded from its FP6 code v / 2), and the plane's scale byte.
+typedef uint32_t W8Codes __attribute__((ext_vector_type(6)));
+typedef _Float16 W8Halves __attribute__((ext_vector_type(32)));
+__device__ __forceinline__ int32_t W8PanelDot(const GemmArgs& g, const uint8_t* w, uint32_t col,
+                                              uint32_t blk, uint32_t l, const uint8_t* a32,
+                                              uint32_t* wscale) {
+  const uint32_t cc = col % kPanelCols, b = blk % 2, i = (b * 2 + l) * kPanelCols + cc;
+  const uint8_t* chunk = w + ((size_t)(col / kPanelCols) * g.w_steps + blk / 2) * kW8Chunk;
+  const uint4 d0 = *reinterpret_cast<const uint4*>(chunk + i * 16);
+  const uint2 d1 = *reinterpret_cast<const uint2*>(chunk + kW8Part8 + i * 8);
+  const W8Codes codes = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y};
+  const W8Halves v = __builtin_amdgcn_cvt_scalef32_pk32_f16_fp6(codes, 1.0f);
+  *wscale = (chunk[kW8Scales + (b * 32 + cc % 32) * 4 + 2 * (cc / 32) + l] + (l ? 5u : 1u)) & 0xFFu;
+  int32_t sum = 0;
+#pragma unroll
+  for (int k = 0; k < 32; ++k)
+    sum += (int32_t)(int8_t)a32[k] * (int32_t)(float)(v[k] * (_Float16)2.0f);
+  return sum;
+}
+
 // Exact recomputation of one output of a linear layer over DDR words (the
 // NPU's ordered fold, tools/iss/gemm_array.cpp:123-147 as emitted per
 // tools/compiler/kernels.cpp:343-395: pieces, then planes, then blocks),
 // starting from acc.
-// kLayout: 0 reads g.w_panels, 1 DDR words, 2 panels (known to the caller).
+// kLayout: 0 reads g.w_panels and g.w_fp6, 1 DDR words, 2 panels, 3 W8
+// panels (known to the caller).
 template <int kLayout = 0>
 __device__ __forceinline__ uint32_t SlowLinear(const GemmArgs& g, const uint8_t* a,
                                                const uint8_t* w0, const uint8_t* w1, uint32_t acc,
                                                uint32_t row, uint32_t col) {
+  const bool fp6 = kLayout == 0 ? g.w_fp6 != 0 : kLayout == 3;
   const bool panels = kLayout == 0 ? g.w_panels != 0 : kLayout == 2;
   const uint32_t quad = row >> 2, t = row & 3;
   const WLaneOff wo = WLane(g, col, panels);
@@ -210,6 +237,12 @@ __device__ __forceinline__ uint32_t SlowLinear(const GemmArgs& g, const uint8_t*
         const uint32_t blk = g.piece_off[p] + b, mode = g.modes[l];
         const uint8_t* aw = a + ((size_t)quad * g.a_row + blk) * kDdrWord;
         const uint8_t* wp = l ? w1 : w0;
+        if (fp6) {
+          uint32_t ws = 0;
+          const int32_t dot = W8PanelDot(g, wp, col, blk, l, aw + t * 32, &ws);
+          acc = AddBits(acc, BlockValue(dot, aw[128 + t], ws, mode));
+          continue;
+        }
         const uint8_t* codes;
         uint32_t wscale;
         if (panels) {

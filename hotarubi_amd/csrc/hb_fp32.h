@@ -127,20 +127,21 @@ HB_HD uint32_t BlockValue(int32_t sum, uint32_t a_scale, uint32_t w_scale, uint3
 }
 
 // ---- VEC requantize (tools/iss/lane.cpp:384-404) ----
+// The reference's steps without branches: its shift is at least 17 (the
+// element's exponent is at most the block's), and from 25 on it takes the
+// magnitude as 0, which the same rounding arithmetic gives with the shift
+// held at 31 (the significand has 24 bits); a zero significand rounds to 0.
 HB_HD uint8_t QuantizeElement(uint32_t value, uint32_t emax) {
-  const uint32_t e = ExpField(value);
   const uint32_t sig = Significand(value);
-  if (sig == 0) return 0;
-  const uint32_t shift = emax - e + 17;
-  uint32_t mag = 0;
-  if (shift < 25) {
-    const uint32_t integer = sig >> shift;
-    const bool guard = ((sig >> (shift - 1)) & 1u) != 0;
-    const bool sticky = (sig & ((1u << (shift - 1)) - 1u)) != 0;
-    mag = integer + ((guard && (sticky || (integer & 1u))) ? 1u : 0u);
-  }
-  if (value >> 31) return mag >= 128 ? 0x80 : (uint8_t)((256u - mag) & 0xFFu);
-  return mag >= 128 ? 0x7F : (uint8_t)mag;
+  const uint32_t shift = emax - ExpField(value) + 17;
+  const uint32_t s = shift < 31u ? shift : 31u;
+  const uint32_t integer = sig >> s;
+  const uint32_t guard = (sig >> (s - 1)) & 1u;
+  const uint32_t sticky = (sig & ((1u << (s - 1)) - 1u)) != 0 ? 1u : 0u;
+  const uint32_t mag = integer + (guard & (sticky | (integer & 1u)));
+  const uint32_t pos = mag >= 128 ? 0x7Fu : mag;
+  const uint32_t neg = mag >= 128 ? 0x80u : ((256u - mag) & 0xFFu);
+  return (uint8_t)((value >> 31) ? neg : pos);
 }
 
 // ---- host encoder (tools/runtime/formats.cpp:35-56) ----

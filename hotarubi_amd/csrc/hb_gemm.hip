@@ -713,6 +713,8 @@ void FreeWorkspace(Workspace& ws) {
 
 hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace& ws,
                         hipStream_t stream, FixedScratch* fixed) {
+  // W8 panels: their own kernel, every shape and mode.
+  if (in.w_fp6) return LaunchW8Linear(in, batch, fast, stream);
   GemmArgs args = in;
   args.ws = nullptr;
   args.splits = 1;

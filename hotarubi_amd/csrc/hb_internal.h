@@ -71,6 +71,9 @@ struct GemmArgs {
   // W planes in the panel layout (HB_LINEAR_PANELS) instead of DDR words;
   // w_steps = ceil(kb_total / 2), the steps of a panel
   uint32_t w_panels, w_steps;
+  // W8 layer over FP6 W8 panels (HB_LINEAR_W8_PANELS): w[0] = w[1] = the
+  // panels of both planes
+  uint32_t w_fp6;
 };
 
 // Weight panels (hb_pack_weights): one plane of n columns x kb_total
@@ -126,6 +129,29 @@ __host__ __device__ __forceinline__ uint32_t WBlockScale(const GemmArgs& g, uint
 // Bytes of one plane.
 inline uint64_t PanelBytes(uint32_t n, uint32_t kb_total) {
   return (uint64_t)((n + kPanelCols - 1) / kPanelCols) * ((kb_total + 1) / 2) * kPanelChunk;
+}
+
+// W8 panels (hb_pack_w8): both nibble planes of a W8 layer as the matrix
+// cores' B operands, FP6 E2M3 codes of v / 2 for each nibble value v (hi
+// plane -8..7, lo plane 0..15), 32 codes (a column's block) in 6 dwords as
+// v_cvt_scalef32_pk32_fp6_f16 packs them.  Panel p of 64 columns is
+// ceil(kb_total / 2) chunks of kW8Chunk bytes, chunk (p, s) at
+// (p * steps + s) * kW8Chunk holding blocks 2s + b, b = 0, 1; with
+// i = (b * 2 + l) * 64 + c for plane l (0 hi, 1 lo) and column 64p + c:
+//   i * 16:              dwords 0..3 of the column-block's codes;
+//   kW8Part8 + i * 8:    dwords 4..5;
+//   kW8Scales + (b * 32 + c % 32) * 4 + 2 (c / 32) + l: its scale byte
+//                        minus 1 (hi) or 5 (lo), modulo 256.
+// Columns past n and blocks past kb_total are zero codes with scale 127.
+// After the chunks, one dword per panel, at W8FlagsOffset: nonzero when a
+// scale byte of the panel is outside [70, 179] (the fast path's window).
+constexpr uint32_t kW8Chunk = 6400, kW8Part8 = 4096, kW8Scales = 6144;
+inline uint64_t W8FlagsOffset(uint32_t n, uint32_t kb_total) {
+  return (uint64_t)((n + kPanelCols - 1) / kPanelCols) * ((kb_total + 1) / 2) * kW8Chunk;
+}
+inline uint64_t W8PanelBytes(uint32_t n, uint32_t kb_total) {
+  const uint64_t flags = (uint64_t)((n + kPanelCols - 1) / kPanelCols) * 4;
+  return W8FlagsOffset(n, kb_total) + (flags + 15) / 16 * 16;
 }
 
 // Byte size of the deferred-epilogue workspace of `args` (sums and flags).
@@ -214,6 +240,14 @@ hipError_t LaunchPanel(const GemmArgs& args, uint32_t batch, hipStream_t stream)
 // Streaming kernel over weight panels with a global-to-LDS ring (hb_stream.hip).
 bool StreamEligible(const GemmArgs& args);
 hipError_t LaunchStream(const GemmArgs& args, uint32_t batch, hipStream_t stream);
+// W8 layers over FP6 W8 panels (hb_w8.hip): every shape, both modes (exact
+// mode folds each output exactly).
+hipError_t LaunchW8Linear(const GemmArgs& args, uint32_t batch, bool fast, hipStream_t stream);
+// The W8 DDR planes (hi, lo) <-> W8 panels (hb_w8.hip).
+hipError_t LaunchPackW8(const uint8_t* hi, const uint8_t* lo, uint32_t n, uint32_t kb_total,
+                        uint8_t* out, hipStream_t stream);
+hipError_t LaunchUnpackW8(const uint8_t* in, uint32_t n, uint32_t kb_total, uint8_t* hi,
+                          uint8_t* lo, hipStream_t stream);
 // DDR words <-> panels of one plane (hb_panel.hip).
 hipError_t LaunchPackPanels(const uint8_t* w, uint32_t n, uint32_t kb_total, uint8_t* out,
                             hipStream_t stream);

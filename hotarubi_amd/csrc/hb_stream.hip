@@ -36,16 +36,16 @@
 
 #include "hb_device.h"
 #include "hb_internal.h"
+#include "hb_ring.h"
 
 namespace hb {
 namespace {
 
+using namespace ring;
+
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x6 __attribute__((ext_vector_type(6)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x32 __attribute__((ext_vector_type(32)));
 
 constexpr int kWaves = 4;                              // one per SIMD
 constexpr int kBM = 32 * kWaves;                       // tile rows
@@ -68,62 +68,6 @@ constexpr uint32_t kSafeLo = 70, kSafeHi = 179;
 static_assert(kAPieces % 64 == 0 && (kALoads + kWLoads) % kWaves == 0, "piece table");
 static_assert(kD * kOps < 64, "load counter range");
 static_assert(kSlot % 16 == 0, "16-byte slots");
-
-template <typename Fn, int... kI>
-__device__ __forceinline__ void UnrollImpl(Fn&& f, std::integer_sequence<int, kI...>) {
-  (f(std::integral_constant<int, kI>{}), ...);
-}
-template <int kN, typename Fn>
-__device__ __forceinline__ void Unroll(Fn&& f) {
-  UnrollImpl(f, std::make_integer_sequence<int, kN>{});
-}
-
-// Direct load into LDS: lane l's 16 bytes at base + voff land at LDS byte
-// lds + 16 l.  lds is wave-uniform (M0).
-// (base and lds are made wave-uniform values in scalar registers.)
-__device__ __forceinline__ uint64_t UniformAddress(const uint8_t* p) {
-  // (the builtin returns int: widen through uint32_t, not by sign extension)
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (hi << 32) | lo;
-}
-__device__ __forceinline__ void Dma16(const uint8_t* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(voff), "s"(UniformAddress(base)), "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
-}
-// Wait until at most kN of this wave's vector memory operations are
-// outstanding (s_waitcnt vmcnt(kN), the other counters left alone).
-template <int kN>
-__device__ __forceinline__ void WaitVm() {
-  __builtin_amdgcn_s_waitcnt((kN & 15) | ((kN >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-__device__ __forceinline__ void WaitLds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
-
-// 32 int8 (8 dwords, K order) -> FP6 E2M3 codes of h = q/32 rounded and of
-// (q - 32h)/2, both exact (hb_fast4.hip).
-__device__ __forceinline__ void SplitA(const uint32_t* x, uint32_t mask, u32x6& h6, u32x6& r6) {
-  const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-  f16x32 q;
-#pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    const uint32_t u = (x[d] & mask) ^ 0x80808080u;
-    const f16x2 p0 =
-        __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
-    const f16x2 p1 =
-        __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
-    q[4 * d] = p0[0];
-    q[4 * d + 1] = p0[1];
-    q[4 * d + 2] = p1[0];
-    q[4 * d + 3] = p1[1];
-  }
-  h6 = __builtin_amdgcn_cvt_scalef32_pk32_fp6_f16(q, 32.0f);
-  const f16x32 hv = __builtin_amdgcn_cvt_scalef32_pk32_f16_fp6(h6, 1.0f);
-  const f16x32 m32 = (_Float16)-32.0f;
-  const f16x32 r = __builtin_elementwise_fma(hv, m32, q);
-  r6 = __builtin_amdgcn_cvt_scalef32_pk32_fp6_f16(r, 2.0f);
-}
 
 struct Schedule {
   uint32_t first, stride, count;

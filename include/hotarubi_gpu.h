@@ -205,8 +205,10 @@ typedef struct hb_ep_op {
 } hb_ep_op;
 
 /* flags: HB_LINEAR_EXACT or HB_LINEAR_FAST, optionally | HB_LINEAR_PANELS
- * (the W planes are weight panels from hb_pack_weights, not DDR words). */
-enum { HB_LINEAR_EXACT = 0, HB_LINEAR_FAST = 1, HB_LINEAR_PANELS = 2 };
+ * (the W planes are weight panels from hb_pack_weights, not DDR words) or
+ * | HB_LINEAR_W8_PANELS (a W8 layer's planes are W8 panels from hb_pack_w8;
+ * w[0] and w[1] both point at them). */
+enum { HB_LINEAR_EXACT = 0, HB_LINEAR_FAST = 1, HB_LINEAR_PANELS = 2, HB_LINEAR_W8_PANELS = 4 };
 enum { HB_MAX_PIECES = 16, HB_MAX_EP_OPS = 8 };
 
 /* C = A x W^T as the emitted instruction sequence computes it:
@@ -246,7 +248,10 @@ typedef struct hb_linear_desc {
    * blocks of |block value| (+ one rounding of each epilogue op), and on
    * N(0,1) activations per output row max |fast - exact| <= 1e-5 *
    * max |exact|.  Tiles whose scale bytes leave the fast path's range are
-   * computed exactly.  | HB_LINEAR_PANELS: w[] are weight panels. */
+   * computed exactly.  | HB_LINEAR_PANELS: w[] are weight panels.
+   * | HB_LINEAR_W8_PANELS: w[0] = w[1] = W8 panels (one piece over every
+   * block; a, w 16-byte aligned); exact mode then folds each output on its
+   * own, correct but slow: use DDR words for exact work. */
   uint32_t flags;
   /* 0: A is [ceil(m/4)][kb_total] words.  Otherwise A words per quad, and
    * each piece's blocks start at its a_word (see hb_piece); every A word a
@@ -313,6 +318,39 @@ int hb_linear_noalloc_async(hb_ctx* ctx, const hb_linear_desc* descs, uint32_t c
 uint64_t hb_panel_bytes(uint32_t n, uint32_t kb_total);
 int hb_pack_weights(hb_ctx* ctx, const void* w, uint32_t n, uint32_t kb_total, void* panels);
 int hb_unpack_weights(hb_ctx* ctx, const void* panels, uint32_t n, uint32_t kb_total, void* w);
+
+/* W8 panels: both nibble planes of a W8 layer (no counterpart in the
+ * reference, which keeps them as two WBUF DDR word planes: SplitW8 and
+ * PackWbuf, tools/compiler/weights.cpp:72-88, tensors.cpp:66-90) converted
+ * once into the FP6 E2M3 operand codes of the GPU's block-scaled matrix
+ * cores, so that large-M fast layers convert only A in their K loop.  Each
+ * nibble value v (hi plane -8..7, lo plane 0..15) becomes the exact FP6 code
+ * of v / 2 and each scale byte ew becomes ew - 1 (hi) or ew - 5 (lo), which
+ * the matrix cores' E8M0 scaling turns back into the reference's weights;
+ * hb_unpack_w8 restores the DDR words bit for bit.  1.5 bytes per weight
+ * (DDR words: 1.125), so skinny layers, bound by weight bandwidth, are
+ * better served by DDR words.
+ *   n columns (a multiple of 8) x kb_total blocks -> ceil(n / 64) panels of
+ *   64 columns, each ceil(kb_total / 2) chunks of 6400 bytes, chunk (p, s)
+ *   at (p * ceil(kb_total / 2) + s) * 6400 for blocks 2s + b, b = 0, 1;
+ *   with i = (b * 2 + l) * 64 + c for plane l (0 hi, 1 lo), column 64p + c:
+ *     bytes i * 16 .. +15 and 4096 + i * 8 .. +7: the column-block's 32 FP6
+ *       codes (6 dwords: the first 4, then 2) in the packing of the matrix
+ *       cores' FP6 operands (v_cvt_scalef32_pk32_fp6_f16);
+ *     byte 6144 + (b * 32 + c % 32) * 4 + 2 (c / 32) + l: its scale byte
+ *       minus 1 (hi) or 5 (lo), modulo 256.
+ *   Columns past n and blocks past kb_total hold zero codes and scale 127.
+ *   Then one dword per panel: nonzero when a scale byte of the panel lies
+ *   outside [70, 179] (its tiles are then folded exactly in fast mode).
+ * hb_w8_panel_bytes gives the size (0 for a bad shape); hb_pack_w8 reads
+ * the hi and lo DDR word planes [n/8][kb_total] x 144 B; hb_unpack_w8 writes
+ * them back (bytes 136..143 of each word zero, as PackWbuf writes them).
+ * All device buffers 16-byte aligned; both calls return when done. */
+uint64_t hb_w8_panel_bytes(uint32_t n, uint32_t kb_total);
+int hb_pack_w8(hb_ctx* ctx, const void* w_hi, const void* w_lo, uint32_t n, uint32_t kb_total,
+               void* panels);
+int hb_unpack_w8(hb_ctx* ctx, const void* panels, uint32_t n, uint32_t kb_total, void* w_hi,
+                 void* w_lo);
 
 /* --------------------------------------------- attention W8 operands -- */
 

@@ -69,3 +69,15 @@ def test_linear_over_unpacked_panels_is_the_same_layer():
 def test_panel_bytes_rejects_bad_shapes():
     assert hb.panel_bytes(12, 3) == 0 and hb.panel_bytes(8, 0) == 0
     assert hb.panel_bytes(960, 80) == 15 * 40 * 2176 == 960 * 2560 * (0.5 + 1 / 32)
+
+
+def test_w8_panel_bytes():
+    """W8 panels (host-only size): 6400-byte chunks per 64 columns and two
+    blocks (both planes' FP6 codes, 1.5 bytes a weight, and their scale
+    bytes), then one flag dword per panel padded to 16 bytes."""
+    assert hb.w8_panel_bytes(12, 3) == 0 and hb.w8_panel_bytes(8, 0) == 0
+    assert hb.w8_panel_bytes(768, 24) == 12 * 12 * 6400 + 48
+    assert hb.w8_panel_bytes(72, 3) == 2 * 2 * 6400 + 16
+    n, kb = 3072, 24
+    codes = n * kb * 32 * 2 * 6 // 8
+    assert hb.w8_panel_bytes(n, kb) == codes + n * kb * 2 + (n // 64) * 4

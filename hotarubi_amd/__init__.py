@@ -54,6 +54,7 @@ EXPORTS = (
     "hb_row_load", "hb_row_load_async", "hb_row_store", "hb_row_store_async",
     "hb_gacc", "hb_gacc_async", "hb_panel_bytes", "hb_pack_weights", "hb_unpack_weights",
     "hb_linear_noalloc_async", "hb_w8_panel_bytes", "hb_pack_w8", "hb_unpack_w8",
+    "hb_w8_from_fp32", "hb_mxfp4_canonical",
 )
 
 
@@ -203,6 +204,8 @@ def lib():
             "hb_w8_panel_bytes": (C.c_uint64, [u32, u32]),
             "hb_pack_w8": (i, [vp, vp, vp, u32, u32, vp]),
             "hb_unpack_w8": (i, [vp, vp, u32, u32, vp, vp]),
+            "hb_w8_from_fp32": (i, [vp, vp, u32, u32, u32, vp, vp]),
+            "hb_mxfp4_canonical": (i, [vp, vp, vp, u32, u32, C.c_int32, u32, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -528,6 +531,26 @@ def unpack_w8(panels, n: int, kb_total: int, w_hi, w_lo, ctx: Context | None = N
     """hb_unpack_w8: W8 panels -> the hi and lo DDR word planes, bit for bit."""
     ctx = ctx or default_context()
     _check(lib().hb_unpack_w8(ctx.handle, _ptr(panels), n, kb_total, _ptr(w_hi), _ptr(w_lo)))
+
+
+def w8_from_fp32(w, rows: int, cols: int, out_rows: int, w_hi, w_lo,
+                 ctx: Context | None = None) -> None:
+    """hb_w8_from_fp32: fp32 weights [rows][cols] -> the W8 hi and lo WBUF word
+    planes [out_rows/8][ceil(cols/32)] x 144 B (PadRows, EncodeMxint8, SplitW8,
+    PackWbuf)."""
+    ctx = ctx or default_context()
+    _check(lib().hb_w8_from_fp32(ctx.handle, _ptr(w), rows, cols, out_rows, _ptr(w_hi),
+                                 _ptr(w_lo)))
+
+
+def mxfp4_canonical(codes, scales, rows: int, cols: int, out_rows: int, w,
+                    exponent_shift: int = 0, ctx: Context | None = None) -> None:
+    """hb_mxfp4_canonical: MXFP4 codes [rows][cols] and E8M0 scale bytes
+    [rows][cols/32] -> canonical WBUF words [out_rows/8][cols/32] x 144 B
+    (CanonicalMxfp4, PackWbuf)."""
+    ctx = ctx or default_context()
+    _check(lib().hb_mxfp4_canonical(ctx.handle, _ptr(codes), _ptr(scales), rows, cols,
+                                    exponent_shift, out_rows, _ptr(w)))
 
 
 def split8(src, rows: int, row_words: int, hi, lo, src_stride: int | None = None,

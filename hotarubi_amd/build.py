@@ -20,7 +20,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libhotarubi_gpu.so")
 SOURCES = ["hb_api.hip", "hb_gemm.hip", "hb_fast.hip", "hb_fast4.hip", "hb_skinny.hip", "hb_vec.hip",
-           "hb_dma.hip", "hb_panel.hip", "hb_stream.hip", "hb_w8.hip"]
+           "hb_dma.hip", "hb_panel.hip", "hb_stream.hip", "hb_w8.hip", "hb_prep.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 DEVICE_FLAGS = [

@@ -1001,6 +1001,55 @@ int hb_encode_mxint8(hb_ctx* ctx, const float* x, uint32_t rows, uint32_t cols, 
 }  // extern "C"
 
 namespace {
+// Runs one preparation launch with the context's flag word cleared first;
+// nonzero flag: the reference's rejection, as HB_EINVAL with `what`.
+template <typename Launch>
+int Prepare(hb_ctx* ctx, Launch launch, const char* name, const char* what) {
+  HB_HIP(hipMemsetAsync(ctx->d_flag, 0, sizeof(uint32_t), ctx->stream));
+  const hipError_t err = launch(ctx->d_flag);
+  if (err != hipSuccess) return HipFail(err, name);
+  uint32_t flag = 0;
+  HB_HIP(hipMemcpyAsync(&flag, ctx->d_flag, sizeof flag, hipMemcpyDeviceToHost, ctx->stream));
+  HB_HIP(hipStreamSynchronize(ctx->stream));
+  if (flag) return Fail(HB_EINVAL, "%s", what);
+  return HB_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int hb_w8_from_fp32(hb_ctx* ctx, const float* w, uint32_t rows, uint32_t cols,
+                    uint32_t out_rows, void* w_hi, void* w_lo) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!w || !w_hi || !w_lo) return Fail(HB_EINVAL, "null weights");
+  if (rows < 1 || cols < 1 || out_rows < rows || out_rows % 8 != 0)
+    return Fail(HB_EINVAL, "cannot pad %u rows to %u (a multiple of 8 at least rows)", rows,
+                out_rows);
+  if (reinterpret_cast<uintptr_t>(w_hi) % 16 != 0 || reinterpret_cast<uintptr_t>(w_lo) % 16 != 0)
+    return Fail(HB_EINVAL, "weight words must be 16-byte aligned");
+  return Prepare(ctx, [&](uint32_t* flag) {
+    return hb::LaunchW8FromFp32(w, rows, cols, out_rows, static_cast<uint8_t*>(w_hi),
+                                static_cast<uint8_t*>(w_lo), flag, ctx->stream);
+  }, "W8 weight launch", "MXINT8 input is infinite or NaN");
+}
+
+int hb_mxfp4_canonical(hb_ctx* ctx, const uint8_t* codes, const uint8_t* scales, uint32_t rows,
+                       uint32_t cols, int32_t exponent_shift, uint32_t out_rows, void* w) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!codes || !scales || !w) return Fail(HB_EINVAL, "null weights");
+  if (rows < 1 || cols < 32 || cols % 32 != 0 || out_rows < rows || out_rows % 8 != 0)
+    return Fail(HB_EINVAL, "cannot pad a %ux%u MXFP4 matrix to %u rows", rows, cols, out_rows);
+  if (reinterpret_cast<uintptr_t>(w) % 16 != 0)
+    return Fail(HB_EINVAL, "weight words must be 16-byte aligned");
+  return Prepare(ctx, [&](uint32_t* flag) {
+    return hb::LaunchMxfp4Canonical(codes, scales, rows, cols, exponent_shift, out_rows,
+                                    static_cast<uint8_t*>(w), flag, ctx->stream);
+  }, "MXFP4 weight launch", "a canonical MXFP4 block exponent is outside E8M0");
+}
+
+}  // extern "C"
+
+namespace {
 
 int DmaSplit(hb_ctx* ctx, const void* src, uint64_t stride, uint32_t rows, uint32_t row_words,
              void* hi, void* lo, bool t32, bool sync) {

@@ -248,6 +248,14 @@ hipError_t LaunchPackW8(const uint8_t* hi, const uint8_t* lo, uint32_t n, uint32
                         uint8_t* out, hipStream_t stream);
 hipError_t LaunchUnpackW8(const uint8_t* in, uint32_t n, uint32_t kb_total, uint8_t* hi,
                           uint8_t* lo, hipStream_t stream);
+// Weight preparation (hb_prep.hip): fp32 weights -> the W8 planes' WBUF
+// words; MXFP4 codes and scale bytes -> canonical WBUF words.  *bad_flag is
+// set where the reference would reject the input.
+hipError_t LaunchW8FromFp32(const float* w, uint32_t rows, uint32_t cols, uint32_t out_rows,
+                            uint8_t* hi, uint8_t* lo, uint32_t* bad_flag, hipStream_t stream);
+hipError_t LaunchMxfp4Canonical(const uint8_t* codes, const uint8_t* scales, uint32_t rows,
+                                uint32_t cols, int32_t exponent_shift, uint32_t out_rows,
+                                uint8_t* out, uint32_t* bad_flag, hipStream_t stream);
 // DDR words <-> panels of one plane (hb_panel.hip).
 hipError_t LaunchPackPanels(const uint8_t* w, uint32_t n, uint32_t kb_total, uint8_t* out,
                             hipStream_t stream);

@@ -499,6 +499,33 @@ int hb_rows_async(hb_ctx* ctx, const hb_rows_desc* desc);
 int hb_encode_mxint8(hb_ctx* ctx, const float* x, uint32_t rows,
                      uint32_t cols, void* out);
 
+/* Weight preparation, the compiler's conversions on device (for a runtime
+ * that loads checkpoints straight into GPU memory).  A weight matrix row is
+ * an output column of the layer.  Both calls return when done.
+ *
+ * hb_w8_from_fp32 replaces SplitW8(EncodeMxint8(PadRows(w, out_rows))) and
+ * PackWbuf of both planes (tools/compiler/smolvla_common.cpp:95-103,
+ * weights.cpp:72-88, tools/runtime/formats.cpp:35-56, tensors.cpp:66-90):
+ * fp32 w [rows][cols] -> the W8 layer's hi and lo WBUF word planes
+ * [out_rows/8][ceil(cols/32)] x 144 B (modes 1 and 2 of hb_linear_desc).
+ * out_rows >= rows and a multiple of 8; rows past `rows` and columns past
+ * `cols` are zeros.  Inf/NaN input returns HB_EINVAL (the reference rejects
+ * it), after the planes are written with such elements as 0.
+ *
+ * hb_mxfp4_canonical replaces PackWbuf(CanonicalMxfp4(m, exponent_shift,
+ * out_rows)) (weights.cpp:39-70) over the matrix ReadMxfp4 reads
+ * (weights.cpp:120-138): codes [rows][cols], one E2M1 code per byte (low
+ * nibble), and E8M0 scale bytes [rows][cols/32] -> WBUF words
+ * [out_rows/8][cols/32] x 144 B, each block rescaled so its largest code has
+ * E2M1 exponent 2.  cols a multiple of 32; out_rows >= rows and a multiple
+ * of 8.  A block exponent outside E8M0 returns HB_EINVAL (the reference
+ * rejects it), with that scale byte written modulo 256. */
+int hb_w8_from_fp32(hb_ctx* ctx, const float* w, uint32_t rows, uint32_t cols,
+                    uint32_t out_rows, void* w_hi, void* w_lo);
+int hb_mxfp4_canonical(hb_ctx* ctx, const uint8_t* codes, const uint8_t* scales,
+                       uint32_t rows, uint32_t cols, int32_t exponent_shift,
+                       uint32_t out_rows, void* w);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,7 +54,10 @@ EXPORTS = (
     "hb_row_load", "hb_row_load_async", "hb_row_store", "hb_row_store_async",
     "hb_gacc", "hb_gacc_async", "hb_panel_bytes", "hb_pack_weights", "hb_unpack_weights",
     "hb_linear_noalloc_async", "hb_w8_panel_bytes", "hb_pack_w8", "hb_unpack_w8",
-    "hb_w8_from_fp32", "hb_mxfp4_canonical",
+    "hb_w8_from_fp32", "hb_mxfp4_canonical", "hb_image_create", "hb_image_destroy",
+    "hb_image_alloc", "hb_image_set_reuse", "hb_image_define", "hb_image_put", "hb_image_get",
+    "hb_image_region", "hb_image_region_count", "hb_image_region_at", "hb_image_end",
+    "hb_image_base",
 )
 
 
@@ -206,6 +209,21 @@ def lib():
             "hb_unpack_w8": (i, [vp, vp, u32, u32, vp, vp]),
             "hb_w8_from_fp32": (i, [vp, vp, u32, u32, u32, vp, vp]),
             "hb_mxfp4_canonical": (i, [vp, vp, vp, u32, u32, C.c_int32, u32, vp]),
+            "hb_image_create": (i, [vp, C.c_uint64, C.POINTER(vp)]),
+            "hb_image_destroy": (None, [vp]),
+            "hb_image_alloc": (i, [vp, C.c_char_p, C.c_uint64, C.c_uint64,
+                                   C.POINTER(C.c_uint64)]),
+            "hb_image_set_reuse": (None, [vp, i]),
+            "hb_image_define": (i, [vp, C.c_char_p, C.c_uint64, C.c_uint64]),
+            "hb_image_put": (i, [vp, C.c_uint64, vp, C.c_uint64]),
+            "hb_image_get": (i, [vp, C.c_uint64, vp, C.c_uint64]),
+            "hb_image_region": (i, [vp, C.c_char_p, C.POINTER(C.c_uint64),
+                                    C.POINTER(C.c_uint64)]),
+            "hb_image_region_count": (u32, [vp]),
+            "hb_image_region_at": (i, [vp, u32, C.POINTER(C.c_char_p), C.POINTER(C.c_uint64),
+                                       C.POINTER(C.c_uint64)]),
+            "hb_image_end": (C.c_uint64, [vp]),
+            "hb_image_base": (vp, [vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -551,6 +569,78 @@ def mxfp4_canonical(codes, scales, rows: int, cols: int, out_rows: int, w,
     ctx = ctx or default_context()
     _check(lib().hb_mxfp4_canonical(ctx.handle, _ptr(codes), _ptr(scales), rows, cols,
                                     exponent_shift, out_rows, _ptr(w)))
+
+
+class Image:
+    """hb_image: the compiler's DDR image container (DdrImage,
+    tools/compiler/ddr_image.hpp) over device memory; ctx=False keeps the
+    bookkeeping only (no device memory)."""
+
+    PAGE = 4096
+
+    def __init__(self, capacity: int, ctx: Context | None | bool = None):
+        if ctx is False:
+            handle_ctx = None
+        else:
+            handle_ctx = (ctx or default_context()).handle
+        h = C.c_void_p()
+        _check(lib().hb_image_create(handle_ctx, capacity, C.byref(h)))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            lib().hb_image_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def alloc(self, name: str, size: int, align: int = 0) -> int:
+        off = C.c_uint64()
+        _check(lib().hb_image_alloc(self.handle, name.encode(), size, align, C.byref(off)))
+        return off.value
+
+    def set_reuse(self, reuse: bool) -> None:
+        lib().hb_image_set_reuse(self.handle, 1 if reuse else 0)
+
+    def define(self, name: str, offset: int, size: int) -> None:
+        _check(lib().hb_image_define(self.handle, name.encode(), offset, size))
+
+    def put(self, offset: int, data: bytes) -> None:
+        buf = C.create_string_buffer(bytes(data), len(data))
+        _check(lib().hb_image_put(self.handle, offset, buf, len(data)))
+
+    def get(self, offset: int, size: int) -> bytes:
+        buf = C.create_string_buffer(size)
+        _check(lib().hb_image_get(self.handle, offset, buf, size))
+        return buf.raw
+
+    def region(self, name: str) -> tuple[int, int]:
+        off, size = C.c_uint64(), C.c_uint64()
+        _check(lib().hb_image_region(self.handle, name.encode(), C.byref(off), C.byref(size)))
+        return off.value, size.value
+
+    def regions(self) -> list[tuple[str, int, int]]:
+        out = []
+        for i in range(int(lib().hb_image_region_count(self.handle))):
+            name, off, size = C.c_char_p(), C.c_uint64(), C.c_uint64()
+            _check(lib().hb_image_region_at(self.handle, i, C.byref(name), C.byref(off),
+                                            C.byref(size)))
+            out.append((name.value.decode(), off.value, size.value))
+        return out
+
+    def end(self) -> int:
+        return int(lib().hb_image_end(self.handle))
+
+    def ptr(self, name: str) -> int:
+        """Device address of a region."""
+        base = lib().hb_image_base(self.handle)
+        if not base:
+            raise HbError(HB_EINVAL, "the image has no device memory")
+        return int(base) + self.region(name)[0]
 
 
 def split8(src, rows: int, row_words: int, hi, lo, src_stride: int | None = None,

@@ -8,7 +8,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
+#include <string>
+#include <vector>
 #include <new>
 #include <string>
 #include <vector>
@@ -22,6 +25,17 @@ struct hb_ctx {
   bool own_stream = false;
   uint32_t* d_flag = nullptr;  // device flag word for hb_encode_mxint8
   hb::Workspace ws;            // split partials / deferred epilogue inputs
+};
+
+// DDR image (DdrImage, tools/compiler/ddr_image.cpp): regions in order of
+// first placement, an index by name, the end of the last placed region.
+struct hb_image {
+  hb_ctx* ctx = nullptr;    // null: bookkeeping only
+  uint8_t* bytes = nullptr;  // device memory, `capacity` bytes
+  uint64_t capacity = 0, end = 0;
+  bool reuse = false;
+  std::vector<std::pair<std::string, std::pair<uint64_t, uint64_t>>> regions;  // offset, size
+  std::map<std::string, size_t, std::less<>> index;
 };
 
 struct hb_onchip {
@@ -1210,5 +1224,149 @@ int hb_t32_split8_async(hb_ctx* ctx, const void* src, uint64_t src_stride, uint3
                         uint32_t row_words, void* hi, void* lo) {
   return DmaSplit(ctx, src, src_stride, rows, row_words, hi, lo, true, false);
 }
+
+}  // extern "C"
+
+// ---------------------------------------------------------- DDR images --
+
+extern "C" {
+
+int hb_image_create(hb_ctx* ctx, uint64_t capacity, hb_image** out) {
+  if (!out) return Fail(HB_EINVAL, "null image");
+  *out = nullptr;
+  auto* img = new (std::nothrow) hb_image;
+  if (!img) return Fail(HB_ENOMEM, "image bookkeeping");
+  img->capacity = capacity;
+  if (ctx != nullptr) {
+    if (int rc = Enter(ctx)) {
+      delete img;
+      return rc;
+    }
+    img->ctx = ctx;
+    if (capacity > 0) {
+      const hipError_t err = hipMalloc(&img->bytes, capacity);
+      if (err != hipSuccess) {
+        delete img;
+        return Fail(HB_ENOMEM, "image of %llu bytes: %s", (unsigned long long)capacity,
+                    hipGetErrorString(err));
+      }
+      const hipError_t zero = hipMemset(img->bytes, 0, capacity);
+      if (zero != hipSuccess) {
+        (void)hipFree(img->bytes);
+        delete img;
+        return HipFail(zero, "image clear");
+      }
+    }
+  }
+  *out = img;
+  return HB_OK;
+}
+
+void hb_image_destroy(hb_image* img) {
+  if (!img) return;
+  if (img->bytes) {
+    (void)hipSetDevice(img->ctx->device);
+    (void)hipFree(img->bytes);
+  }
+  delete img;
+}
+
+int hb_image_alloc(hb_image* img, const char* name, uint64_t size, uint64_t align,
+                   uint64_t* offset) {
+  if (!img || !name) return Fail(HB_EINVAL, "null image or name");
+  if (align == 0) align = 4096;
+  const auto found = img->index.find(name);
+  if (img->reuse && found != img->index.end()) {
+    const auto& region = img->regions[found->second].second;
+    if (size > region.second)
+      return Fail(HB_EINVAL, "region %s reused with %llu bytes but holds %llu", name,
+                  (unsigned long long)size, (unsigned long long)region.second);
+    if (offset) *offset = region.first;
+    return HB_OK;
+  }
+  const uint64_t at = (img->end + align - 1) / align * align;
+  if (at < img->end || at + size < at || at + size > img->capacity)
+    return Fail(HB_EINVAL, "region %s of %llu bytes at %#llx exceeds the image of %llu bytes",
+                name, (unsigned long long)size, (unsigned long long)at,
+                (unsigned long long)img->capacity);
+  if (found != img->index.end()) {
+    img->regions[found->second].second = {at, size};
+  } else {
+    img->index.emplace(name, img->regions.size());
+    img->regions.emplace_back(name, std::make_pair(at, size));
+  }
+  img->end = at + size;
+  if (offset) *offset = at;
+  return HB_OK;
+}
+
+void hb_image_set_reuse(hb_image* img, int reuse) {
+  if (img) img->reuse = reuse != 0;
+}
+
+int hb_image_define(hb_image* img, const char* name, uint64_t offset, uint64_t size) {
+  if (!img || !name) return Fail(HB_EINVAL, "null image or name");
+  if (offset + size < offset || offset + size > img->end || img->index.count(name))
+    return Fail(HB_EINVAL, "cannot define region %s at %#llx", name, (unsigned long long)offset);
+  img->index.emplace(name, img->regions.size());
+  img->regions.emplace_back(name, std::make_pair(offset, size));
+  return HB_OK;
+}
+
+int hb_image_put(hb_image* img, uint64_t offset, const void* bytes, uint64_t size) {
+  if (!img || (!bytes && size)) return Fail(HB_EINVAL, "null image or bytes");
+  if (offset + size < offset || offset + size > img->capacity)
+    return Fail(HB_EINVAL, "%llu bytes at %#llx exceed the image", (unsigned long long)size,
+                (unsigned long long)offset);
+  if (!img->bytes) return Fail(HB_EINVAL, "the image has no device memory");
+  if (int rc = Enter(img->ctx)) return rc;
+  if (size == 0) return HB_OK;
+  HB_HIP(hipMemcpyAsync(img->bytes + offset, bytes, size, hipMemcpyHostToDevice,
+                        img->ctx->stream));
+  HB_HIP(hipStreamSynchronize(img->ctx->stream));
+  return HB_OK;
+}
+
+int hb_image_get(const hb_image* img, uint64_t offset, void* bytes, uint64_t size) {
+  if (!img || (!bytes && size)) return Fail(HB_EINVAL, "null image or bytes");
+  if (offset + size < offset || offset + size > img->capacity)
+    return Fail(HB_EINVAL, "%llu bytes at %#llx exceed the image", (unsigned long long)size,
+                (unsigned long long)offset);
+  if (!img->bytes) return Fail(HB_EINVAL, "the image has no device memory");
+  if (int rc = Enter(img->ctx)) return rc;
+  if (size == 0) return HB_OK;
+  HB_HIP(hipMemcpyAsync(bytes, img->bytes + offset, size, hipMemcpyDeviceToHost,
+                        img->ctx->stream));
+  HB_HIP(hipStreamSynchronize(img->ctx->stream));
+  return HB_OK;
+}
+
+int hb_image_region(const hb_image* img, const char* name, uint64_t* offset, uint64_t* size) {
+  if (!img || !name) return Fail(HB_EINVAL, "null image or name");
+  const auto found = img->index.find(name);
+  if (found == img->index.end()) return Fail(HB_EINVAL, "no region named %s", name);
+  const auto& region = img->regions[found->second].second;
+  if (offset) *offset = region.first;
+  if (size) *size = region.second;
+  return HB_OK;
+}
+
+uint32_t hb_image_region_count(const hb_image* img) {
+  return img ? (uint32_t)img->regions.size() : 0u;
+}
+
+int hb_image_region_at(const hb_image* img, uint32_t index, const char** name, uint64_t* offset,
+                       uint64_t* size) {
+  if (!img || index >= img->regions.size()) return Fail(HB_EINVAL, "no region %u", index);
+  const auto& entry = img->regions[index];
+  if (name) *name = entry.first.c_str();
+  if (offset) *offset = entry.second.first;
+  if (size) *size = entry.second.second;
+  return HB_OK;
+}
+
+uint64_t hb_image_end(const hb_image* img) { return img ? img->end : 0u; }
+
+void* hb_image_base(const hb_image* img) { return img ? img->bytes : nullptr; }
 
 }  // extern "C"

@@ -246,7 +246,6 @@ __global__ __launch_bounds__(512) void PanelKernel(GemmArgs g) {
   // W cursor: global step u; per tile, the panel's chunk 0.
   uint32_t wk = 0, ws = 0, wcached = ~0u;
   const uint8_t* wpanel = nullptr;
-  bool wbad = false;  // a scale byte of this wave's panel left the window (current load tile)
   auto wload = [&](RawW& rw) {
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t k = min(wk, sc.count - 1);

@@ -526,6 +526,39 @@ int hb_mxfp4_canonical(hb_ctx* ctx, const uint8_t* codes, const uint8_t* scales,
                        uint32_t rows, uint32_t cols, int32_t exponent_shift,
                        uint32_t out_rows, void* w);
 
+/* ------------------------------------------------------ DDR images -- */
+
+/* The compiler's DDR image container, DdrImage
+ * (tools/compiler/ddr_image.hpp:1-51, ddr_image.cpp:1-63), over device
+ * memory: a runtime loads a compiled image (image.bin, and the regions of
+ * meta.json, tools/compiler/output.cpp:58-113) into one allocation and takes
+ * each named region's device address for hb_linear and the other calls.
+ * The region rules are DdrImage's: hb_image_alloc places a region at the
+ * image's end rounded up to `align` (0: one page, 4096 bytes) and fails if it
+ * passes the capacity; with reuse on, a name already placed returns its
+ * region if the size fits (else fails); without reuse, allocating a name
+ * again moves it to a new region (one entry, in its first place in the
+ * list); hb_image_define names [offset, offset + size) inside the image's
+ * end under a new name; hb_image_put writes bytes anywhere below the
+ * capacity.  Failures return HB_EINVAL with DdrImage's message.  A new
+ * image's bytes are zero.  ctx NULL: bookkeeping only, no device memory
+ * (put, get and base are then unavailable). */
+typedef struct hb_image hb_image;
+int hb_image_create(hb_ctx* ctx, uint64_t capacity, hb_image** out);
+void hb_image_destroy(hb_image* image);
+int hb_image_alloc(hb_image* image, const char* name, uint64_t size, uint64_t align,
+                   uint64_t* offset);
+void hb_image_set_reuse(hb_image* image, int reuse);
+int hb_image_define(hb_image* image, const char* name, uint64_t offset, uint64_t size);
+int hb_image_put(hb_image* image, uint64_t offset, const void* bytes, uint64_t size);
+int hb_image_get(const hb_image* image, uint64_t offset, void* bytes, uint64_t size);
+int hb_image_region(const hb_image* image, const char* name, uint64_t* offset, uint64_t* size);
+uint32_t hb_image_region_count(const hb_image* image);
+int hb_image_region_at(const hb_image* image, uint32_t index, const char** name,
+                       uint64_t* offset, uint64_t* size);
+uint64_t hb_image_end(const hb_image* image);
+void* hb_image_base(const hb_image* image);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,7 +19,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def header_symbols():
     text = open(os.path.join(ROOT, "include", "hotarubi_gpu.h")).read()
-    return sorted(set(re.findall(r"^\s*(?:int|uint64_t|const char\*)\s+(hb_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(
+        r"^\s*(?:int|void\*?|uint32_t|uint64_t|const char\*)\s+(hb_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():

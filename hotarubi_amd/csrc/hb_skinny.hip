@@ -378,15 +378,14 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
 // with v_mfma_scale_f32_32x32x64_f8f6f4: lane l's A operand is 32 values of
 // row l % 32 and block l / 32 of the step, its B operand 32 values of
 // column l % 32 and the same block (formats and scale bytes as above).
-// The K ranges ("splits") of a tile meet in the workspace: each split
-// writes its 32 x 32 sums (element e of lane l at e * 64 + l) and its window
-// flag, then counts itself on the tile's counter; the split that counts
-// last adds the partials in split order, so the sum does not depend on
-// which split that is, runs the epilogue and the requantize, stores C, and
-// puts the counter back to zero for the next launch.  A tile of one split
-// finishes in place.  Per split about 3.4 KB of operands per step (MXFP4),
-// so a workgroup moves a few 10 KB: small layers are latency-bound, and
-// this spreads them over many CUs in one launch instead of two.
+// The K ranges ("splits") of a tile are the waves of its workgroup (up to
+// kMaxSplitWaves): each wave folds its range, the partial sums meet in LDS,
+// and wave 0 adds them in split order, so the sum does not depend on which
+// wave finishes first, then runs the epilogue and the requantize and stores
+// C.  Per split about 3.4 KB of operands per step (MXFP4), so a workgroup
+// moves a few 10 KB: small layers are latency-bound, and the splits put
+// every tile's loads in flight at once with one round trip to memory,
+// finishing in the same workgroup.
 template <bool kW8>
 struct RawSplit {
   uint32_t a[8], sa;
@@ -394,13 +393,16 @@ struct RawSplit {
   uint32_t nib;  // 0x0F0F0F0F, or 0 for a block past the range (adds zero)
 };
 
+constexpr int kMaxSplitWaves = 8;
 template <bool kW8, bool kMulti>
-__global__ __launch_bounds__(64) void SplitKernel(GemmArgs g) {
+__global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
   constexpr int kWP = kW8 ? 2 : 1;
   typedef float f32x16 __attribute__((ext_vector_type(16)));
-  const uint32_t lane = threadIdx.x;
-  const uint32_t tiles = g.gx * g.gy;
-  const uint32_t tile = blockIdx.x % tiles, split = blockIdx.x / tiles;
+  __shared__ float lds_part[kMaxSplitWaves][16 * 64];  // [split][e][lane]
+  __shared__ uint32_t lds_flag[kMaxSplitWaves];
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t tile = blockIdx.x;
+  const uint32_t split = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t col0 = (tile % g.gx) * 32, row0 = (tile / g.gx) * 32;
   const uint32_t r32 = lane & 31, hb = lane >> 5;
   const uint8_t* a = g.a;
@@ -498,14 +500,15 @@ __global__ __launch_bounds__(64) void SplitKernel(GemmArgs g) {
   constexpr int kPreOps = 2;
   f32x16 pre_init = {}, pre_x2[kPreOps] = {};
   float pre_v[kPreOps] = {};
-  if (g.acc && col_in) {
+  const bool finisher = split == 0;  // uniform: wave 0 finishes the tile
+  if (finisher && g.acc && col_in) {
 #pragma unroll
     for (int e = 0; e < 16; ++e)
       if (row_of(e) < g.m) pre_init[e] = __uint_as_float(g.c[(size_t)row_of(e) * g.n + col]);
   }
 #pragma unroll
   for (int op = 0; op < kPreOps; ++op) {
-    if ((uint32_t)op >= g.n_ops || !col_in) continue;
+    if (!finisher || (uint32_t)op >= g.n_ops || !col_in) continue;
     const uint32_t kind = g.op_kind[op];
     if (kind == kEpAddP || kind == kEpMulP) pre_v[op] = __uint_as_float(g.op_vec[op][col]);
     if (kind == kEpAdd || kind == kEpActMul) {
@@ -532,51 +535,18 @@ __global__ __launch_bounds__(64) void SplitKernel(GemmArgs g) {
     }
   }
   bool slow = __builtin_amdgcn_ballot_w64(unsafe) != 0;
-  f32x16 sum;
-  if (g.splits > 1) {
-    float* part = g.ws + kSplitCounterBytes / 4;
-    uint32_t* flags = reinterpret_cast<uint32_t*>(part + (size_t)tiles * g.splits * 1024);
-    uint32_t* counters = reinterpret_cast<uint32_t*>(g.ws);
-    // Partials, flags and the counter are exchanged with device-scope
-    // atomic stores, loads and adds, which the L2 writes through or reads
-    // coherently: a device-scope fence would write back and invalidate the
-    // whole L2 of the XCD in every workgroup.  The stores complete (load
-    // counter at zero) before the count.
-    float* mine = part + ((size_t)tile * g.splits + split) * 1024;
+  f32x16 sum = acc;
+  if (g.splits > 1) {  // the waves' partials meet in LDS; wave 0 adds them in split order
 #pragma unroll
-    for (int e = 0; e < 16; ++e)
-      __hip_atomic_store(&mine[e * 64 + lane], acc[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (lane == 0)
-      __hip_atomic_store(&flags[tile * g.splits + split], slow ? 1u : 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    uint32_t old = 0;
-    if (lane == 0)
-      old = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old != g.splits - 1) return;  // (uniform) another split finishes the tile
-    if (lane == 0)
-      __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    auto partial = [&](uint32_t s) __attribute__((always_inline)) {
-      float* ps = part + ((size_t)tile * g.splits + s) * 1024;
-      f32x16 v;
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        v[e] = __hip_atomic_load(&ps[e * 64 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return v;
-    };
-    auto flag = [&](uint32_t s) __attribute__((always_inline)) {
-      return __hip_atomic_load(&flags[tile * g.splits + s], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT) != 0;
-    };
-    sum = partial(0);
-    slow = flag(0);
+    for (int e = 0; e < 16; ++e) lds_part[split][e * 64 + lane] = acc[e];
+    if (lane == 0) lds_flag[split] = slow ? 1u : 0u;
+    __syncthreads();
+    if (!finisher) return;
     for (uint32_t s = 1; s < g.splits; ++s) {
-      sum += partial(s);
-      slow |= flag(s);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sum[e] += lds_part[s][e * 64 + lane];
+      slow |= lds_flag[s] != 0;
     }
-  } else {
-    sum = acc;
   }
 
   uint32_t* c = g.c;
@@ -672,31 +642,24 @@ bool SplitEligible(const GemmArgs& args, uint32_t batch) {
 }
 
 size_t SplitPlan(GemmArgs& args) {
-  // splits of at least 4 steps, at most 8 per tile (the last split reads
-  // them all), within kSplitMaxPartials partial tiles
-  constexpr uint32_t kMinSteps = 4, kMaxSplits = 8;
+  // splits (waves) of at least 4 steps, at most kMaxSplitWaves per tile
+  constexpr uint32_t kMinSteps = 4, kMaxSplits = kMaxSplitWaves;
   args.gx = (args.n + 31) / 32;
   args.gy = (args.quads * 4 + 31) / 32;
   args.gz = 1;
   uint32_t nblocks = 0;
   for (uint32_t p = 0; p < args.n_pieces; ++p) nblocks += args.piece_kb[p];
-  const uint32_t steps = (nblocks + 1) / 2, tiles = args.gx * args.gy;
+  const uint32_t steps = (nblocks + 1) / 2;
   uint32_t per = (steps + kMaxSplits - 1) / kMaxSplits;
   per = per < kMinSteps ? kMinSteps : per;
-  uint32_t splits = (steps + per - 1) / per;
-  if (tiles > kSplitCounters) splits = 1;
-  while (splits > 1 && tiles * splits > kSplitMaxPartials) {
-    --splits;
-    per = (steps + splits - 1) / splits;
-    splits = (steps + per - 1) / per;
-  }
+  const uint32_t splits = (steps + per - 1) / per;
   args.splits = splits;
   args.split_steps = splits > 1 ? per : steps;
-  return splits > 1 ? (size_t)tiles * splits * (1024 * sizeof(float) + sizeof(uint32_t)) : 0;
+  return 0;  // the partials meet in LDS: no workspace
 }
 
 hipError_t LaunchSplitLinear(const GemmArgs& args, hipStream_t stream) {
-  const dim3 grid(args.gx * args.gy * args.splits), block(64);
+  const dim3 grid(args.gx * args.gy), block(64 * args.splits);
   const bool w8 = args.n_planes == 2, multi = args.n_pieces > 1;
   if (w8) {
     if (multi) hipLaunchKernelGGL((SplitKernel<true, true>), grid, block, 0, stream, args);

@@ -249,6 +249,9 @@ class Chain:
         self.g = torch.Generator(device=self.dev).manual_seed(seed)
         self.quads = (m + 3) // 4
         self.descs, self.keep, self.ops, self.bytes = [], [], 0.0, 0.0
+        # launch plan: lists of descriptor indices; a list of several is one
+        # hb_linear_group_async call (grouped=False: every layer on its own)
+        self.plan, self.grouped, self._arrays = [], True, None
 
     def a_words(self, kb):
         t = self.torch.randint(0, 256, (self.quads * kb, 144), generator=self.g, device=self.dev,
@@ -299,15 +302,32 @@ class Chain:
         self.descs.append(self.hb.linear_desc(self.m, n, kb, a, planes, modes, c, ops=ops,
                                               tbuf=tbuf, q_out=q, onto=onto, mode=self.mode,
                                               w8_panels=w8p))
+        self.plan.append([len(self.descs) - 1])
         self.ops += 2.0 * self.m * n * kb * 32
         vectors = sum(1 for k, _ in ops if k in (self.hb.EP_ADDP, self.hb.EP_MULP))
         out = self.m * n * (1 + 1 / 32) if q is not None else 4 * self.m * n
         self.bytes += layer_bytes(self.m, n, kb, 8 if len(planes) == 2 else 4, vectors) - \
             4 * self.m * n + out + (4 * self.m * n if onto else 0)
 
+    def group(self, k):
+        """The last k layers added form one group launch (layers the model
+        computes from the same inputs, or a gated pair)."""
+        self.plan[-k:] = [sum(self.plan[-k:], [])]
+
     def run(self, ctx):
-        for d in self.descs:
-            self.hb.launch(d, ctx)
+        if not self.grouped:
+            for d in self.descs:
+                self.hb.launch(d, ctx)
+            return
+        if self._arrays is None:
+            self._arrays = [self.descs[p[0]] if len(p) == 1 else
+                            (type(self.descs[0]) * len(p))(*[self.descs[i] for i in p])
+                            for p in self.plan]
+        for p, arr in zip(self.plan, self._arrays):
+            if len(p) == 1:
+                self.hb.launch(arr, ctx)
+            else:
+                self.hb.linear_group(arr, ctx)
 
 
 class ExpertStep(Chain):
@@ -336,6 +356,7 @@ class ExpertStep(Chain):
             for _, n in heads:
                 self.add(n, self.KB, a1, [self.w_words(n, self.KB)], self.f32(n),
                          q=self.a_words(n // 32))
+            self.group(len(heads))
             self.add(self.WIDTH, self.KBQ, ao, [self.w_words(self.WIDTH, self.KBQ)], x[1],
                      ops=[(hb.EP_ADD, x[0])])
             up = self.f32(self.HID)
@@ -343,6 +364,7 @@ class ExpertStep(Chain):
             h = self.a_words(self.KBH)
             self.add(self.HID, self.KB, a2, [self.w_words(self.HID, self.KB)], self.f32(self.HID),
                      ops=[(hb.EP_ACT_MUL, up)], q=h, tbuf=tb)
+            self.group(2)
             self.add(self.WIDTH, self.KBH, h, [self.w_words(self.WIDTH, self.KBH)], x[2],
                      ops=[(hb.EP_ADD, x[1])])
         act, tim, hid, xin = self.a_words(1), self.a_words(self.KB), self.a_words(self.KB), \
@@ -383,6 +405,7 @@ class PrefixStep(Chain):
             for n in (self.HIDDEN, self.KV, self.KV):
                 self.add(n, self.KB, a1, [self.w_words(n, self.KB)], self.f32(n),
                          q=self.a_words(n // 32))
+            self.group(3)
             self.add(self.HIDDEN, self.KB, ao, [self.w_words(self.HIDDEN, self.KB)], x[1],
                      ops=[(hb.EP_ADD, x[0])])
             up = self.f32(self.INTER)
@@ -390,6 +413,7 @@ class PrefixStep(Chain):
             h = self.a_words(self.KBI)
             self.add(self.INTER, self.KB, a2, [self.w_words(self.INTER, self.KB)],
                      self.f32(self.INTER), ops=[(hb.EP_ACT_MUL, up)], q=h, tbuf=tb)
+            self.group(2)
             self.add(self.HIDDEN, self.KBI, h, [self.w_words(self.HIDDEN, self.KBI)], x[2],
                      ops=[(hb.EP_ADD, x[1])])
         torch.cuda.synchronize()
@@ -735,6 +759,18 @@ def time_chain(torch, ctx, work, steps=10, graph=True):
     eager = t0.elapsed_time(t1) / steps
     out = {"m": work.m, "gemms": len(work.descs), "gops": round(work.ops / 1e9, 3),
            "eager_ms": round(eager, 4)}
+    if work.grouped and len(work.plan) < len(work.descs):
+        out["launch_calls"] = len(work.plan)
+        work.grouped = False  # the same chain, one call per layer, for comparison
+        for _ in range(2):
+            work.run(ctx)
+        t0.record(stream)
+        for _ in range(steps):
+            work.run(ctx)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        out["ungrouped_eager_ms"] = round(t0.elapsed_time(t1) / steps, 4)
+        work.grouped = True
     if graph:
         try:
             side = torch.cuda.Stream()

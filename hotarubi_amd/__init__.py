@@ -57,7 +57,7 @@ EXPORTS = (
     "hb_w8_from_fp32", "hb_mxfp4_canonical", "hb_image_create", "hb_image_destroy",
     "hb_image_alloc", "hb_image_set_reuse", "hb_image_define", "hb_image_put", "hb_image_get",
     "hb_image_region", "hb_image_region_count", "hb_image_region_at", "hb_image_end",
-    "hb_image_base",
+    "hb_image_base", "hb_linear_group_async",
 )
 
 
@@ -187,6 +187,7 @@ def lib():
             "hb_linear": (i, [vp, C.POINTER(_LinearDesc)]),
             "hb_linear_async": (i, [vp, C.POINTER(_LinearDesc)]),
             "hb_linear_batched_async": (i, [vp, C.POINTER(_LinearDesc), u32]),
+            "hb_linear_group_async": (i, [vp, C.POINTER(_LinearDesc), u32]),
             "hb_linear_noalloc_async": (i, [vp, C.POINTER(_LinearDesc), u32]),
             "hb_encode_mxint8": (i, [vp, vp, u32, u32, vp]),
             "hb_gacc": (i, [vp, C.POINTER(_GaccDesc)]),
@@ -447,6 +448,16 @@ def launch(desc: _LinearDesc, ctx: Context | None = None) -> None:
     """hb_linear_async on a prebuilt descriptor (ordered on the context's stream)."""
     ctx = ctx or default_context()
     _check(lib().hb_linear_async(ctx.handle, C.byref(desc)))
+
+
+def linear_group(descs, ctx: Context | None = None) -> None:
+    """hb_linear_group_async: up to 4 independent small fast layers (and
+    gated pairs) in one launch where possible; the result of launching them
+    in order.  descs: a list of descriptors or a prebuilt ctypes array of
+    them (reused across calls)."""
+    ctx = ctx or default_context()
+    arr = descs if isinstance(descs, C.Array) else (_LinearDesc * len(descs))(*descs)
+    _check(lib().hb_linear_group_async(ctx.handle, arr, len(descs)))
 
 
 def linear_batched(descs, ctx: Context | None = None) -> None:

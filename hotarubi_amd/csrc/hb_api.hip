@@ -909,6 +909,73 @@ int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count
   return LinearBatched(ctx, d, count);
 }
 
+int hb_linear_group_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
+  if (int rc = Enter(ctx)) return rc;
+  if (!d || count < 1 || count > HB_MAX_GROUP)
+    return Fail(HB_EINVAL, "a group holds 1 to %d layers, not %u", HB_MAX_GROUP, count);
+  hb::SplitGroup grp;
+  std::memset(&grp, 0, sizeof grp);
+  bool fuse = true;
+  for (uint32_t i = 0; i < count; ++i) {
+    bool mixed = false;
+    if (int rc = LinearArgs(&d[i], &grp.g[i], &mixed)) return rc;
+    const hb::GemmArgs& g = grp.g[i];
+    fuse = fuse && !mixed && (d[i].flags & HB_LINEAR_FAST) && !g.w_fp6 && hb::FastEligible(g) &&
+           hb::SplitEligible(g, 1) && g.n_planes == grp.g[0].n_planes &&
+           (g.n_pieces > 1) == (grp.g[0].n_pieces > 1);
+  }
+  if (!fuse) {  // one launch per layer, in order
+    for (uint32_t i = 0; i < count; ++i)
+      if (int rc = LinearBatched(ctx, &d[i], 1)) return rc;
+    return HB_OK;
+  }
+  // Fused pairs: a later layer whose ACT_MUL reads an earlier one's C over
+  // the same m x n runs in the earlier one's workgroups, after it.
+  constexpr uint32_t kNone = hb::kMaxGroup;
+  uint32_t partner[hb::kMaxGroup], pair_op[hb::kMaxGroup];
+  bool second[hb::kMaxGroup] = {};
+  for (uint32_t i = 0; i < count; ++i) partner[i] = kNone;
+  for (uint32_t j = 1; j < count; ++j)
+    for (uint32_t o = 0; o < d[j].n_ops && !second[j]; ++o) {
+      if (d[j].ops[o].op != HB_EP_ACT_MUL) continue;
+      for (uint32_t i = 0; i < j; ++i)
+        if (partner[i] == kNone && !second[i] && d[j].ops[o].x2 == d[i].c && d[i].m == d[j].m &&
+            d[i].n == d[j].n) {
+          partner[i] = j;
+          pair_op[i] = o;
+          second[j] = true;
+          break;
+        }
+    }
+  uint32_t waves = 1, end = 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    hb::SplitPlan(grp.g[i]);
+    grp.g[i].fast_ep = 1u;
+  }
+  for (uint32_t i = 0; i < count; ++i) {
+    if (second[i]) continue;
+    uint32_t w = grp.g[i].splits;
+    if (partner[i] != kNone) {  // a pair's layers fold side by side in one workgroup
+      hb::GemmArgs& g2 = grp.g[partner[i]];
+      if (w + g2.splits > hb::kMaxSplitWaves) {
+        hb::SplitPlan(grp.g[i], hb::kMaxSplitWaves / 2);
+        hb::SplitPlan(g2, hb::kMaxSplitWaves / 2);
+      }
+      w = grp.g[i].splits + g2.splits;
+    }
+    waves = std::max(waves, w);
+    const uint32_t u = grp.units++;
+    end += grp.g[i].gx * grp.g[i].gy;
+    grp.tile_end[u] = end;
+    grp.first[u] = i;
+    grp.second[u] = partner[i];
+    grp.x2_op[u] = partner[i] == kNone ? 0u : pair_op[i];
+  }
+  const hipError_t err = hb::LaunchSplitGroup(grp, waves, ctx->stream);
+  if (err != hipSuccess) return HipFail(err, "group launch");
+  return HB_OK;
+}
+
 int hb_linear_noalloc_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) {
   if (int rc = Enter(ctx)) return rc;
   void* p = nullptr;

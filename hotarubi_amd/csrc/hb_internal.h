@@ -268,10 +268,25 @@ hipError_t LaunchLinearSkinny(const GemmArgs& args, uint32_t batch, hipStream_t 
 // K split over workgroups, the last split of a tile finishing it.
 constexpr uint32_t kSplitMaxRows = 160;
 bool SplitEligible(const GemmArgs& args, uint32_t batch);
-// Grid and K split of a split launch (sets gx, gy, splits, split_steps) and
-// the workspace bytes it needs past the counters (0: no partials).
-size_t SplitPlan(GemmArgs& args);
+// Grid and K split of a split launch (sets gx, gy, splits, split_steps:
+// splits of at least 4 steps, at most max_splits, one wave each) and the
+// workspace bytes it needs past the counters (0: no partials).
+constexpr uint32_t kMaxSplitWaves = 8;
+size_t SplitPlan(GemmArgs& args, uint32_t max_splits = kMaxSplitWaves);
 hipError_t LaunchSplitLinear(const GemmArgs& args, hipStream_t stream);
+// Up to kMaxGroup single-launch split layers (args from SplitPlan, one
+// format) in one launch: units of one layer or a fused pair (the second's op
+// x2_op reads the first's C); second[u] == kMaxGroup for a single layer;
+// tile_end[u] the cumulative workgroup count.  A pair's layers fold side by
+// side (their splits add up to at most kMaxSplitWaves); `waves` = the
+// largest wave count of a unit.
+constexpr uint32_t kMaxGroup = HB_MAX_GROUP;
+struct SplitGroup {
+  GemmArgs g[kMaxGroup];
+  uint32_t units;
+  uint32_t tile_end[kMaxGroup], first[kMaxGroup], second[kMaxGroup], x2_op[kMaxGroup];
+};
+hipError_t LaunchSplitGroup(const SplitGroup& grp, uint32_t waves, hipStream_t stream);
 // Exact tile kernel grid for a linear layer (column tiles, row tiles).
 void ExactGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy);
 // Deferred epilogue (hb_vec.hip): reads args.ws, writes C and q_out.

@@ -393,16 +393,24 @@ struct RawSplit {
   uint32_t nib;  // 0x0F0F0F0F, or 0 for a block past the range (adds zero)
 };
 
-constexpr int kMaxSplitWaves = 8;
+typedef float f32x16s __attribute__((ext_vector_type(16)));
+
+// One layer's tile of a split launch, called by the waves of the workgroup
+// that fold it (`split`: the wave's K range; a wave past the layer's splits
+// folds nothing).  The partials meet in part / flag (LDS, [split][e][lane])
+// and the wave of split 0 finishes the tile.  A fused pair (`pair`) is two
+// layers of one tile whose waves fold at the same time: the first layer's
+// finisher leaves its values in y_lds ([e][lane]), and after a second
+// barrier the second layer's finisher reads them from x2_lds as op x2_op's
+// [m][n] operand.  Every wave of the workgroup calls this once (barriers).
 template <bool kW8, bool kMulti>
-__global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
+__device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint32_t split,
+                                          float (*lds_part)[16 * 64], uint32_t* lds_flag,
+                                          bool pair, float* y_lds, const float* x2_lds,
+                                          uint32_t x2_op) {
   constexpr int kWP = kW8 ? 2 : 1;
-  typedef float f32x16 __attribute__((ext_vector_type(16)));
-  __shared__ float lds_part[kMaxSplitWaves][16 * 64];  // [split][e][lane]
-  __shared__ uint32_t lds_flag[kMaxSplitWaves];
+  typedef f32x16s f32x16;
   const uint32_t lane = threadIdx.x & 63;
-  const uint32_t tile = blockIdx.x;
-  const uint32_t split = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t col0 = (tile % g.gx) * 32, row0 = (tile / g.gx) * 32;
   const uint32_t r32 = lane & 31, hb = lane >> 5;
   const uint8_t* a = g.a;
@@ -412,7 +420,8 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
   uint32_t nblocks = 0;
   for (uint32_t p = 0; p < g.n_pieces; ++p) nblocks += g.piece_kb[p];
   const uint32_t steps = (nblocks + 1) / 2;
-  const uint32_t s_begin = split * g.split_steps, s_end = min(s_begin + g.split_steps, steps);
+  const uint32_t s_begin = split < g.splits ? split * g.split_steps : steps;
+  const uint32_t s_end = min(s_begin + g.split_steps, steps);
 
   // the lane's A row and W column (a row or column past the layer reads
   // the last one's bytes; its outputs are not stored)
@@ -508,7 +517,7 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
   }
 #pragma unroll
   for (int op = 0; op < kPreOps; ++op) {
-    if (!finisher || (uint32_t)op >= g.n_ops || !col_in) continue;
+    if (!finisher || (uint32_t)op >= g.n_ops || !col_in || (x2_lds && op == (int)x2_op)) continue;
     const uint32_t kind = g.op_kind[op];
     if (kind == kEpAddP || kind == kEpMulP) pre_v[op] = __uint_as_float(g.op_vec[op][col]);
     if (kind == kEpAdd || kind == kEpActMul) {
@@ -536,79 +545,131 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
   }
   bool slow = __builtin_amdgcn_ballot_w64(unsafe) != 0;
   f32x16 sum = acc;
-  if (g.splits > 1) {  // the waves' partials meet in LDS; wave 0 adds them in split order
+  if (blockDim.x > 64) {  // the waves' partials meet in LDS; the finisher adds them in split order
+    if (split < g.splits) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) lds_part[split][e * 64 + lane] = acc[e];
-    if (lane == 0) lds_flag[split] = slow ? 1u : 0u;
+      for (int e = 0; e < 16; ++e) lds_part[split][e * 64 + lane] = acc[e];
+      if (lane == 0) lds_flag[split] = slow ? 1u : 0u;
+    }
     __syncthreads();
-    if (!finisher) return;
-    for (uint32_t s = 1; s < g.splits; ++s) {
+    if (finisher) {
+      for (uint32_t s = 1; s < g.splits; ++s) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sum[e] += lds_part[s][e * 64 + lane];
-      slow |= lds_flag[s] != 0;
+        for (int e = 0; e < 16; ++e) sum[e] += lds_part[s][e * 64 + lane];
+        slow |= lds_flag[s] != 0;
+      }
     }
   }
-
-  uint32_t* c = g.c;
-  f32x16 y;
+  auto finish = [&]() __attribute__((always_inline)) {
+    uint32_t* c = g.c;
+    f32x16 y;
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const uint32_t row = row_of(e);
-    y[e] = pre_init[e] + sum[e] + 0.0f;
-    if (slow && col_in && (row >> 2) < g.quads)  // a scale byte left the window: exactly
-      y[e] = __uint_as_float(SlowLinear(g, a, w0, w1, __float_as_uint(pre_init[e]), row, col));
-  }
-  const uint64_t* act = g.tbuf != nullptr ? g.tbuf + 512 : nullptr;
-  for (uint32_t op = 0; op < g.n_ops; ++op) {
-    const uint32_t kind = g.op_kind[op];
-    float pv = 0.0f;
-    f32x16 x2 = {};
-    if (op < (uint32_t)kPreOps) {
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t row = row_of(e);
+      y[e] = pre_init[e] + sum[e] + 0.0f;
+      if (slow && col_in && (row >> 2) < g.quads)  // a scale byte left the window: exactly
+        y[e] = __uint_as_float(SlowLinear(g, a, w0, w1, __float_as_uint(pre_init[e]), row, col));
+    }
+    const uint64_t* act = g.tbuf != nullptr ? g.tbuf + 512 : nullptr;
+    for (uint32_t op = 0; op < g.n_ops; ++op) {
+      const uint32_t kind = g.op_kind[op];
+      float pv = 0.0f;
+      f32x16 x2 = {};
+      if (x2_lds && op == x2_op) {  // rows past m read zeros, as from memory
 #pragma unroll
-      for (int i = 0; i < kPreOps; ++i)
-        if (op == (uint32_t)i) {
-          pv = pre_v[i];
-          x2 = pre_x2[i];
+        for (int e = 0; e < 16; ++e) x2[e] = row_of(e) < g.m && col_in ? x2_lds[e * 64 + lane] : 0.0f;
+      } else if (op < (uint32_t)kPreOps) {
+#pragma unroll
+        for (int i = 0; i < kPreOps; ++i)
+          if (op == (uint32_t)i) {
+            pv = pre_v[i];
+            x2 = pre_x2[i];
+          }
+      } else if (col_in) {
+        if (kind == kEpAddP || kind == kEpMulP) pv = __uint_as_float(g.op_vec[op][col]);
+        if (kind == kEpAdd || kind == kEpActMul) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (row_of(e) < g.m) x2[e] = __uint_as_float(g.op_x2[op][(size_t)row_of(e) * g.n + col]);
         }
-    } else if (col_in) {
-      if (kind == kEpAddP || kind == kEpMulP) pv = __uint_as_float(g.op_vec[op][col]);
-      if (kind == kEpAdd || kind == kEpActMul) {
+      }
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if (row_of(e) < g.m) x2[e] = __uint_as_float(g.op_x2[op][(size_t)row_of(e) * g.n + col]);
+      for (int e = 0; e < 16; ++e) y[e] = EpApplyFast(kind, g.op_imm[op], y[e], x2[e], pv, act);
+    }
+    if (col_in) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t row = row_of(e);
+        if (row < g.m) c[(size_t)row * g.n + col] = __float_as_uint(y[e]);
       }
     }
+    if (g.q_out != nullptr) {
+      // one MXINT8 block: the row's 32 columns are the 32 lanes of this half
 #pragma unroll
-    for (int e = 0; e < 16; ++e) y[e] = EpApplyFast(kind, g.op_imm[op], y[e], x2[e], pv, act);
-  }
-  if (col_in) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const uint32_t row = row_of(e);
-      if (row < g.m) c[(size_t)row * g.n + col] = __float_as_uint(y[e]);
-    }
-  }
-  if (g.q_out != nullptr) {
-    // one MXINT8 block: the row's 32 columns are the 32 lanes of this half
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const uint32_t row = row_of(e);
-      const bool in = (row >> 2) < g.quads && col_in;
-      const uint32_t bits = __float_as_uint(y[e]);
-      uint32_t ex = in ? ExpField(bits) : 0u;
-      ex = max(ex, (uint32_t)__shfl_xor((int)ex, 1));
-      ex = max(ex, (uint32_t)__shfl_xor((int)ex, 2));
-      ex = max(ex, (uint32_t)__shfl_xor((int)ex, 4));
-      ex = max(ex, (uint32_t)__shfl_xor((int)ex, 8));
-      ex = max(ex, (uint32_t)__shfl_xor((int)ex, 16));
-      if (in) {
-        uint8_t* word = g.q_out + ((size_t)(row >> 2) * (g.n >> 5) + (col >> 5)) * kDdrWord;
-        word[(row & 3) * 32 + r32] = QuantizeElement(bits, ex);
-        if (r32 == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(ex);
-        if (r32 < 12 && (row & 3) == 0) word[132 + r32] = 0;
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t row = row_of(e);
+        const bool in = (row >> 2) < g.quads && col_in;
+        const uint32_t bits = __float_as_uint(y[e]);
+        uint32_t ex = in ? ExpField(bits) : 0u;
+        ex = max(ex, (uint32_t)__shfl_xor((int)ex, 1));
+        ex = max(ex, (uint32_t)__shfl_xor((int)ex, 2));
+        ex = max(ex, (uint32_t)__shfl_xor((int)ex, 4));
+        ex = max(ex, (uint32_t)__shfl_xor((int)ex, 8));
+        ex = max(ex, (uint32_t)__shfl_xor((int)ex, 16));
+        if (in) {
+          uint8_t* word = g.q_out + ((size_t)(row >> 2) * (g.n >> 5) + (col >> 5)) * kDdrWord;
+          word[(row & 3) * 32 + r32] = QuantizeElement(bits, ex);
+          if (r32 == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(ex);
+          if (r32 < 12 && (row & 3) == 0) word[132 + r32] = 0;
+        }
       }
     }
+    if (y_lds) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) y_lds[e * 64 + lane] = y[e];
+    }
+    };
+  // phase 0 finishes a lone layer or a pair's first; phase 1 a pair's second
+  const uint32_t my_phase = x2_lds ? 1u : 0u;
+#pragma clang loop unroll(disable)
+  for (uint32_t phase = 0; phase < (pair ? 2u : 1u); ++phase) {
+    if (phase == 1) __syncthreads();
+    if (finisher && phase == my_phase) finish();
   }
+}
+
+
+template <bool kW8, bool kMulti>
+__global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
+  __shared__ float lds_part[kMaxSplitWaves][16 * 64];
+  __shared__ uint32_t lds_flag[kMaxSplitWaves];
+  SplitTile<kW8, kMulti>(g, blockIdx.x, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lds_part,
+                         lds_flag, false, nullptr, nullptr, 0);
+}
+
+// A group of layers in one launch: unit u owns workgroups [tile_end[u - 1],
+// tile_end[u]) and is one layer, or a pair whose second layer's op x2_op
+// reads the first's C.  A pair's layers fold at the same time, the first on
+// waves [0, s1), the second on waves [s1, s1 + s2) (s = the layer's splits,
+// s1 + s2 <= kMaxSplitWaves), their partials in rows of one LDS array; the
+// first's values reach the second's finisher through LDS.
+template <bool kW8, bool kMulti>
+__global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitGroupKernel(SplitGroup grp) {
+  __shared__ float lds_part[kMaxSplitWaves][16 * 64];
+  __shared__ float lds_y[16 * 64];
+  __shared__ uint32_t lds_flag[kMaxSplitWaves];
+  uint32_t u = 0;
+  while (u + 1 < grp.units && blockIdx.x >= grp.tile_end[u]) ++u;  // uniform
+  const uint32_t tile = blockIdx.x - (u ? grp.tile_end[u - 1] : 0u);
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t second = grp.second[u];
+  const bool pair = second < kMaxGroup;
+  const uint32_t s1 = pair ? grp.g[grp.first[u]].splits : kMaxSplitWaves;
+  const bool in2 = wave >= s1;  // (a wave of the pair's second layer)
+  const uint32_t base = in2 ? s1 : 0u;
+  SplitTile<kW8, kMulti>(grp.g[in2 ? second : grp.first[u]], tile, wave - base, lds_part + base,
+                         lds_flag + base, pair, pair && !in2 ? lds_y : nullptr,
+                         in2 ? lds_y : nullptr, grp.x2_op[u]);
 }
 
 template <int kMT, bool kW8, bool kMulti>
@@ -641,16 +702,16 @@ bool SplitEligible(const GemmArgs& args, uint32_t batch) {
   return batch == 1 && args.quads * 4 <= kSplitMaxRows;
 }
 
-size_t SplitPlan(GemmArgs& args) {
-  // splits (waves) of at least 4 steps, at most kMaxSplitWaves per tile
-  constexpr uint32_t kMinSteps = 4, kMaxSplits = kMaxSplitWaves;
+size_t SplitPlan(GemmArgs& args, uint32_t max_splits) {
+  // splits (waves) of at least 4 steps, at most max_splits per tile
+  constexpr uint32_t kMinSteps = 4;
   args.gx = (args.n + 31) / 32;
   args.gy = (args.quads * 4 + 31) / 32;
   args.gz = 1;
   uint32_t nblocks = 0;
   for (uint32_t p = 0; p < args.n_pieces; ++p) nblocks += args.piece_kb[p];
   const uint32_t steps = (nblocks + 1) / 2;
-  uint32_t per = (steps + kMaxSplits - 1) / kMaxSplits;
+  uint32_t per = (steps + max_splits - 1) / max_splits;
   per = per < kMinSteps ? kMinSteps : per;
   const uint32_t splits = (steps + per - 1) / per;
   args.splits = splits;
@@ -667,6 +728,20 @@ hipError_t LaunchSplitLinear(const GemmArgs& args, hipStream_t stream) {
   } else {
     if (multi) hipLaunchKernelGGL((SplitKernel<false, true>), grid, block, 0, stream, args);
     else hipLaunchKernelGGL((SplitKernel<false, false>), grid, block, 0, stream, args);
+  }
+  return hipGetLastError();
+}
+
+hipError_t LaunchSplitGroup(const SplitGroup& grp, uint32_t waves, hipStream_t stream) {
+  const dim3 grid(grp.tile_end[grp.units - 1]), block(64 * waves);
+  const GemmArgs& g0 = grp.g[grp.first[0]];
+  const bool w8 = g0.n_planes == 2, multi = g0.n_pieces > 1;
+  if (w8) {
+    if (multi) hipLaunchKernelGGL((SplitGroupKernel<true, true>), grid, block, 0, stream, grp);
+    else hipLaunchKernelGGL((SplitGroupKernel<true, false>), grid, block, 0, stream, grp);
+  } else {
+    if (multi) hipLaunchKernelGGL((SplitGroupKernel<false, true>), grid, block, 0, stream, grp);
+    else hipLaunchKernelGGL((SplitGroupKernel<false, false>), grid, block, 0, stream, grp);
   }
   return hipGetLastError();
 }

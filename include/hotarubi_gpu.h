@@ -209,7 +209,7 @@ typedef struct hb_ep_op {
  * | HB_LINEAR_W8_PANELS (a W8 layer's planes are W8 panels from hb_pack_w8;
  * w[0] and w[1] both point at them). */
 enum { HB_LINEAR_EXACT = 0, HB_LINEAR_FAST = 1, HB_LINEAR_PANELS = 2, HB_LINEAR_W8_PANELS = 4 };
-enum { HB_MAX_PIECES = 16, HB_MAX_EP_OPS = 8 };
+enum { HB_MAX_PIECES = 16, HB_MAX_EP_OPS = 8, HB_MAX_GROUP = 4 };
 
 /* C = A x W^T as the emitted instruction sequence computes it:
  *   acc = onto ? c[r][n] : +0
@@ -288,6 +288,19 @@ int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* descs,
  * on one GPU share that GPU's array and leave their partials in it:
  * calls that overlap in time on one GPU (different streams or contexts)
  * race, so serialize them. */
+/* A group of up to HB_MAX_GROUP layers in one launch where possible (no
+ * counterpart in the reference, whose compiler emits each GEMM on its own:
+ * the caller knows which of them are independent, e.g. the q, k and v
+ * projections of one input).  The result is that of hb_linear_async on
+ * each layer in order, provided no layer reads what another writes, with
+ * one exception: a layer whose HB_EP_ACT_MUL operand x2 is an earlier
+ * layer's c over the same m x n (the gated MLP's gate over up) runs in that
+ * layer's workgroups after it and reads its values there.  Groups of fast
+ * layers of at most 160 rows of one weight format (all MXFP4 or all W8 DDR
+ * planes, one piece or all several) share one launch; any other group runs
+ * as one launch per layer, in order.  No allocation in the shared launch. */
+int hb_linear_group_async(hb_ctx* ctx, const hb_linear_desc* descs, uint32_t count);
+
 #define HB_NOALLOC_SCRATCH_BYTES (8u << 20)
 int hb_linear_noalloc_async(hb_ctx* ctx, const hb_linear_desc* descs, uint32_t count);
 

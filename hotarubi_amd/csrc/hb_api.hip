@@ -930,7 +930,8 @@ int hb_linear_group_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) 
     return HB_OK;
   }
   // Fused pairs: a later layer whose ACT_MUL reads an earlier one's C over
-  // the same m x n runs in the earlier one's workgroups, after it.
+  // the same m x n folds beside it in its workgroups and reads its values
+  // there.
   constexpr uint32_t kNone = hb::kMaxGroup;
   uint32_t partner[hb::kMaxGroup], pair_op[hb::kMaxGroup];
   bool second[hb::kMaxGroup] = {};
@@ -947,23 +948,36 @@ int hb_linear_group_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) 
           break;
         }
     }
-  uint32_t waves = 1, end = 0;
-  for (uint32_t i = 0; i < count; ++i) {
-    hb::SplitPlan(grp.g[i]);
-    grp.g[i].fast_ep = 1u;
-  }
-  for (uint32_t i = 0; i < count; ++i) {
-    if (second[i]) continue;
-    uint32_t w = grp.g[i].splits;
-    if (partner[i] != kNone) {  // a pair's layers fold side by side in one workgroup
-      hb::GemmArgs& g2 = grp.g[partner[i]];
-      if (w + g2.splits > hb::kMaxSplitWaves) {
-        hb::SplitPlan(grp.g[i], hb::kMaxSplitWaves / 2);
-        hb::SplitPlan(g2, hb::kMaxSplitWaves / 2);
+  // Split plans: a lone layer's as its own launch would take (at most
+  // kMaxSplitWaves splits), a pair's layers at most half that each (they
+  // share a workgroup).  Where the grid would not fit the CUs in one round,
+  // the caps halve (pairs first): a second round costs more than longer K
+  // ranges per wave.
+  uint32_t cap1 = hb::kMaxSplitWaves, cap2 = hb::kMaxSplitWaves / 2, waves = 1, end = 0;
+  const uint64_t cus = (uint64_t)hb::DeviceCus();
+  for (;;) {
+    waves = 1;
+    end = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+      if (second[i]) continue;
+      hb::SplitPlan(grp.g[i], partner[i] == kNone ? cap1 : cap2);
+      uint32_t w = grp.g[i].splits;
+      if (partner[i] != kNone) {
+        hb::SplitPlan(grp.g[partner[i]], cap2);
+        w += grp.g[partner[i]].splits;
       }
-      w = grp.g[i].splits + g2.splits;
+      waves = std::max(waves, w);
+      end += grp.g[i].gx * grp.g[i].gy;
     }
-    waves = std::max(waves, w);
+    const uint64_t resident = cus * std::max(1u, hb::kSplitWavesPerCu / waves);
+    if (end <= resident || (cap1 == 1 && cap2 == 1)) break;
+    if (cap2 > 1) cap2 /= 2;
+    else cap1 /= 2;
+  }
+  end = 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    grp.g[i].fast_ep = 1u;
+    if (second[i]) continue;
     const uint32_t u = grp.units++;
     end += grp.g[i].gx * grp.g[i].gy;
     grp.tile_end[u] = end;

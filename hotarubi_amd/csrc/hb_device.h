@@ -150,16 +150,18 @@ __device__ __forceinline__ float EpApplyFast(uint32_t kind, uint32_t imm, float 
   }
 }
 
-// EpApplyFast over 16 values of a lane: the kind is resolved once, each
+// EpApplyFast over N (4, 16) values of a lane: the kind is resolved once, each
 // case is a straight run.  x2 holds the op's [m][n] operand, p the vector
 // value of each element's column (P = float: one column for all 16; P =
 // f32x16_t: one per element).  kSerial keeps the 16 table lookups of an
 // activation from all being in flight at once (for callers short of
 // registers); otherwise their latencies overlap.
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-template <bool kSerial = true, typename P>
-__device__ __forceinline__ void EpApplyFast16(uint32_t kind, uint32_t imm, f32x16_t& y,
-                                              const f32x16_t& x2, const P& p, const uint64_t* t) {
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+template <bool kSerial = true, typename V, typename P>
+__device__ __forceinline__ void EpApplyFastN(uint32_t kind, uint32_t imm, V& y, const V& x2,
+                                             const P& p, const uint64_t* t) {
+  constexpr int kN = sizeof(V) / sizeof(float);
   switch (kind) {
     case kEpAddP: y = (y + p) + 0.0f; break;
     case kEpMulP: y = (y + 0.0f) * p + 0.0f; break;
@@ -168,27 +170,50 @@ __device__ __forceinline__ void EpApplyFast16(uint32_t kind, uint32_t imm, f32x1
     case kEpAdd: y = (y + x2) + 0.0f; break;
     case kEpRelu:
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int r = 0; r < kN; ++r) {
         const float prod = y[r] + 0.0f;
         y[r] = (prod > 0.0f ? prod : 0.0f) + 0.0f;
       }
       break;
     case kEpAct:
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int r = 0; r < kN; ++r) {
         y[r] = ActGateFast(y[r], t);
         if (kSerial) __builtin_amdgcn_sched_barrier(0);
       }
       break;
     case kEpActMul:
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int r = 0; r < kN; ++r) {
         y[r] = (ActGateFast(y[r], t) + 0.0f) * x2[r] + 0.0f;
         if (kSerial) __builtin_amdgcn_sched_barrier(0);
       }
       break;
     default: break;
   }
+}
+template <bool kSerial = true, typename P>
+__device__ __forceinline__ void EpApplyFast16(uint32_t kind, uint32_t imm, f32x16_t& y,
+                                              const f32x16_t& x2, const P& p, const uint64_t* t) {
+  EpApplyFastN<kSerial>(kind, imm, y, x2, p, t);
+}
+
+// Largest value over the 16 lanes of each DPP row (lanes 16r .. 16r + 15):
+// xor 1 and xor 2 (quad permutes), the half-row mirror (lane i and 7 - i of
+// each 8), the row mirror (i and 15 - i).  All four are register moves of
+// the DPP unit, with no trip through LDS.
+__device__ __forceinline__ uint32_t RowMax16(uint32_t x) {
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false));
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false));
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false));
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xF, 0xF, false));
+  return x;
+}
+// ... over the 32 lanes of each half of the wave: the two rows of a half
+// meet through one swizzle (bit mode, lane i reads lane i ^ 16 of its 32).
+__device__ __forceinline__ uint32_t HalfMax32(uint32_t x) {
+  x = RowMax16(x);
+  return max(x, (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x401F));
 }
 
 // QuantizeBlock for one token: values[32] -> bytes and scale byte.

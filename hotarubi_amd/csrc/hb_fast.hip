@@ -450,12 +450,7 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const uint32_t v = __float_as_uint(y[r]), row = row_l + row_step(r);
-          uint32_t x = ExpField(v);
-          x = max(x, (uint32_t)__shfl_xor((int)x, 1));
-          x = max(x, (uint32_t)__shfl_xor((int)x, 2));
-          x = max(x, (uint32_t)__shfl_xor((int)x, 4));
-          x = max(x, (uint32_t)__shfl_xor((int)x, 8));
-          x = max(x, (uint32_t)__shfl_xor((int)x, 16));
+          const uint32_t x = HalfMax32(ExpField(v));
           if ((row >> 2) < g.quads && blk < nb) {
             uint8_t* word = q_out + ((size_t)(row >> 2) * nb + blk) * kDdrWord;
             word[(row & 3) * 32 + (l & 31)] = QuantizeElement(v, x);

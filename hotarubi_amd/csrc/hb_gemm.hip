@@ -568,13 +568,8 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
         uint32_t emax[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          uint32_t e = max(ExpField(__float_as_uint(res[i][4 * jb + v])),
-                           ExpField(__float_as_uint(res[i][4 * jb + 4 + v])));
-          e = max(e, (uint32_t)__shfl_xor((int)e, 1));
-          e = max(e, (uint32_t)__shfl_xor((int)e, 2));
-          e = max(e, (uint32_t)__shfl_xor((int)e, 4));
-          e = max(e, (uint32_t)__shfl_xor((int)e, 8));
-          emax[v] = e;
+          emax[v] = RowMax16(max(ExpField(__float_as_uint(res[i][4 * jb + v])),
+                                 ExpField(__float_as_uint(res[i][4 * jb + 4 + v]))));
         }
         if (quad < g.quads && blk < nb) {
           uint8_t* word = q_out + ((size_t)quad * nb + blk) * kDdrWord;

@@ -281,6 +281,11 @@ hipError_t LaunchSplitLinear(const GemmArgs& args, hipStream_t stream);
 // side (their splits add up to at most kMaxSplitWaves); `waves` = the
 // largest wave count of a unit.
 constexpr uint32_t kMaxGroup = HB_MAX_GROUP;
+// Compute units of the current device (cached per device).
+int DeviceCus();
+// Waves of the split kernels one CU holds at once (2 per SIMD: they take
+// more than 128 VGPRs).
+constexpr uint32_t kSplitWavesPerCu = 8;
 struct SplitGroup {
   GemmArgs g[kMaxGroup];
   uint32_t units;

@@ -354,12 +354,7 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
       if (row < g.m) c[(size_t)row * g.n + col] = y;
     }
     if (q_out != nullptr) {
-      uint32_t e = in ? ExpField(y) : 0u;
-      e = max(e, (uint32_t)__shfl_xor((int)e, 1));
-      e = max(e, (uint32_t)__shfl_xor((int)e, 2));
-      e = max(e, (uint32_t)__shfl_xor((int)e, 4));
-      e = max(e, (uint32_t)__shfl_xor((int)e, 8));
-      e = max(e, (uint32_t)__shfl_xor((int)e, 16));
+      const uint32_t e = HalfMax32(in ? ExpField(y) : 0u);
       if (in) {
         const uint32_t nb = g.n >> 5, c32 = col & 31;
         uint8_t* word = q_out + ((size_t)(row >> 2) * nb + (col >> 5)) * kDdrWord;
@@ -397,15 +392,18 @@ typedef float f32x16s __attribute__((ext_vector_type(16)));
 
 // One layer's tile of a split launch, called by the waves of the workgroup
 // that fold it (`split`: the wave's K range; a wave past the layer's splits
-// folds nothing).  The partials meet in part / flag (LDS, [split][e][lane])
-// and the wave of split 0 finishes the tile.  A fused pair (`pair`) is two
-// layers of one tile whose waves fold at the same time: the first layer's
-// finisher leaves its values in y_lds ([e][lane]), and after a second
-// barrier the second layer's finisher reads them from x2_lds as op x2_op's
-// [m][n] operand.  Every wave of the workgroup calls this once (barriers).
+// folds nothing; nwaves: the layer's waves in the workgroup).  The
+// partials meet in part / flag (LDS, [split][e][lane]) and up to 4 of the
+// layer's waves finish the tile, 4 of each lane's 16 rows apiece.  A fused
+// pair (`pair`) is two layers of one tile whose waves fold at the same
+// time: the first layer's finishers leave its values in y_lds ([e][lane]),
+// and after a second barrier the second layer's finishers read them from
+// x2_lds as op x2_op's [m][n] operand.  Every wave of the workgroup calls
+// this once (barriers).
 template <bool kW8, bool kMulti>
 __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint32_t split,
-                                          float (*lds_part)[16 * 64], uint32_t* lds_flag,
+                                          uint32_t nwaves, float (*lds_part)[16 * 64],
+                                          uint32_t* lds_flag,
                                           bool pair, float* y_lds, const float* x2_lds,
                                           uint32_t x2_op) {
   constexpr int kWP = kW8 ? 2 : 1;
@@ -503,27 +501,34 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
   const uint32_t col = col0 + r32;
   const bool col_in = col < g.n;
   auto row_of = [&](int e) { return row0 + 8 * (e / 4) + 4 * hb + (e & 3); };
-  // The epilogue's own operands (the initial C, and the first two ops'
-  // [m][n] operand or column value) are loaded before the K loop, so the
-  // split that finishes the tile does not wait for them at the end.
+  // The epilogue is shared: the tile's 16 elements per lane form 4 groups
+  // of 4 rows (e / 4), group j finished by the layer's wave j % min(4,
+  // nwaves) (`own`: this wave's groups).  Each finisher loads its groups'
+  // own operands (the initial C, and the first two ops' [m][n] operand or
+  // column value) before the K loop, so it does not wait for them at the end.
+  const uint32_t nfin = min(nwaves, 4u);
+  uint32_t own = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) own |= j % nfin == split ? 1u << j : 0u;
+  auto owns = [&](int e) { return ((own >> (e / 4)) & 1u) != 0; };
   constexpr int kPreOps = 2;
   f32x16 pre_init = {}, pre_x2[kPreOps] = {};
   float pre_v[kPreOps] = {};
-  const bool finisher = split == 0;  // uniform: wave 0 finishes the tile
-  if (finisher && g.acc && col_in) {
+  if (g.acc && col_in) {
 #pragma unroll
     for (int e = 0; e < 16; ++e)
-      if (row_of(e) < g.m) pre_init[e] = __uint_as_float(g.c[(size_t)row_of(e) * g.n + col]);
+      if (owns(e) && row_of(e) < g.m)
+        pre_init[e] = __uint_as_float(g.c[(size_t)row_of(e) * g.n + col]);
   }
 #pragma unroll
   for (int op = 0; op < kPreOps; ++op) {
-    if (!finisher || (uint32_t)op >= g.n_ops || !col_in || (x2_lds && op == (int)x2_op)) continue;
+    if (!own || (uint32_t)op >= g.n_ops || !col_in || (x2_lds && op == (int)x2_op)) continue;
     const uint32_t kind = g.op_kind[op];
     if (kind == kEpAddP || kind == kEpMulP) pre_v[op] = __uint_as_float(g.op_vec[op][col]);
     if (kind == kEpAdd || kind == kEpActMul) {
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        if (row_of(e) < g.m)
+        if (owns(e) && row_of(e) < g.m)
           pre_x2[op][e] = __uint_as_float(g.op_x2[op][(size_t)row_of(e) * g.n + col]);
     }
   }
@@ -545,106 +550,116 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
   }
   bool slow = __builtin_amdgcn_ballot_w64(unsafe) != 0;
   f32x16 sum = acc;
-  if (blockDim.x > 64) {  // the waves' partials meet in LDS; the finisher adds them in split order
+  if (blockDim.x > 64) {  // the partials meet in LDS; each finisher adds its groups' in split order
     if (split < g.splits) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) lds_part[split][e * 64 + lane] = acc[e];
       if (lane == 0) lds_flag[split] = slow ? 1u : 0u;
     }
     __syncthreads();
-    if (finisher) {
+    if (own) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (owns(e)) sum[e] = lds_part[0][e * 64 + lane];
+      slow = lds_flag[0] != 0;
       for (uint32_t s = 1; s < g.splits; ++s) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sum[e] += lds_part[s][e * 64 + lane];
+        for (int e = 0; e < 16; ++e)
+          if (owns(e)) sum[e] += lds_part[s][e * 64 + lane];
         slow |= lds_flag[s] != 0;
       }
     }
   }
-  auto finish = [&]() __attribute__((always_inline)) {
-    uint32_t* c = g.c;
-    f32x16 y;
+  const uint64_t* act = g.tbuf != nullptr ? g.tbuf + 512 : nullptr;
+  // group j's rows: ops, C, the requantize, and (a pair's first layer) the
+  // values the second reads
+  auto finish_group = [&](auto j_c) __attribute__((always_inline)) {
+    constexpr int j = decltype(j_c)::value;
+    f32x4_t y;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
+    for (int i = 0; i < 4; ++i) {
+      const int e = 4 * j + i;
       const uint32_t row = row_of(e);
-      y[e] = pre_init[e] + sum[e] + 0.0f;
+      y[i] = pre_init[e] + sum[e] + 0.0f;
       if (slow && col_in && (row >> 2) < g.quads)  // a scale byte left the window: exactly
-        y[e] = __uint_as_float(SlowLinear(g, a, w0, w1, __float_as_uint(pre_init[e]), row, col));
+        y[i] = __uint_as_float(SlowLinear(g, a, w0, w1, __float_as_uint(pre_init[e]), row, col));
     }
-    const uint64_t* act = g.tbuf != nullptr ? g.tbuf + 512 : nullptr;
     for (uint32_t op = 0; op < g.n_ops; ++op) {
       const uint32_t kind = g.op_kind[op];
       float pv = 0.0f;
-      f32x16 x2 = {};
+      f32x4_t x2 = {};
       if (x2_lds && op == x2_op) {  // rows past m read zeros, as from memory
 #pragma unroll
-        for (int e = 0; e < 16; ++e) x2[e] = row_of(e) < g.m && col_in ? x2_lds[e * 64 + lane] : 0.0f;
+        for (int i = 0; i < 4; ++i)
+          x2[i] = row_of(4 * j + i) < g.m && col_in ? x2_lds[(4 * j + i) * 64 + lane] : 0.0f;
       } else if (op < (uint32_t)kPreOps) {
 #pragma unroll
-        for (int i = 0; i < kPreOps; ++i)
-          if (op == (uint32_t)i) {
-            pv = pre_v[i];
-            x2 = pre_x2[i];
+        for (int o = 0; o < kPreOps; ++o)
+          if (op == (uint32_t)o) {
+            pv = pre_v[o];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x2[i] = pre_x2[o][4 * j + i];
           }
       } else if (col_in) {
         if (kind == kEpAddP || kind == kEpMulP) pv = __uint_as_float(g.op_vec[op][col]);
         if (kind == kEpAdd || kind == kEpActMul) {
 #pragma unroll
-          for (int e = 0; e < 16; ++e)
-            if (row_of(e) < g.m) x2[e] = __uint_as_float(g.op_x2[op][(size_t)row_of(e) * g.n + col]);
+          for (int i = 0; i < 4; ++i)
+            if (row_of(4 * j + i) < g.m)
+              x2[i] = __uint_as_float(g.op_x2[op][(size_t)row_of(4 * j + i) * g.n + col]);
         }
       }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) y[e] = EpApplyFast(kind, g.op_imm[op], y[e], x2[e], pv, act);
+      EpApplyFastN<false>(kind, g.op_imm[op], y, x2, pv, act);
     }
     if (col_in) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const uint32_t row = row_of(e);
-        if (row < g.m) c[(size_t)row * g.n + col] = __float_as_uint(y[e]);
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t row = row_of(4 * j + i);
+        if (row < g.m) g.c[(size_t)row * g.n + col] = __float_as_uint(y[i]);
       }
     }
     if (g.q_out != nullptr) {
       // one MXINT8 block: the row's 32 columns are the 32 lanes of this half
+      uint32_t ex[4];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const uint32_t row = row_of(e);
-        const bool in = (row >> 2) < g.quads && col_in;
-        const uint32_t bits = __float_as_uint(y[e]);
-        uint32_t ex = in ? ExpField(bits) : 0u;
-        ex = max(ex, (uint32_t)__shfl_xor((int)ex, 1));
-        ex = max(ex, (uint32_t)__shfl_xor((int)ex, 2));
-        ex = max(ex, (uint32_t)__shfl_xor((int)ex, 4));
-        ex = max(ex, (uint32_t)__shfl_xor((int)ex, 8));
-        ex = max(ex, (uint32_t)__shfl_xor((int)ex, 16));
-        if (in) {
+      for (int i = 0; i < 4; ++i)
+        ex[i] = HalfMax32((row_of(4 * j + i) >> 2) < g.quads && col_in
+                              ? ExpField(__float_as_uint(y[i])) : 0u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t row = row_of(4 * j + i);
+        if ((row >> 2) < g.quads && col_in) {
           uint8_t* word = g.q_out + ((size_t)(row >> 2) * (g.n >> 5) + (col >> 5)) * kDdrWord;
-          word[(row & 3) * 32 + r32] = QuantizeElement(bits, ex);
-          if (r32 == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(ex);
+          word[(row & 3) * 32 + r32] = QuantizeElement(__float_as_uint(y[i]), ex[i]);
+          if (r32 == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(ex[i]);
           if (r32 < 12 && (row & 3) == 0) word[132 + r32] = 0;
         }
       }
     }
     if (y_lds) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) y_lds[e * 64 + lane] = y[e];
+      for (int i = 0; i < 4; ++i) y_lds[(4 * j + i) * 64 + lane] = y[i];
     }
-    };
+  };
   // phase 0 finishes a lone layer or a pair's first; phase 1 a pair's second
   const uint32_t my_phase = x2_lds ? 1u : 0u;
 #pragma clang loop unroll(disable)
   for (uint32_t phase = 0; phase < (pair ? 2u : 1u); ++phase) {
     if (phase == 1) __syncthreads();
-    if (finisher && phase == my_phase) finish();
+    if (own && phase == my_phase) {
+      UnrollS([&](auto j_c) {
+        if ((own >> decltype(j_c)::value) & 1u) finish_group(j_c);
+      }, std::make_integer_sequence<int, 4>{});
+    }
   }
 }
-
 
 template <bool kW8, bool kMulti>
 __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
   __shared__ float lds_part[kMaxSplitWaves][16 * 64];
   __shared__ uint32_t lds_flag[kMaxSplitWaves];
-  SplitTile<kW8, kMulti>(g, blockIdx.x, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lds_part,
-                         lds_flag, false, nullptr, nullptr, 0);
+  SplitTile<kW8, kMulti>(g, blockIdx.x, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+                         blockDim.x / 64, lds_part, lds_flag, false, nullptr, nullptr, 0);
 }
 
 // A group of layers in one launch: unit u owns workgroups [tile_end[u - 1],
@@ -667,9 +682,10 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitGroupKernel(SplitGro
   const uint32_t s1 = pair ? grp.g[grp.first[u]].splits : kMaxSplitWaves;
   const bool in2 = wave >= s1;  // (a wave of the pair's second layer)
   const uint32_t base = in2 ? s1 : 0u;
-  SplitTile<kW8, kMulti>(grp.g[in2 ? second : grp.first[u]], tile, wave - base, lds_part + base,
-                         lds_flag + base, pair, pair && !in2 ? lds_y : nullptr,
-                         in2 ? lds_y : nullptr, grp.x2_op[u]);
+  const uint32_t waves = blockDim.x / 64;
+  SplitTile<kW8, kMulti>(grp.g[in2 ? second : grp.first[u]], tile, wave - base,
+                         in2 ? waves - s1 : min(s1, waves), lds_part + base, lds_flag + base, pair,
+                         pair && !in2 ? lds_y : nullptr, in2 ? lds_y : nullptr, grp.x2_op[u]);
 }
 
 template <int kMT, bool kW8, bool kMulti>

@@ -577,6 +577,15 @@ __global__ __launch_bounds__(256) void UnpackW8Kernel(const uint8_t* in, uint32_
 // that do not overlap them).
 uint32_t StepCycles(int tp) { return 420u * (uint32_t)tp + 300u; }
 
+
+template <int kTP>
+void Launch(const GemmArgs& args, hipStream_t stream) {
+  hipLaunchKernelGGL(W8Kernel<kTP>, dim3(args.gx * args.gy * args.gz), dim3(256), 0, stream,
+                     args);
+}
+
+}  // namespace
+
 int DeviceCus() {
   static int cus[64] = {};
   int dev = 0;
@@ -590,14 +599,6 @@ int DeviceCus() {
   }
   return cus[dev];
 }
-
-template <int kTP>
-void Launch(const GemmArgs& args, hipStream_t stream) {
-  hipLaunchKernelGGL(W8Kernel<kTP>, dim3(args.gx * args.gy * args.gz), dim3(256), 0, stream,
-                     args);
-}
-
-}  // namespace
 
 hipError_t LaunchW8Linear(const GemmArgs& in, uint32_t batch, bool fast, hipStream_t stream) {
   GemmArgs args = in;

@@ -1,6 +1,7 @@
 """hb_linear_group_async on an MI355X: several small fast layers in one
 launch give the results of launching them one by one (bit for bit where
-every layer keeps its own K split plan), and a gated pair (gate's ACT_MUL
+every layer keeps the K split plan of its own launch; a grid that would
+not fit the CUs in one round takes fewer splits), and a gated pair (gate's ACT_MUL
 operand is up's C, tools/compiler/smolvla_expert.cpp:400-420 and
 smolvla_lm.cpp:226-245 emit them in that order) folds both layers in one
 workgroup, the gate reading up's values there.  Shapes: the SmolVLA
@@ -100,15 +101,21 @@ def test_group_expert_qkv(gpu):
     k.check_oracle()
 
 
-@pytest.mark.parametrize("m,n,kb,w8", [(50, 2048, 23, False), (141, 2560, 30, False),
-                                       (50, 736, 23, True)])
-def test_group_gated_pair(gpu, m, n, kb, w8):
+@pytest.mark.parametrize("m,n,kb,w8,bitwise", [
+    (50, 2048, 23, False, True),    # expert: 128 tiles x (3 + 3) waves, the separate plans
+    (141, 2560, 30, False, False),  # prefix: 400 tiles do not fit one round at 4 + 4 waves,
+                                    # so each layer takes 2 splits (other bits, same tolerance)
+    (50, 736, 23, True, True)])
+def test_group_gated_pair(gpu, m, n, kb, w8, bitwise):
     rng = np.random.default_rng(510 + m + kb)
     up = Layer(rng, m, n, kb, w8=w8)
     gate = Layer(rng, m, n, kb, w8=w8, quantize=True, act_mul=True, a=up.a, a_d=up.a_d)
     say("group gated pair", dict(m=m, n=n, kb=kb, w8=w8))
     sep, grp = run_both(gpu, [up, gate], {1: 0})
-    same(sep, grp)
+    if bitwise:
+        same(sep, grp)
+    else:
+        helpers.check_fast(grp[0][0], sep[0][0])
     up.check_oracle()
     gate.check_oracle(x2_bits=grp[0][0])
 

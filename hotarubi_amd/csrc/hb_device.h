@@ -198,6 +198,17 @@ __device__ __forceinline__ void EpApplyFast16(uint32_t kind, uint32_t imm, f32x1
   EpApplyFastN<kSerial>(kind, imm, y, x2, p, t);
 }
 
+// Reads one dword of every 64-byte line of a kernel argument at once, with
+// one wait for all, so the argument reads that follow (scattered over the
+// structure, many behind branches) hit the scalar cache instead of each
+// waiting for memory in turn.
+__device__ __forceinline__ void TouchArgs(const void* args, size_t bytes) {
+  const uint32_t* p = static_cast<const uint32_t*>(args);
+  uint32_t x = 0;
+  for (size_t i = 0; i < bytes / 64; ++i) x ^= p[i * 16];
+  asm volatile("; args touched %0" ::"s"(x));
+}
+
 // Largest value over the 16 lanes of each DPP row (lanes 16r .. 16r + 15):
 // xor 1 and xor 2 (quad permutes), the half-row mirror (lane i and 7 - i of
 // each 8), the row mirror (i and 15 - i).  All four are register moves of

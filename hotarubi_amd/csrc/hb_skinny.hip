@@ -511,25 +511,30 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
 #pragma unroll
   for (uint32_t j = 0; j < 4; ++j) own |= j % nfin == split ? 1u << j : 0u;
   auto owns = [&](int e) { return ((own >> (e / 4)) & 1u) != 0; };
+  // The loads are unconditional, at rows and columns clamped into the
+  // layer (a guarded load would wait for its data at once); rows past m
+  // select 0 in the epilogue.
   constexpr int kPreOps = 2;
   f32x16 pre_init = {}, pre_x2[kPreOps] = {};
   float pre_v[kPreOps] = {};
-  if (g.acc && col_in) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-      if (owns(e) && row_of(e) < g.m)
-        pre_init[e] = __uint_as_float(g.c[(size_t)row_of(e) * g.n + col]);
-  }
-#pragma unroll
-  for (int op = 0; op < kPreOps; ++op) {
-    if (!own || (uint32_t)op >= g.n_ops || !col_in || (x2_lds && op == (int)x2_op)) continue;
-    const uint32_t kind = g.op_kind[op];
-    if (kind == kEpAddP || kind == kEpMulP) pre_v[op] = __uint_as_float(g.op_vec[op][col]);
-    if (kind == kEpAdd || kind == kEpActMul) {
+  const uint32_t ccol = min(col, g.n - 1);
+  auto crow = [&](int e) { return (size_t)min(row_of(e), g.m - 1) * g.n + ccol; };
+  if (own) {
+    if (g.acc) {
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        if (owns(e) && row_of(e) < g.m)
-          pre_x2[op][e] = __uint_as_float(g.op_x2[op][(size_t)row_of(e) * g.n + col]);
+        if (owns(e)) pre_init[e] = __uint_as_float(g.c[crow(e)]);
+    }
+#pragma unroll
+    for (int op = 0; op < kPreOps; ++op) {
+      if ((uint32_t)op >= g.n_ops || (x2_lds && op == (int)x2_op)) continue;
+      const uint32_t kind = g.op_kind[op];
+      if (kind == kEpAddP || kind == kEpMulP) pre_v[op] = __uint_as_float(g.op_vec[op][ccol]);
+      if (kind == kEpAdd || kind == kEpActMul) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (owns(e)) pre_x2[op][e] = __uint_as_float(g.op_x2[op][crow(e)]);
+      }
     }
   }
 
@@ -580,9 +585,10 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
     for (int i = 0; i < 4; ++i) {
       const int e = 4 * j + i;
       const uint32_t row = row_of(e);
-      y[i] = pre_init[e] + sum[e] + 0.0f;
+      const float init = row < g.m ? pre_init[e] : 0.0f;
+      y[i] = init + sum[e] + 0.0f;
       if (slow && col_in && (row >> 2) < g.quads)  // a scale byte left the window: exactly
-        y[i] = __uint_as_float(SlowLinear(g, a, w0, w1, __float_as_uint(pre_init[e]), row, col));
+        y[i] = __uint_as_float(SlowLinear(g, a, w0, w1, __float_as_uint(init), row, col));
     }
     for (uint32_t op = 0; op < g.n_ops; ++op) {
       const uint32_t kind = g.op_kind[op];
@@ -598,7 +604,7 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
           if (op == (uint32_t)o) {
             pv = pre_v[o];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x2[i] = pre_x2[o][4 * j + i];
+            for (int i = 0; i < 4; ++i) x2[i] = row_of(4 * j + i) < g.m ? pre_x2[o][4 * j + i] : 0.0f;
           }
       } else if (col_in) {
         if (kind == kEpAddP || kind == kEpMulP) pv = __uint_as_float(g.op_vec[op][col]);
@@ -658,6 +664,7 @@ template <bool kW8, bool kMulti>
 __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
   __shared__ float lds_part[kMaxSplitWaves][16 * 64];
   __shared__ uint32_t lds_flag[kMaxSplitWaves];
+  TouchArgs(&g, sizeof g);
   SplitTile<kW8, kMulti>(g, blockIdx.x, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
                          blockDim.x / 64, lds_part, lds_flag, false, nullptr, nullptr, 0);
 }
@@ -673,6 +680,7 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitGroupKernel(SplitGro
   __shared__ float lds_part[kMaxSplitWaves][16 * 64];
   __shared__ float lds_y[16 * 64];
   __shared__ uint32_t lds_flag[kMaxSplitWaves];
+  TouchArgs(&grp.units, sizeof grp - offsetof(SplitGroup, units));
   uint32_t u = 0;
   while (u + 1 < grp.units && blockIdx.x >= grp.tile_end[u]) ++u;  // uniform
   const uint32_t tile = blockIdx.x - (u ? grp.tile_end[u - 1] : 0u);
@@ -683,7 +691,9 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitGroupKernel(SplitGro
   const bool in2 = wave >= s1;  // (a wave of the pair's second layer)
   const uint32_t base = in2 ? s1 : 0u;
   const uint32_t waves = blockDim.x / 64;
-  SplitTile<kW8, kMulti>(grp.g[in2 ? second : grp.first[u]], tile, wave - base,
+  const GemmArgs& g = grp.g[in2 ? second : grp.first[u]];
+  TouchArgs(&g, sizeof g);
+  SplitTile<kW8, kMulti>(g, tile, wave - base,
                          in2 ? waves - s1 : min(s1, waves), lds_part + base, lds_flag + base, pair,
                          pair && !in2 ? lds_y : nullptr, in2 ? lds_y : nullptr, grp.x2_op[u]);
 }

@@ -141,15 +141,16 @@ def cpu_baseline_cores(m, n, kb, budget_s=10.0):
                       f"over {threads} threads by column groups, median {t:.3f} s"}
 
 
-def counted_traffic(kernel_tag):
-    """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE, calibrated against
-    a device copy of known size), or None when no summary covers it."""
+def counted_traffic(line):
+    """HBM bytes per pass of a bench line, from the committed rocprofv3
+    counter summary (FETCH_SIZE and WRITE_SIZE over the pass's dispatches,
+    calibrated against a device copy of known size; `--profile-lines` makes
+    it), or None when the summary has no row for the line."""
     path = os.path.join(PROFILES, "hbm_traffic.txt")
     if not os.path.exists(path):
         return None
-    for line in open(path):
-        m = re.match(r"\|\s*" + re.escape(kernel_tag) + r"\s*\|.*\|\s*([0-9]+)\s*\|\s*$", line)
+    for row in open(path):
+        m = re.match(r"\|\s*" + re.escape(line) + r"\s*\|.*\|\s*([0-9]+)\s*\|\s*$", row)
         if m:
             return int(m.group(1))
     return None
@@ -798,15 +799,20 @@ def time_chain(torch, ctx, work, steps=10, graph=True):
 
 
 def time_expert_step(hb, torch, ctx, batch, mode, steps=10):
-    """Milliseconds per SmolVLA action-expert step (eager and graph)."""
+    """Milliseconds per SmolVLA action-expert step (eager and graph), with
+    its roofline over the best of the two."""
     work = ExpertStep(hb, torch, batch, mode)
     out = {"batch": batch, **time_chain(torch, ctx, work, steps)}
+    best = min(out["eager_ms"], out.get("graph_ms", out["eager_ms"]))
+    out["tops"], out["roofline"] = chain_summary(
+        work, best, "fp6_fp4", f"expert_b{batch}" if mode == hb.FAST else None)
     del work
     return out
 
 
-def chain_summary(work, ms, mfma_class):
-    """TOPS and roofline of one pass over a chain taking `ms`."""
+def chain_summary(work, ms, mfma_class, line=None):
+    """TOPS and roofline of one pass over a chain taking `ms` (traffic: the
+    counted HBM bytes per pass of bench line `line`)."""
     tops = work.ops / (ms * 1e-3) / 1e12
     gbs = work.bytes / (ms * 1e-3) / 1e9
     peak = MFMA_PEAK[mfma_class]
@@ -816,6 +822,7 @@ def chain_summary(work, ms, mfma_class):
     else:
         roof = {"bound": "mfma", "achieved": round(tops, 1), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(tops / peak, 4), "mfma_class": mfma_class}
+    roof["traffic"] = counted_traffic(line) if line else None
     return round(tops, 3), roof
 
 
@@ -848,7 +855,7 @@ def time_steps(hb, torch, ctx, stream, work, steps, warmup, settle_s=0.0):
     return t0.elapsed_time(t1) / steps
 
 
-def summarize(work, ms, mfma_class, kernel_tag=None):
+def summarize(work, ms, mfma_class, line=None):
     ops, nbytes = work.ops(), work.bytes()
     tops = ops / (ms * 1e-3) / 1e12
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -860,7 +867,7 @@ def summarize(work, ms, mfma_class, kernel_tag=None):
     else:
         roof = {"bound": "mfma", "achieved": round(tops, 1), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(tops / peak, 4)}
-    roof["traffic"] = counted_traffic(kernel_tag) if kernel_tag else None
+    roof["traffic"] = counted_traffic(line) if line else None
     return tops, roof
 
 
@@ -896,6 +903,243 @@ TOLERANCE = ("fast mode: per element |got - exact| <= 2^-17 * sum over blocks of
              "holds on N(0,1) data); exact mode: bitwise")
 
 
+# Bench lines that --line runs alone (the counter and trace runs of
+# --profile-lines): name -> (description, builder).  A builder returns an
+# object with run(ctx), ops() / bytes() per pass.
+class BatchedLine:
+    def __init__(self, hb, work):
+        self.hb, self.work = hb, work
+
+    def run(self, ctx):
+        self.hb.linear_batched(self.work.descs, ctx)
+
+    def ops(self):
+        return self.work.ops()
+
+    def bytes(self):
+        return self.work.bytes()
+
+
+class ChainLine:
+    def __init__(self, work):
+        self.work = work
+
+    def run(self, ctx):
+        self.work.run(ctx)
+
+    def ops(self):
+        return self.work.ops
+
+    def bytes(self):
+        return self.work.bytes
+
+
+def bench_lines(hb, torch, ctx):
+    n, kb = 960, 80
+    F, E = hb.FAST, hb.EXACT
+
+    def wl(*a, **k):
+        return lambda: BatchedLine(hb, Workload(hb, torch, ctx, *a, **k))
+
+    return {
+        "headline_fast": ("MXFP4 M=128 K=2560 N=960 x256 layers, fast, weights in panels",
+                          wl(128, n, kb, False, 256, F, panels=True)),
+        "headline_exact": ("MXFP4 M=128 K=2560 N=960 x256 layers, exact, DDR words",
+                           wl(128, n, kb, False, 256, E)),
+        "sweep_m1": ("MXFP4 M=1 K=2560 N=960 x256 layers, fast, DDR words",
+                     wl(1, n, kb, False, 256, F, seed=3)),
+        "sweep_m16": ("MXFP4 M=16 K=2560 N=960 x256 layers, fast, DDR words",
+                      wl(16, n, kb, False, 256, F, seed=3)),
+        "sweep_m1024": ("MXFP4 M=1024 K=2560 N=960 x64 layers, fast, weights in panels",
+                        wl(1024, n, kb, False, 64, F, seed=3, panels=True)),
+        "w8_fast": ("W8 M=64 K=960 N=2560 + MULP + ADDP x128 layers, fast",
+                    wl(64, 2560, 30, True, 128, F, epilogue=True, seed=4)),
+        "w8_exact": ("W8 M=64 K=960 N=2560 + MULP + ADDP x128 layers, exact",
+                     wl(64, 2560, 30, True, 128, E, epilogue=True, seed=4)),
+        "siglip_fast": ("SigLIP-style W8 set, 12 layers x 4 GEMMs, M=2048, fast, W8 panels",
+                        lambda: ChainLine(SiglipSet(hb, torch, F, w8_panels=True))),
+        "siglip_exact": ("SigLIP-style W8 set, 12 layers x 4 GEMMs, M=2048, exact, DDR words",
+                         lambda: ChainLine(SiglipSet(hb, torch, E))),
+        "sparsedrive_fast": ("SparseDrive-S stage-1 im2col M=67584 K=576 N=64, MXFP4, fast",
+                             lambda: ChainLine(SparseDriveConv(hb, torch, F))),
+        "sparsedrive_exact": ("SparseDrive-S stage-1 im2col M=67584 K=576 N=64, MXFP4, exact",
+                              lambda: ChainLine(SparseDriveConv(hb, torch, E))),
+        "expert_b1": ("SmolVLA action-expert step GEMM chain, B=1 (M=50), fast, grouped",
+                      lambda: ChainLine(ExpertStep(hb, torch, 1, F))),
+        "expert_b32": ("SmolVLA action-expert step GEMM chain, B=32 (M=1600), fast, grouped",
+                       lambda: ChainLine(ExpertStep(hb, torch, 32, F))),
+        "prefix_b1": ("SmolVLA LM prefix GEMM chain, B=1 (M=141), fast, grouped",
+                      lambda: ChainLine(PrefixStep(hb, torch, 1, F))),
+        "prefix_b32": ("SmolVLA LM prefix GEMM chain, B=32 (M=4512), fast, grouped",
+                       lambda: ChainLine(PrefixStep(hb, torch, 32, F))),
+    }
+
+
+def run_line(args):
+    """--line NAME: build that line's workload, copy --copy-probe MiB (the
+    counters' calibration, and the marker after which the line's own
+    dispatches start), run --steps passes, print one JSON line."""
+    import torch
+    import hotarubi_amd as hb
+    ctx = hb.Context(0)
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    desc, make = bench_lines(hb, torch, ctx)[args.line]
+    work = make()
+    torch.cuda.synchronize()
+    x = torch.ones(max(args.copy_probe, 1) << 20, dtype=torch.uint8, device="cuda:0")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    del x, y
+    for _ in range(args.steps):
+        work.run(ctx)
+    torch.cuda.synchronize()
+    print(json.dumps({"line": args.line, "workload": desc, "passes": args.steps,
+                      "ops_per_pass": work.ops(), "bytes_per_pass": work.bytes()}), flush=True)
+    ctx.close()
+
+
+SQ_COUNTERS = ["GRBM_GUI_ACTIVE", "SQ_WAVES", "SQ_BUSY_CYCLES", "SQ_WAVE_CYCLES",
+               "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_LDS",
+               "SQ_WAIT_INST_ANY"]
+
+
+def profile_lines(args):
+    """--profile-lines A,B,...: for each line, four rocprofv3 runs of
+    `bench.py --line` as child processes (kernel trace, FETCH_SIZE,
+    WRITE_SIZE, SQ counters), each its own pass; writes one summary per line
+    and the traffic rows into --profile-out."""
+    import csv
+    import subprocess
+    out_dir = os.path.abspath(args.profile_out)
+    os.makedirs(out_dir, exist_ok=True)
+    env = dict(os.environ, TMPDIR="/tmp")
+    me = os.path.abspath(__file__)
+    rows = []
+    for line in args.profile_lines.split(","):
+        res = {}
+        for kind, prof in (("trace", ["--kernel-trace", "--stats"]),
+                           ("fetch", ["--pmc", "FETCH_SIZE"]), ("write", ["--pmc", "WRITE_SIZE"]),
+                           ("sq", ["--pmc"] + SQ_COUNTERS)):
+            d = os.path.join(out_dir, "raw", f"{line}_{kind}")
+            cmd = ["timeout", "-s", "KILL", "150", "rocprofv3", *prof, "--output-format", "csv",
+                   "-d", d, "-o", "run", "--", sys.executable, me, "--line", line,
+                   "--steps", str(args.steps), "--copy-probe", "256"]
+            print(f"profile {line} {kind}", flush=True)
+            r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True)
+            info = [json.loads(t) for t in r.stdout.splitlines() if t.startswith('{"line"')]
+            if r.returncode != 0 or not info:
+                print(r.stdout[-2000:], r.stderr[-2000:], file=sys.stderr)
+                sys.exit(f"rocprofv3 run failed: {line} {kind} (exit {r.returncode})")
+            res["info"] = info[-1]
+            name = "run_kernel_trace.csv" if kind == "trace" else "run_counter_collection.csv"
+            recs = list(csv.DictReader(open(os.path.join(d, name))))
+            res[kind] = recs
+        rows.append(summarize_profile(line, res, out_dir))
+    with open(os.path.join(out_dir, "traffic_rows.md"), "w") as f:
+        for r in rows:
+            f.write(r + "\n")
+
+
+def _dispatches_after_probe(recs, key="Dispatch_Id"):
+    """The records of the dispatches after the last device copy of the
+    probe (the line's passes), grouped by dispatch, in order."""
+    by = {}
+    for r in recs:
+        by.setdefault(int(r[key]), []).append(r)
+    ids = sorted(by)
+    probe = [i for i in ids if "copyBuffer" in by[i][0]["Kernel_Name"]]
+    last = probe[-1] if probe else -1
+    return [by[i] for i in ids if i > last], [by[i] for i in probe[-3:]]
+
+
+def summarize_profile(line, res, out_dir):
+    info = res["info"]
+    passes = info["passes"]
+    # trace: per kernel, time over the passes
+    recs, _ = _dispatches_after_probe(res["trace"])
+    per = {}
+    for grp in recs:
+        r = grp[0]
+        k = r["Kernel_Name"].replace("hb::(anonymous namespace)::", "").replace("void ", "")
+        k = re.sub(r"\(.*", "", k)
+        t = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+        e = per.setdefault(k, [0, 0.0])
+        e[0] += 1
+        e[1] += t
+    total_us = sum(v[1] for v in per.values())
+    span = [(int(g[0]["Start_Timestamp"]), int(g[0]["End_Timestamp"])) for g in recs]
+    wall_us = (max(b for _, b in span) - min(a for a, _ in span)) / 1000.0 if span else 0.0
+    top = sorted(per.items(), key=lambda kv: -kv[1][1])
+
+    def counter_sum(kind, name):
+        recs_k, probe = _dispatches_after_probe(res[kind])
+        tot = sum(float(r["Counter_Value"]) for g in recs_k for r in g if r["Counter_Name"] == name)
+        pr = [sum(float(r["Counter_Value"]) for r in g if r["Counter_Name"] == name) for g in probe]
+        return tot / passes, (sum(pr) / len(pr) if pr else 0.0)
+
+    fetch, fetch_probe = counter_sum("fetch", "FETCH_SIZE")
+    write, write_probe = counter_sum("write", "WRITE_SIZE")
+    copy_kib = 256 * 1024
+    f_read = copy_kib / fetch_probe if fetch_probe else float("nan")
+    f_write = copy_kib / write_probe if write_probe else float("nan")
+    read_b, write_b = fetch * 1024 * f_read, write * 1024 * f_write
+    traffic = int(round(read_b + write_b))
+    alg = info["bytes_per_pass"]
+    sq = {c: counter_sum("sq", c)[0] for c in SQ_COUNTERS}
+    cycles = sq["GRBM_GUI_ACTIVE"] / 8.0  # per XCD, summed over the 8
+    simds = 1024.0
+    waves = max(sq["SQ_WAVES"], 1.0)
+    lines = [
+        f"# {top[0][0] if top else '?'} — {info['workload']}",
+        "",
+        "Commands (each a child process of the first; run from `/tmp`, `TMPDIR=/tmp`):",
+        "",
+        f"    python3 bench.py --profile-lines {line} --profile-out <dir> --steps {passes}",
+        f"    rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- \\",
+        f"        python3 bench.py --line {line} --steps {passes} --copy-probe 256",
+        f"    rocprofv3 --pmc FETCH_SIZE ... (same program), then --pmc WRITE_SIZE, then",
+        f"    rocprofv3 --pmc {' '.join(SQ_COUNTERS)} ...",
+        "",
+        f"Per pass ({passes} passes after the 256 MiB copy probe): "
+        f"{len(recs) // max(passes, 1)} dispatches, "
+        f"{total_us / passes:.1f} us of kernel time, {wall_us / passes:.1f} us first start to "
+        f"last end.",
+        "",
+        "| kernel | dispatches | total us | avg us | share |",
+        "|---|---|---|---|---|",
+    ]
+    for k, (c, t) in top[:8]:
+        lines.append(f"| `{k}` | {c} | {t:.1f} | {t / c:.2f} | {t / total_us:.1%} |")
+    lines += [
+        "",
+        f"HBM traffic per pass (calibration: the probe's 256 MiB copy reads FETCH_SIZE "
+        f"{fetch_probe:.1f} KiB, writes WRITE_SIZE {write_probe:.1f} KiB; factors "
+        f"{f_read:.5f} / {f_write:.5f}): read {read_b / 1e6:.2f} MB, written "
+        f"{write_b / 1e6:.2f} MB, total {traffic / 1e6:.2f} MB against {alg / 1e6:.2f} MB "
+        f"algorithmic (x{traffic / alg:.3f}).",
+        "",
+        f"SQ counters per pass (summed over the chip; `GRBM_GUI_ACTIVE` per XCD, summed over "
+        f"8: {cycles:.0f} cycles):",
+        "",
+        f"- waves {sq['SQ_WAVES']:.0f}; VALU instructions per wave "
+        f"{sq['SQ_INSTS_VALU'] / waves:.0f}; MFMA instructions per wave "
+        f"{sq['SQ_INSTS_MFMA'] / waves:.0f}; LDS instructions per wave "
+        f"{sq['SQ_INSTS_LDS'] / waves:.0f}",
+        f"- matrix cores busy {sq['SQ_VALU_MFMA_BUSY_CYCLES'] / simds / max(cycles, 1):.1%} of "
+        f"the busy cycles per SIMD ({sq['SQ_VALU_MFMA_BUSY_CYCLES'] / simds:.0f} of "
+        f"{cycles:.0f})",
+        f"- a wave lives {sq['SQ_WAVE_CYCLES'] / waves:.0f} cycles on average, waiting on "
+        f"instruction issue dependencies (`SQ_WAIT_INST_ANY`) "
+        f"{sq['SQ_WAIT_INST_ANY'] / max(sq['SQ_WAVE_CYCLES'], 1):.1%} of them",
+    ]
+    with open(os.path.join(out_dir, f"{line}.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    return (f"| {line} | {top[0][0] if top else '?'} | {passes} | {fetch:.1f} | {write:.1f} | "
+            f"{int(read_b)} | {int(write_b)} | {traffic} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -911,7 +1155,17 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     ap.add_argument("--settle", type=float, default=0.5, metavar="S",
                     help="seconds of untimed headline steps before the warmup (0: none)")
+    ap.add_argument("--line", default=None, help="run one bench line's workload alone")
+    ap.add_argument("--profile-lines", default=None, metavar="A,B,...",
+                    help="rocprofv3 trace and counter runs of these lines (child processes)")
+    ap.add_argument("--profile-out", default="gpurun_out/lines")
     args = ap.parse_args()
+    if args.profile_lines:
+        profile_lines(args)
+        return
+    if args.line:
+        run_line(args)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}); nothing in this build "
               "spans several GPUs.", file=sys.stderr)
@@ -939,9 +1193,9 @@ def main():
     # the exact kernel reads DDR words)
     work = Workload(hb, torch, ctx, args.m, n, kb, False, args.layers, mode, panels=fast)
     ms = time_steps(hb, torch, ctx, stream, work, args.steps, args.warmup, settle_s=args.settle)
-    tag = "StreamKernel" if fast else "GemmTileKernel<linear,128,128>"
+    std = args.m == 128 and args.layers == 256  # the shape the counter runs cover
     tops, roof = summarize(work, ms, "fp6_fp4" if fast else "bf16",
-                           tag if (args.m == 128 and args.layers == 256) else None)
+                           ("headline_fast" if fast else "headline_exact") if std else None)
     del work
 
     out = {
@@ -976,7 +1230,8 @@ def main():
         w2 = Workload(hb, torch, ctx, args.m, n, kb, False, args.layers, other,
                       panels=other == hb.FAST)
         ms2 = time_steps(hb, torch, ctx, stream, w2, extra_steps, extra_warm, settle_s=0.2)
-        t2, r2 = summarize(w2, ms2, "bf16" if fast else "fp6_fp4")
+        t2, r2 = summarize(w2, ms2, "bf16" if fast else "fp6_fp4",
+                           ("headline_exact" if fast else "headline_fast") if std else None)
         out["exact" if fast else "fast"] = {"value": round(t2, 3), "unit": "TOPS",
                                             "ms_per_step": round(ms2, 4), "roofline": r2}
         del w2
@@ -987,7 +1242,7 @@ def main():
         for m, L, pan in ((1, 256, False), (16, 256, False), (1024, 64, True)):
             ws = Workload(hb, torch, ctx, m, n, kb, False, L, hb.FAST, seed=3, panels=pan)
             mss = time_steps(hb, torch, ctx, stream, ws, extra_steps, extra_warm, settle_s=0.2)
-            ts, rs = summarize(ws, mss, "fp6_fp4")
+            ts, rs = summarize(ws, mss, "fp6_fp4", f"sweep_m{m}")
             sweep[f"M={m}"] = {"value": round(ts, 3), "unit": "TOPS", "layers": L,
                                "weights": "panels" if pan else "DDR words",
                                "ms_per_step": round(mss, 4), "roofline": rs}
@@ -1007,7 +1262,7 @@ def main():
         for name, md, cls in (("fast", hb.FAST, "int8"), ("exact", hb.EXACT, "bf16")):
             wk = Workload(hb, torch, ctx, 64, 2560, 30, True, L8, md, epilogue=True, seed=4)
             ms8 = time_steps(hb, torch, ctx, stream, wk, extra_steps, extra_warm, settle_s=0.2)
-            t8, r8 = summarize(wk, ms8, cls)
+            t8, r8 = summarize(wk, ms8, cls, f"w8_{name}")
             w8[name] = {"value": round(t8, 3), "unit": "TOPS", "ms_per_step": round(ms8, 4),
                         "roofline": r8}
             del wk
@@ -1017,19 +1272,19 @@ def main():
         # over W8 panels, the weights' layout for large-M W8 layers, exact
         # mode over DDR words) and the SparseDrive-S stage-1 3x3 im2col GEMM
         # (MXFP4), fast and exact
-        for key, desc, cls_fast, make in (
-                ("siglip_w8_set", "W8 SigLIP-style encoder: 12 layers x {QKV 768->2304, out "
+        for key, short, desc, cls_fast, make in (
+                ("siglip_w8_set", "siglip", "W8 SigLIP-style encoder: 12 layers x {QKV 768->2304, out "
                  "768->768, up 768->3072 + GELU + requantize, down 3072->768}, M=2048, "
                  "MULP + ADDP; fast: W8 panels, exact: DDR words", "int8",
                  lambda md: SiglipSet(hb, torch, md, w8_panels=md == hb.FAST)),
-                ("sparsedrive_stage1_conv_mxfp4", "MXFP4 im2col GEMM M=67584 K=576 N=64 "
+                ("sparsedrive_stage1_conv_mxfp4", "sparsedrive", "MXFP4 im2col GEMM M=67584 K=576 N=64 "
                  "(SparseDrive-S stage-1 3x3 conv, 6 cameras)", "fp6_fp4",
                  lambda md: SparseDriveConv(hb, torch, md))):
             rec = {}
             for name, md, cls in (("fast", hb.FAST, cls_fast), ("exact", hb.EXACT, "bf16")):
                 wk = make(md)
                 t = time_chain(torch, ctx, wk, steps=5, graph=False)
-                tops, roof = chain_summary(wk, t["eager_ms"], cls)
+                tops, roof = chain_summary(wk, t["eager_ms"], cls, f"{short}_{name}")
                 rec[name] = {"value": tops, "unit": "TOPS", "ms_per_pass": t["eager_ms"],
                              "gemms": t["gemms"], "m": t["m"], "roofline": roof}
                 del wk
@@ -1057,7 +1312,7 @@ def main():
             wk = PrefixStep(hb, torch, b, mode)
             t = time_chain(torch, ctx, wk, steps=5)
             best = min(t["eager_ms"], t.get("graph_ms", t["eager_ms"]))
-            tops, roof = chain_summary(wk, best, "fp6_fp4")
+            tops, roof = chain_summary(wk, best, "fp6_fp4", f"prefix_b{b}" if fast else None)
             prefix[f"B={b}"] = {**t, "tops": tops, "roofline": roof}
             del wk
         ctx.set_stream(stream.cuda_stream)

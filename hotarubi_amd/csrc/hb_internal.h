@@ -190,16 +190,22 @@ void FreeWorkspace(Workspace& ws);
 // Workgroup -> tile mapping.  The hardware deals workgroups round-robin over
 // the 8 XCDs, each with its own L2; remapping puts consecutive logical tiles
 // (x fastest, then y, then layer z) on one XCD, so the workgroups that share
-// a layer's weights and activations share an L2.
+// a layer's weights and activations share an L2 (XcdLogical).
 constexpr uint32_t kXcds = 8;
 struct TileId {
   uint32_t x, y, z;
 };
+// Any count of workgroups: XCD x (blocks b with b % 8 == x, the hardware's
+// deal) takes the contiguous run of logical indices [x q + min(x, r),
+// + q + (x < r)), q = total / 8, r = total % 8 -- a bijection, so the
+// logical neighbours of a block sit on its XCD and share its L2.
+__device__ __forceinline__ uint32_t XcdLogical(uint32_t b, uint32_t total) {
+  const uint32_t x = b % kXcds, q = total / kXcds, r = total % kXcds;
+  return x * q + min(x, r) + b / kXcds;
+}
+
 __device__ __forceinline__ TileId LogicalTile(uint32_t gx, uint32_t gy, uint32_t gz) {
-  const uint32_t b = blockIdx.x;
-  const uint32_t total = gx * gy * gz;
-  uint32_t l = b;
-  if (total % kXcds == 0) l = (b % kXcds) * (total / kXcds) + b / kXcds;
+  const uint32_t l = XcdLogical(blockIdx.x, gx * gy * gz);
   TileId t;
   t.x = l % gx;
   t.y = (l / gx) % gy;

@@ -409,7 +409,9 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
   constexpr int kWP = kW8 ? 2 : 1;
   typedef f32x16s f32x16;
   const uint32_t lane = threadIdx.x & 63;
-  const uint32_t col0 = (tile % g.gx) * 32, row0 = (tile / g.gx) * 32;
+  // logical tiles run row tiles fastest: the workgroups of one column tile
+  // (which read the same weights) are neighbours, on one XCD
+  const uint32_t col0 = (tile / g.gy) * 32, row0 = (tile % g.gy) * 32;
   const uint32_t r32 = lane & 31, hb = lane >> 5;
   const uint8_t* a = g.a;
   const uint8_t* w0 = g.w[0];
@@ -665,7 +667,8 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
   __shared__ float lds_part[kMaxSplitWaves][16 * 64];
   __shared__ uint32_t lds_flag[kMaxSplitWaves];
   TouchArgs(&g, sizeof g);
-  SplitTile<kW8, kMulti>(g, blockIdx.x, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+  SplitTile<kW8, kMulti>(g, XcdLogical(blockIdx.x, gridDim.x),
+                         __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
                          blockDim.x / 64, lds_part, lds_flag, false, nullptr, nullptr, 0);
 }
 
@@ -681,9 +684,10 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitGroupKernel(SplitGro
   __shared__ float lds_y[16 * 64];
   __shared__ uint32_t lds_flag[kMaxSplitWaves];
   TouchArgs(&grp.units, sizeof grp - offsetof(SplitGroup, units));
+  const uint32_t l = XcdLogical(blockIdx.x, gridDim.x);
   uint32_t u = 0;
-  while (u + 1 < grp.units && blockIdx.x >= grp.tile_end[u]) ++u;  // uniform
-  const uint32_t tile = blockIdx.x - (u ? grp.tile_end[u - 1] : 0u);
+  while (u + 1 < grp.units && l >= grp.tile_end[u]) ++u;  // uniform
+  const uint32_t tile = l - (u ? grp.tile_end[u - 1] : 0u);
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t second = grp.second[u];
   const bool pair = second < kMaxGroup;

@@ -1011,6 +1011,7 @@ def profile_lines(args):
     WRITE_SIZE, SQ counters), each its own pass; writes one summary per line
     and the traffic rows into --profile-out."""
     import csv
+    import shutil
     import subprocess
     out_dir = os.path.abspath(args.profile_out)
     os.makedirs(out_dir, exist_ok=True)
@@ -1037,6 +1038,7 @@ def profile_lines(args):
             recs = list(csv.DictReader(open(os.path.join(d, name))))
             res[kind] = recs
         rows.append(summarize_profile(line, res, out_dir))
+        shutil.rmtree(os.path.join(out_dir, "raw"), ignore_errors=True)  # the CSVs are large
     with open(os.path.join(out_dir, "traffic_rows.md"), "w") as f:
         for r in rows:
             f.write(r + "\n")
@@ -1090,6 +1092,14 @@ def summarize_profile(line, res, out_dir):
     sq = {c: counter_sum("sq", c)[0] for c in SQ_COUNTERS}
     cycles = sq["GRBM_GUI_ACTIVE"] / 8.0  # per XCD, summed over the 8
     simds = 1024.0
+    # The clock over the line's kernel time; under the counter profiler a
+    # short dispatch's GRBM window also covers the profiler's own work, so
+    # lines of many short dispatches fall back to the 2.4 GHz peak clock.
+    ghz = cycles / (total_us / passes) / 1e3 if total_us else 0.0
+    clock_note = f"{ghz:.2f} GHz from GRBM_GUI_ACTIVE"
+    if not 1.0 <= ghz <= 2.6:
+        ghz, clock_note = 2.4, "2.4 GHz peak clock (GRBM_GUI_ACTIVE spans the profiler's gaps)"
+    kernel_cycles = total_us / passes * ghz * 1e3
     waves = max(sq["SQ_WAVES"], 1.0)
     lines = [
         f"# {top[0][0] if top else '?'} — {info['workload']}",
@@ -1127,14 +1137,15 @@ def summarize_profile(line, res, out_dir):
         f"{sq['SQ_INSTS_VALU'] / waves:.0f}; MFMA instructions per wave "
         f"{sq['SQ_INSTS_MFMA'] / waves:.0f}; LDS instructions per wave "
         f"{sq['SQ_INSTS_LDS'] / waves:.0f}",
-        f"- matrix cores busy {sq['SQ_VALU_MFMA_BUSY_CYCLES'] / simds / max(cycles, 1):.1%} of "
-        f"the busy cycles per SIMD ({sq['SQ_VALU_MFMA_BUSY_CYCLES'] / simds:.0f} of "
-        f"{cycles:.0f})",
+        f"- matrix cores busy {sq['SQ_VALU_MFMA_BUSY_CYCLES'] / simds / max(kernel_cycles, 1):.1%}"
+        f" of the kernel time per SIMD ({sq['SQ_VALU_MFMA_BUSY_CYCLES'] / simds:.0f} of "
+        f"{kernel_cycles:.0f} cycles at {clock_note})",
         f"- a wave lives {sq['SQ_WAVE_CYCLES'] / waves:.0f} cycles on average, waiting on "
         f"instruction issue dependencies (`SQ_WAIT_INST_ANY`) "
         f"{sq['SQ_WAIT_INST_ANY'] / max(sq['SQ_WAVE_CYCLES'], 1):.1%} of them",
     ]
-    with open(os.path.join(out_dir, f"{line}.md"), "w") as f:
+    kname = re.sub(r"<.*", "", top[0][0]).lower() if top else "kernels"
+    with open(os.path.join(out_dir, f"{kname}_{line}.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     return (f"| {line} | {top[0][0] if top else '?'} | {passes} | {fetch:.1f} | {write:.1f} | "
             f"{int(read_b)} | {int(write_b)} | {traffic} |")

@@ -74,6 +74,8 @@ struct GemmArgs {
   // W8 layer over FP6 W8 panels (HB_LINEAR_W8_PANELS): w[0] = w[1] = the
   // panels of both planes
   uint32_t w_fp6;
+  // tile order of BandTile: column tiles in bands of this width (0: LogicalTile)
+  uint32_t band;
 };
 
 // Weight panels (hb_pack_weights): one plane of n columns x kb_total
@@ -212,6 +214,27 @@ __device__ __forceinline__ TileId LogicalTile(uint32_t gx, uint32_t gy, uint32_t
   t.z = l / (gx * gy);
   return t;
 }
+
+// Tile order for grids that re-read operands: logical tiles run over bands
+// of `band` column tiles, row tiles within a band, so the contiguous run of
+// tiles an XCD takes (XcdLogical) is about run / band row tiles by `band`
+// column tiles -- a rectangle, whose A rows and W columns its L2 fetches once.
+__device__ __forceinline__ TileId BandTile(uint32_t gx, uint32_t gy, uint32_t gz, uint32_t band) {
+  const uint32_t l = XcdLogical(blockIdx.x, gx * gy * gz);
+  band = band ? band : gx;  // 0: whole rows of column tiles, as LogicalTile
+  const uint32_t per = gx * gy, li = l % per, b0 = li / (gy * band) * band;
+  const uint32_t w = min(band, gx - b0), in = li - b0 * gy;
+  TileId t;
+  t.x = b0 + in % w;
+  t.y = in / w;
+  t.z = l / per;
+  return t;
+}
+// The band width that minimizes the A and W bytes the XCDs fetch: an XCD's
+// run of about tiles / 8 is rows x band, fetching rows x a_tile + band x
+// w_tile (a_tile, w_tile: the A bytes of a row tile, the W bytes of a column
+// tile).
+uint32_t BandFor(uint32_t gx, uint32_t gy, uint64_t a_tile, uint64_t w_tile);
 
 // Launchers (hb_gemm.hip).
 hipError_t LaunchGemmInstr(const GemmArgs& args, hipStream_t stream);

@@ -32,6 +32,7 @@
 // After the K loop the ring is free: the outputs are staged there per wave,
 // with the activation table, and the epilogue (ops, C, requantize) runs per
 // 32-column tile.
+#include <algorithm>
 #include <utility>
 
 #include "hb_device.h"
@@ -94,7 +95,7 @@ void W8Kernel(GemmArgs g) {
   constexpr uint32_t kSlot = C::kSlot;
   __shared__ __attribute__((aligned(16))) uint8_t lds_ring[kD * kSlot];
 
-  const TileId tile = LogicalTile(g.gx, g.gy, g.gz);
+  const TileId tile = BandTile(g.gx, g.gy, g.gz, g.band);
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t steps = g.w_steps, nblocks = g.kb_total;
@@ -586,6 +587,22 @@ void Launch(const GemmArgs& args, hipStream_t stream) {
 
 }  // namespace
 
+uint32_t BandFor(uint32_t gx, uint32_t gy, uint64_t a_tile, uint64_t w_tile) {
+  const uint64_t run = std::max<uint64_t>(1, (uint64_t)gx * gy / kXcds);
+  uint32_t best = gx;
+  uint64_t best_bytes = ~0ull;
+  for (uint32_t b = 1; b <= gx; ++b) {
+    const uint64_t rows = std::min<uint64_t>(gy, (run + b - 1) / b);
+    const uint64_t cols = std::min<uint64_t>(b, run);
+    const uint64_t bytes = rows * a_tile + cols * w_tile;
+    if (bytes < best_bytes) {
+      best_bytes = bytes;
+      best = b;
+    }
+  }
+  return best;
+}
+
 int DeviceCus() {
   static int cus[64] = {};
   int dev = 0;
@@ -624,6 +641,10 @@ hipError_t LaunchW8Linear(const GemmArgs& in, uint32_t batch, bool fast, hipStre
   }
   args.gx = (n_panels + best - 1) / best;
   if ((uint64_t)args.gx * args.gy * args.gz >= (1ull << 31)) return hipErrorInvalidValue;
+  // A row tile: kBM rows x kb_total blocks of 36 bytes (32 codes, a scale);
+  // a column tile: `best` panels of w_steps chunks
+  args.band = BandFor(args.gx, args.gy, (uint64_t)kBM * args.kb_total * 36,
+                      (uint64_t)best * args.w_steps * kW8Chunk);
   if (best == 4) Launch<4>(args, stream);
   else if (best == 3) Launch<3>(args, stream);
   else Launch<2>(args, stream);

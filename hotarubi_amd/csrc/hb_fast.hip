@@ -39,6 +39,7 @@ namespace {
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x6 __attribute__((ext_vector_type(6)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -410,46 +411,50 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
       }
       return;
     }
-    // Ops (FP32 hardware arithmetic), C and requantize, one MFMA tile (16
-    // values per lane) at a time, all in registers: the tile's values and
+    // Ops (FP32 hardware arithmetic), C and requantize, half an MFMA tile
+    // (8 of a lane's 16 values) at a time, all in registers: the values and
     // each op's operands are loaded at once (independent loads, one wait),
-    // and each op is a straight run over the 16 values.
-    for (uint32_t t0 = e0; t0 < e1; t0 += 16) {
-      // Output r of the tile is row row_l + RowStep(r), column col: the
-      // row step is uniform, so each access is a uniform base plus one
-      // per-lane 32-bit offset (no per-row 64-bit addresses to keep live).
-      const uint32_t col = col_at(t0), row_l = row_at(t0);
-      const uint32_t off_l = row_l * g.n + col;
+    // and each op is a straight run over the 8 values.  (Whole tiles of 16
+    // with their 16 operands spilled to scratch at 128 registers.)
+    for (uint32_t t0 = e0; t0 < e1; t0 += 8) {
+      // Output r of the tile is row row_l + RowStep(r), column col; this
+      // half's registers are r0 .. r0 + 7 (r0 = 0 or 8), rows row_h +
+      // RowStep(i), i < 8 (RowStep(r0 + i) = 2 r0 + RowStep(i)).  The row
+      // step is uniform, so each access is a uniform base plus one per-lane
+      // 32-bit offset (no per-row 64-bit addresses to keep live).
+      const uint32_t tb = t0 & ~15u, r0 = t0 & 15u;
+      const uint32_t col = col_at(tb), row_h = row_at(tb) + 2 * r0;
+      const uint32_t off_l = row_h * g.n + col;
       auto row_step = [](int r) { return (uint32_t)(8 * (r / 4) + (r & 3)); };
-      f32x16 y;
+      f32x8 y;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) y[r] = vals[(t0 + r) * 64 + l];
+      for (int i = 0; i < 8; ++i) y[i] = vals[(t0 + i) * 64 + l];
       for (uint32_t o = 0; o < g.n_ops; ++o) {
         const uint32_t kind = g.op_kind[o];
-        f32x16 x2 = {};
+        f32x8 x2 = {};
         float p = 0.0f;
         if (kind == kEpAdd || kind == kEpActMul) {
           const uint32_t* src = g.op_x2[o] + z * g.op_x2_batch[o];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const uint32_t* src_r = src + row_step(r) * g.n;  // uniform
-            x2[r] = __uint_as_float(row_l + row_step(r) < g.m && col < g.n ? src_r[off_l] : 0u);
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t* src_r = src + row_step(i) * g.n;  // uniform
+            x2[i] = __uint_as_float(row_h + row_step(i) < g.m && col < g.n ? src_r[off_l] : 0u);
           }
         } else if (kind == kEpAddP || kind == kEpMulP) {
           p = lds_vec[o][col - col0];
         }
-        EpApplyFast16(kind, g.op_imm[o], y, x2, p, lds_act);
+        EpApplyFastN(kind, g.op_imm[o], y, x2, p, lds_act);
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        uint32_t* c_r = c + row_step(r) * g.n;  // uniform
-        if (row_l + row_step(r) < g.m && col < g.n) c_r[off_l] = __float_as_uint(y[r]);
+      for (int i = 0; i < 8; ++i) {
+        uint32_t* c_r = c + row_step(i) * g.n;  // uniform
+        if (row_h + row_step(i) < g.m && col < g.n) c_r[off_l] = __float_as_uint(y[i]);
       }
       if (q_out != nullptr) {  // MXINT8 requantize over the 32 lanes holding a row's block
         const uint32_t nb = g.n >> 5, blk = (col - (l & 31)) >> 5;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const uint32_t v = __float_as_uint(y[r]), row = row_l + row_step(r);
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t v = __float_as_uint(y[i]), row = row_h + row_step(i);
           const uint32_t x = HalfMax32(ExpField(v));
           if ((row >> 2) < g.quads && blk < nb) {
             uint8_t* word = q_out + ((size_t)(row >> 2) * nb + blk) * kDdrWord;

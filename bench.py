@@ -729,6 +729,55 @@ class SiglipSet(Chain):
         torch.cuda.synchronize()
 
 
+class SparseDriveHead(Chain):
+    """SparseDrive-S detection head GEMMs (tools/compiler/sparsedrive_head.cpp:
+    HeadOrder 62-76, the attention projections 800-886, OutProjection
+    889-990, Ffn 1535-1620), on 928 anchor rows (900 padded) per frame.
+    Six decoder blocks: the first an FFN only, the other five a temporal
+    and a self attention and an FFN.  Attention, per block: q (512 -> 512,
+    W8, bias, requantize) over the anchors, k and v over the keys (the
+    anchors, or 608 temporal rows), the out projection (512 -> 512, W8,
+    bias, the residual add, requantize) and fc_after (512 -> 256, W8).
+    FFN: fc1 (512 -> 1024, MXFP4, bias, ReLU, requantize), fc2 (1024 ->
+    256, MXFP4) and the identity projection (512 -> 256, MXFP4) onto fc2's
+    output, then bias.  The deformable aggregation's and refinement's small
+    GEMMs, the norms and the attention itself are outside this chain (their
+    outputs are synthetic MXINT8 tensors of the right shape)."""
+
+    ROWS, TEMP, D, DQ, FF, BLOCKS = 928, 608, 256, 512, 1024, 6
+
+    def __init__(self, hb, torch, frames, mode):
+        super().__init__(hb, torch, self.ROWS * frames, mode, 51 + frames)
+        kd, kq, kf = self.D // 32, self.DQ // 32, self.FF // 32
+        rows = self.m
+        for blk in range(self.BLOCKS):
+            for temporal in ((True, False) if blk else ()):
+                x = self.a_words(kq)
+                for part in range(3):  # q over the anchors, k and v over the keys
+                    keys = self.TEMP * frames if (temporal and part) else rows
+                    sub = Chain(hb, torch, keys, mode, 61 + part)
+                    sub.keep, sub.descs, sub.plan = self.keep, self.descs, self.plan
+                    sub.add(self.DQ, kq, sub.a_words(kq) if keys != rows else x,
+                            sub.w8(self.DQ, kq), sub.f32(self.DQ),
+                            ops=[(hb.EP_ADDP, sub.vec(self.DQ, 0.1))], q=sub.a_words(kq))
+                    self.ops += sub.ops
+                    self.bytes += sub.bytes
+                o = self.a_words(kq)
+                self.add(self.DQ, kq, self.a_words(kq), self.w8(self.DQ, kq), self.f32(self.DQ),
+                         ops=[(hb.EP_ADDP, self.vec(self.DQ, 0.1)),
+                              (hb.EP_ADD, self.f32(self.DQ))], q=o)
+                self.add(self.D, kq, o, self.w8(self.D, kq), self.f32(self.D))
+            a = self.a_words(kq)
+            h = self.a_words(kf)
+            self.add(self.FF, kq, a, [self.w_words(self.FF, kq)], self.f32(self.FF),
+                     ops=[(hb.EP_ADDP, self.vec(self.FF, 0.1)), (hb.EP_RELU, None)], q=h)
+            out = self.f32(self.D)
+            self.add(self.D, kf, h, [self.w_words(self.D, kf)], out)
+            self.add(self.D, kq, a, [self.w_words(self.D, kq)], out, onto=True,
+                     ops=[(hb.EP_ADDP, self.vec(self.D, 0.1))])
+        torch.cuda.synchronize()
+
+
 class SparseDriveConv(Chain):
     """SparseDrive-S backbone stage-1 3x3 convolution as its im2col GEMM:
     6 cameras x 64 x 176 output positions = 67,584 rows, K = 3*3*64 = 576,
@@ -964,6 +1013,12 @@ def bench_lines(hb, torch, ctx):
                              lambda: ChainLine(SparseDriveConv(hb, torch, F))),
         "sparsedrive_exact": ("SparseDrive-S stage-1 im2col M=67584 K=576 N=64, MXFP4, exact",
                               lambda: ChainLine(SparseDriveConv(hb, torch, E))),
+        "sparsedrive_head_f1": ("SparseDrive-S det head GEMMs, 6 blocks, 928 anchor rows (1 "
+                                "frame), W8 attention + MXFP4 FFN, fast",
+                                lambda: ChainLine(SparseDriveHead(hb, torch, 1, F))),
+        "sparsedrive_head_f16": ("SparseDrive-S det head GEMMs, 6 blocks, 16 frames (14848 "
+                                 "anchor rows), W8 attention + MXFP4 FFN, fast",
+                                 lambda: ChainLine(SparseDriveHead(hb, torch, 16, F))),
         "expert_b1": ("SmolVLA action-expert step GEMM chain, B=1 (M=50), fast, grouped",
                       lambda: ChainLine(ExpertStep(hb, torch, 1, F))),
         "expert_b32": ("SmolVLA action-expert step GEMM chain, B=32 (M=1600), fast, grouped",
@@ -1308,6 +1363,26 @@ def main():
                 del wk
             rec["workload"] = desc
             out[key] = rec
+        # SparseDrive-S detection head GEMMs at 1 frame (both modes) and 16
+        head = {"workload": "SparseDrive-S det head GEMM chain: 6 blocks (5 with temporal "
+                            "and self attention: q/k/v 512->512 W8 + bias + requantize, out "
+                            "512->512 W8 + bias + residual + requantize, fc_after 512->256 W8; "
+                            "6 FFNs: fc1 512->1024 MXFP4 + bias + ReLU + requantize, fc2 "
+                            "1024->256, identity 512->256 onto + bias), 928 rows per frame"}
+        for frames, modes in ((1, (("fast", hb.FAST, "fp6_fp4"), ("exact", hb.EXACT, "bf16"))),
+                              (16, (("fast", hb.FAST, "fp6_fp4"),))):
+            for name, md, cls in modes:
+                wk = SparseDriveHead(hb, torch, frames, md)
+                t = time_chain(torch, ctx, wk, steps=5, graph=False)
+                tops, roof = chain_summary(wk, t["eager_ms"], cls,
+                                           f"sparsedrive_head_f{frames}" if md == hb.FAST else None)
+                head[f"frames={frames}"] = head.get(f"frames={frames}", {})
+                head[f"frames={frames}"][name] = {"value": tops, "unit": "TOPS",
+                                                  "ms_per_pass": t["eager_ms"],
+                                                  "gemms": t["gemms"], "m": t["m"],
+                                                  "roofline": roof}
+                del wk
+        out["sparsedrive_head"] = head
         ctx.set_stream(stream.cuda_stream)
 
     if not args.quick and args.only in (None, "smolvla"):

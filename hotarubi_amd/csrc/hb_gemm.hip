@@ -676,6 +676,7 @@ namespace {
 // 256 of 2 by 9-13% (the split sums written and read again cost more than the
 // parallelism gains); 32 workgroups, or no split, lost 50-70% at M = 141.
 constexpr uint32_t kSmallGrid = 128, kTargetWorkgroups = 128, kMinSplitSteps = 4;
+constexpr uint32_t kSplitMidRows = 1024;
 }  // namespace
 
 hipError_t GrowWorkspace(Workspace& ws, size_t bytes, hipStream_t stream) {
@@ -747,6 +748,16 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   args.gx = gx;
   args.gy = gy;
   const bool small = batch == 1 && gx * gy < kSmallGrid;
+  // A layer of up to kSplitMidRows rows whose 128-row grid is small: the
+  // single-launch split kernel's 32 x 32 tiles (enough workgroups, no
+  // partial sums through memory, no second launch) instead of K splits of
+  // 128-row tiles and the epilogue kernel (SparseDrive-S's head at 928
+  // rows: 2x faster; at 1,600 rows and more the 128-row tiles win).
+  if (small && fastk && args.quads * 4 <= kSplitMidRows) {
+    SplitPlan(args);
+    args.fast_ep = 1u;
+    return LaunchSplitLinear(args, stream);
+  }
   args.fast_ep = fastk ? 1u : 0u;
   if (fastk && !small && StreamEligible(args)) return LaunchStream(args, batch, stream);
   if (fastk && !small && PanelEligible(args)) return LaunchPanel(args, batch, stream);

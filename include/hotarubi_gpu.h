@@ -276,30 +276,33 @@ int hb_linear_async(hb_ctx* ctx, const hb_linear_desc* desc);
  * stride from one layer to the next; otherwise HB_EINVAL. */
 int hb_linear_batched_async(hb_ctx* ctx, const hb_linear_desc* descs,
                             uint32_t count);
-/* hb_linear_batched_async without any device allocation.  No counterpart in
- * the reference: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, serving loops and harnesses that forbid
- * hipMalloc).  The partial sums of a small layer's K splits and its slow
- * flags, which hb_linear keeps in the context's growable workspace, go to a
- * fixed per-device scratch array of HB_NOALLOC_SCRATCH_BYTES instead
- * (resolved when a context is created on the device, held until the
- * process ends).  A layer that needs more returns HB_ENOMEM, naming the
- * size; every other argument rule is hb_linear_batched_async's.  All calls
- * on one GPU share that GPU's array and leave their partials in it:
- * calls that overlap in time on one GPU (different streams or contexts)
- * race, so serialize them. */
 /* A group of up to HB_MAX_GROUP layers in one launch where possible (no
  * counterpart in the reference, whose compiler emits each GEMM on its own:
  * the caller knows which of them are independent, e.g. the q, k and v
  * projections of one input).  The result is that of hb_linear_async on
  * each layer in order, provided no layer reads what another writes, with
  * one exception: a layer whose HB_EP_ACT_MUL operand x2 is an earlier
- * layer's c over the same m x n (the gated MLP's gate over up) runs in that
- * layer's workgroups after it and reads its values there.  Groups of fast
+ * layer's c over the same m x n (the gated MLP's gate over up) folds beside
+ * it in its workgroups and reads its values there.  Groups of fast
  * layers of at most 160 rows of one weight format (all MXFP4 or all W8 DDR
  * planes, one piece or all several) share one launch; any other group runs
  * as one launch per layer, in order.  No allocation in the shared launch. */
 int hb_linear_group_async(hb_ctx* ctx, const hb_linear_desc* descs, uint32_t count);
+
+/* hb_linear_batched_async without any device allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc).  The partial sums and slow flags of a small layer's K splits
+ * across workgroups (fast layers of more than 1,024 rows on few tiles, and
+ * small exact layers with ops or requantize), which hb_linear keeps in the
+ * context's growable workspace, go to a fixed per-device scratch array of
+ * HB_NOALLOC_SCRATCH_BYTES instead
+ * (resolved when a context is created on the device, held until the
+ * process ends).  A layer that needs more returns HB_ENOMEM, naming the
+ * size; every other argument rule is hb_linear_batched_async's.  All calls
+ * on one GPU share that GPU's array and leave their partials in it:
+ * calls that overlap in time on one GPU (different streams or contexts)
+ * race, so serialize them. */
 
 #define HB_NOALLOC_SCRATCH_BYTES (8u << 20)
 int hb_linear_noalloc_async(hb_ctx* ctx, const hb_linear_desc* descs, uint32_t count);

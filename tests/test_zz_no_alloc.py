@@ -78,21 +78,29 @@ def run_both(gpu, m, n, kb, a, planes, modes, mode, ops=(), layers=1):
 
 def test_two_calls_in_a_row_second_smaller(gpu):
     rng = np.random.default_rng(11)
-    # 141 x 960 x 2560 MXFP4: 150 tiles of 32 x 32, 8 K splits each, ~4.9 MB
-    # of partial sums
-    m, n, kb = 141, 960, 80
+    # 1100 x 512 x 512 MXFP4: more than 1,024 rows on 18 tiles of 128 x 256,
+    # so K splits through the array (2 splits, ~4.5 MB of partial sums)
+    m, n, kb = 1100, 512, 16
     a, planes, modes = mxfp4_layer(rng, m, n, kb)
     say("call 1", dict(m=m, n=n, kb=kb))
     ref, got = run_both(gpu, m, n, kb, a, planes, modes, hb.FAST)
     assert np.array_equal(got, ref)
     want, _ = helpers.oracle_linear_mt(m, n, kb, a, planes, modes)
     helpers.check_fast(got[0], want)
-    # smaller: 72 x 512 x 768 W8 (48 tiles, 3 K splits) over what call 1 left
-    m, n, kb = 72, 512, 24
-    a, planes, modes = w8_layer(rng, m, n, kb)
+    # smaller: 100 x 256 x 256 exact with MULP and ADDP (the deferred
+    # epilogue's sums in the array) over what call 1 left
+    m, n, kb = 100, 256, 8
+    a, planes, modes = mxfp4_layer(rng, m, n, kb)
+    scale = rng.uniform(0.5, 2.0, n).astype(np.float32)
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
     say("call 2", dict(m=m, n=n, kb=kb))
-    ref, got = run_both(gpu, m, n, kb, a, planes, modes, hb.FAST)
+    ref, got = run_both(gpu, m, n, kb, a, planes, modes, hb.EXACT,
+                        ops=[(hb.EP_MULP, dev(scale)), (hb.EP_ADDP, dev(bias))])
     assert np.array_equal(got, ref)
+    want, _ = helpers.oracle_linear_mt(m, n, kb, a, planes, modes,
+                                       ops=[(hb.EP_MULP, scale.view(np.uint32)),
+                                            (hb.EP_ADDP, bias.view(np.uint32))])
+    assert np.array_equal(got[0], want)
 
 
 def test_exact_deferred_epilogue(gpu):
@@ -169,10 +177,11 @@ def test_graph_capture_of_a_new_shape(gpu):
 
 
 def test_oversize_layer_is_rejected(gpu):
-    # 256 x 4096 x 2048 MXFP4: 32 tiles of 128 x 256 rows, 4 K splits, ~16.8 MB
-    # of partial sums, over the 8 MiB array
+    # 2048 x 1024 x 2048 MXFP4: 64 tiles of 128 x 256 (more than 1,024 rows,
+    # so the K-split route), 2 K splits, ~16.8 MB of partial sums, over the
+    # 8 MiB array
     rng = np.random.default_rng(15)
-    m, n, kb = 256, 4096, 64
+    m, n, kb = 2048, 1024, 64
     a = helpers.activations(rng, m, kb * 32)[1]
     w = torch.zeros((n // 8 * kb, 144), dtype=torch.uint8, device=DEV)
     c = torch.zeros((m, n), dtype=torch.float32, device=DEV)

@@ -109,6 +109,13 @@ def lib():
             ("hbo_linear", C.c_int, [C.c_uint32, C.c_uint32, C.c_uint32, u8p, C.c_uint32,
                                      C.POINTER(u8p), u32p, C.c_uint32, C.POINTER(Piece),
                                      C.c_int, u32p, C.c_uint32, C.POINTER(EpOp), u64p, u8p]),
+            ("hbo_linear_fp8", C.c_int, [C.c_uint32, C.c_uint32, C.c_uint32, u8p, u8p,
+                                         C.c_uint32, C.POINTER(Piece), C.c_int, u32p,
+                                         C.c_uint32, C.POINTER(EpOp), u64p, u8p]),
+            ("hbo_fp8_int", C.c_int32, [C.c_uint8]),
+            ("hbo_block_value_fp8", C.c_uint32, [C.c_int32, C.c_uint32, C.c_uint32]),
+            ("hbo_quantize_fp8", C.c_uint8, [C.c_uint32, C.c_int32]),
+            ("hbo_encode_mxfp8", C.c_int, [u32p, C.c_uint32, C.c_uint32, u8p, i32p]),
             ("hbo_gemm_cycles", C.c_uint64, [C.POINTER(GemmCmd), C.c_uint32]),
             ("hbo_align_element", C.c_uint8, [C.c_uint8, C.c_uint32]),
             ("hbo_split8", C.c_int, [u8p, C.c_uint64, C.c_uint32, C.c_uint32, u8p, u8p]),
@@ -417,9 +424,36 @@ def canonical_mxfp4(code, e, exponent_shift=0, out_rows=None):
     return oc, oe
 
 
+def fp8_int(code: int) -> int:
+    """E4M3 code -> its value in units of 2^-9 (this build's MXFP8 definition)."""
+    return int(lib().hbo_fp8_int(code))
+
+
+def block_value_fp8(s: int, a_scale: int, w_scale: int) -> int:
+    return int(lib().hbo_block_value_fp8(s, a_scale, w_scale))
+
+
+def quantize_fp8(bits: int, x: int) -> int:
+    return int(lib().hbo_quantize_fp8(bits, x))
+
+
+def encode_mxfp8(x_bits: np.ndarray):
+    """fp32 bits [rows][cols] -> (E4M3 codes uint8 [rows][cols padded to 32],
+    block exponents int32 [rows][blocks]); OCP MX rule, RNE, saturating."""
+    x_bits = np.ascontiguousarray(x_bits, np.uint32)
+    rows, cols = x_bits.shape
+    kp = (cols + 31) // 32 * 32
+    q = np.zeros((rows, kp), np.uint8)
+    e = np.zeros((rows, kp // 32), np.int32)
+    if lib().hbo_encode_mxfp8(_ptr(x_bits, u32p), rows, cols, _ptr(q, u8p), _ptr(e, i32p)):
+        raise ValueError(last_error())
+    return q, e
+
+
 def linear(m, n, kb_total, a_words, planes, modes, pieces=None, c=None, onto=False,
-           ops=(), tbuf=None, quantize=False):
-    """hbo_linear; returns (c bits [m][n], q_out words or None)."""
+           ops=(), tbuf=None, quantize=False, a_fp8=False):
+    """hbo_linear (hbo_linear_fp8 with a_fp8: A holds MXFP8 E4M3 codes, one
+    MXFP4 plane); returns (c bits [m][n], q_out words or None)."""
     L = lib()
     a_words = np.ascontiguousarray(a_words, np.uint8)
     planes = [np.ascontiguousarray(p, np.uint8) for p in planes]
@@ -446,9 +480,14 @@ def linear(m, n, kb_total, a_words, planes, modes, pieces=None, c=None, onto=Fal
             eps[i].x2 = _ptr(v, u32p)
     tb = np.zeros(TBUF_DEPTH, np.uint64) if tbuf is None else np.ascontiguousarray(tbuf, np.uint64)
     q_out = np.zeros(((m // 4) * (n // 32), 144), np.uint8) if quantize else None
-    rc = L.hbo_linear(m, n, kb_total, _ptr(a_words, u8p), len(planes), wp, md, len(pieces), pc,
-                      1 if onto else 0, _ptr(cc, u32p), len(ops), eps, _ptr(tb, u64p),
-                      _ptr(q_out, u8p) if quantize else None)
+    if a_fp8:
+        rc = L.hbo_linear_fp8(m, n, kb_total, _ptr(a_words, u8p), _ptr(planes[0], u8p),
+                              len(pieces), pc, 1 if onto else 0, _ptr(cc, u32p), len(ops), eps,
+                              _ptr(tb, u64p), _ptr(q_out, u8p) if quantize else None)
+    else:
+        rc = L.hbo_linear(m, n, kb_total, _ptr(a_words, u8p), len(planes), wp, md, len(pieces),
+                          pc, 1 if onto else 0, _ptr(cc, u32p), len(ops), eps, _ptr(tb, u64p),
+                          _ptr(q_out, u8p) if quantize else None)
     if rc:
         raise ValueError(last_error())
     return cc, q_out

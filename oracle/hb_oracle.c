@@ -313,6 +313,107 @@ int hbo_encode_mxint8(const uint32_t* x, uint32_t rows, uint32_t cols,
   return g_error[0] ? 1 : 0;
 }
 
+/* ---- MXFP8 E4M3 activations (no counterpart in the reference) ----------
+ * This build's definition, pinned in tests/test_oracle_fp8.py against
+ * exact rational arithmetic and brute force over the 256 codes:
+ *  - an E4M3 code (OCP FP8 E4M3FN: bias 7, no infinities, max 448) is an
+ *    integer A_int times 2^-9: m for exponent field 0, (8 + m) << (e - 1)
+ *    otherwise (codes 0x7F / 0xFF, NaN in E4M3FN, read as +-480 and are
+ *    not valid input);
+ *  - a block of 32 such codes against an MXFP4 block: S = sum A_int *
+ *    W_int (W_int = 2 x E2M1 magnitude, signed) is exact in 28 bits; its
+ *    value S * 2^(ea + ew - 264) is rounded once to FP32 by the reference's
+ *    Round / Pack (RNE, below normal -> +0, exponent >= 255 -> +-inf);
+ *  - blocks fold in the reference's order with its FP32 add;
+ *  - encoding (OCP MX): block exponent X = floor(log2 max|x|) - 8, clamped to
+ *    [-127, 127] (0 for a zero block), elements x * 2^-X rounded to nearest
+ *    even on the E4M3 grid and saturated to +-448; infinities and NaNs are
+ *    rejected. */
+int32_t hbo_fp8_int(uint8_t code) {
+  const uint32_t e = (code >> 3) & 15u, m = code & 7u;
+  const int32_t u = e == 0 ? (int32_t)m : (int32_t)((8u + m) << (e - 1u));
+  return (code & 0x80u) ? -u : u;
+}
+
+uint32_t hbo_block_value_fp8(int32_t sum, uint32_t a_scale, uint32_t w_scale) {
+  if (sum == 0) return 0u;
+  const uint32_t sign = sum < 0 ? 1u : 0u;
+  const uint32_t mag = (uint32_t)(sum < 0 ? -sum : sum);
+  int msb = 31;
+  while (!((mag >> msb) & 1u)) --msb;
+  const int32_t exponent = (int32_t)(a_scale + w_scale) - 264 + msb + 127;
+  if (msb <= 23) return hbo_fp32_pack(sign, exponent, (mag << (23 - msb)) & 0x7FFFFFu);
+  const int sh = msb - 23;
+  const uint32_t sig24 = mag >> sh;
+  const int guard = (mag >> (sh - 1)) & 1u;
+  const int sticky = (mag & ((1u << (sh - 1)) - 1u)) != 0;
+  return hbo_fp32_round(sign, exponent, sig24, guard, sticky);
+}
+
+uint8_t hbo_quantize_fp8(uint32_t bits, int32_t x) {
+  const uint32_t field = exp_field(bits);
+  if (field == 0xFFu) {
+    fail("MXFP8 input is infinite or NaN");
+    return 0;
+  }
+  const uint64_t sig = field == 0 ? (bits & 0x7FFFFFu) : ((bits & 0x7FFFFFu) | 0x800000u);
+  if (sig == 0) return 0;
+  int bw = 64;
+  while (!((sig >> (bw - 1)) & 1u)) --bw;
+  const int64_t ev = (field == 0 ? -149 : (int64_t)field - 150) - x; /* |y| = sig 2^ev */
+  int64_t qe = (int64_t)bw - 1 + ev - 3;                                /* the grid step */
+  if (qe < -9) qe = -9;
+  const int64_t s = qe - ev;
+  uint64_t mant;
+  if (s <= 0) {
+    mant = sig << (-s);
+  } else if (s > 40) {
+    mant = 0;
+  } else {
+    const uint64_t kept = sig >> s, rest = sig & ((1ull << s) - 1ull), half = 1ull << (s - 1);
+    mant = kept + ((rest > half || (rest == half && (kept & 1u))) ? 1u : 0u);
+  }
+  /* magnitude in units of 2^-9, saturated to 448 */
+  uint64_t u = qe + 9 > 30 ? ~0ull : mant << (qe + 9);
+  if (mant != 0 && (qe + 9 > 30 || u > 229376u)) u = 229376u;
+  if (u == 0) return 0;
+  uint8_t code;
+  if (u < 8) {
+    code = (uint8_t)u;
+  } else {
+    int top = 63;
+    while (!((u >> top) & 1u)) --top;
+    code = (uint8_t)(((uint32_t)(top - 2) << 3) | ((uint32_t)(u >> (top - 3)) & 7u));
+  }
+  return (uint8_t)(code | ((bits >> 31) ? 0x80u : 0u));
+}
+
+int hbo_encode_mxfp8(const uint32_t* x, uint32_t rows, uint32_t cols, uint8_t* q,
+                     int32_t* e) {
+  const uint32_t kp = pad_to_block(cols), blocks = kp / 32u;
+  g_error[0] = 0;
+  for (uint32_t r = 0; r < rows; ++r) {
+    for (uint32_t kb = 0; kb < blocks; ++kb) {
+      const uint32_t end = cols < (kb + 1) * 32u ? cols : (kb + 1) * 32u;
+      uint32_t amax = 0;
+      for (uint32_t c = kb * 32u; c < end; ++c) {
+        const uint32_t mag = x[(size_t)r * cols + c] & 0x7FFFFFFFu;
+        if (mag > amax) amax = mag;
+      }
+      int32_t ex = 0;
+      if (amax) {
+        ex = (int32_t)exp_field(amax) - 127 - 8;
+        if (ex < -127) ex = -127;
+        if (ex > 127) ex = 127;
+      }
+      e[(size_t)r * blocks + kb] = ex;
+      for (uint32_t c = kb * 32u; c < (kb + 1) * 32u; ++c)
+        q[(size_t)r * kp + c] = c < end ? hbo_quantize_fp8(x[(size_t)r * cols + c], ex) : 0;
+    }
+  }
+  return g_error[0] ? 1 : 0;
+}
+
 /* formats.cpp:66-70 */
 static int scale_byte(int32_t e, uint8_t* out) {
   if (e < -127 || e > 127) return fail("block exponent %d is outside E8M0", e);
@@ -1011,13 +1112,14 @@ static uint32_t epilogue(const hbo_ep_op* op, uint32_t y, size_t r, uint32_t n,
   }
 }
 
-int hbo_linear(uint32_t m, uint32_t n, uint32_t kb_total, const uint8_t* a,
-               uint32_t n_planes, const uint8_t* const* w,
-               const uint32_t* modes, uint32_t n_pieces,
-               const hbo_piece* pieces, int onto, uint32_t* c,
-               uint32_t n_ops, const hbo_ep_op* ops, const uint64_t* tbuf,
-               uint8_t* q_out) {
+static int linear_impl(uint32_t m, uint32_t n, uint32_t kb_total, const uint8_t* a,
+                       uint32_t n_planes, const uint8_t* const* w, const uint32_t* modes,
+                       uint32_t n_pieces, const hbo_piece* pieces, int onto, uint32_t* c,
+                       uint32_t n_ops, const hbo_ep_op* ops, const uint64_t* tbuf,
+                       uint8_t* q_out, int a_fp8) {
   if (m % 4 || n % 8) return fail("linear %ux%u is not a multiple of 4x8", m, n);
+  if (a_fp8 && (n_planes != 1 || modes[0] != MODE_FP4))
+    return fail("MXFP8 activations take one MXFP4 weight plane");
   if (q_out && n % 32) return fail("quantized output needs n %% 32 == 0, n = %u", n);
   if (n_planes < 1 || n_planes > 2 || n_pieces < 1) return fail("bad planes/pieces");
   for (uint32_t p = 0; p < n_pieces; ++p)
@@ -1039,10 +1141,11 @@ int hbo_linear(uint32_t m, uint32_t n, uint32_t kb_total, const uint8_t* a,
             for (uint32_t k = 0; k < 32; ++k) {
               const uint32_t idx = cl * 32 + k;
               const uint32_t byte = ww[idx / 2];
-              sum += (int32_t)(int8_t)aw[t * 32 + k] *
-                     hbo_weight_value(idx % 2 == 0 ? (byte & 0xFu) : (byte >> 4), mode);
+              const int32_t av = a_fp8 ? hbo_fp8_int(aw[t * 32 + k]) : (int32_t)(int8_t)aw[t * 32 + k];
+              sum += av * hbo_weight_value(idx % 2 == 0 ? (byte & 0xFu) : (byte >> 4), mode);
             }
-            acc = hbo_fp32_add(acc, hbo_block_value(sum, aw[128 + t], ww[128 + cl], mode));
+            acc = hbo_fp32_add(acc, a_fp8 ? hbo_block_value_fp8(sum, aw[128 + t], ww[128 + cl])
+                                          : hbo_block_value(sum, aw[128 + t], ww[128 + cl], mode));
           }
         }
       }
@@ -1065,6 +1168,25 @@ int hbo_linear(uint32_t m, uint32_t n, uint32_t kb_total, const uint8_t* a,
     }
   }
   return 0;
+}
+
+int hbo_linear(uint32_t m, uint32_t n, uint32_t kb_total, const uint8_t* a,
+               uint32_t n_planes, const uint8_t* const* w,
+               const uint32_t* modes, uint32_t n_pieces,
+               const hbo_piece* pieces, int onto, uint32_t* c,
+               uint32_t n_ops, const hbo_ep_op* ops, const uint64_t* tbuf,
+               uint8_t* q_out) {
+  return linear_impl(m, n, kb_total, a, n_planes, w, modes, n_pieces, pieces, onto, c, n_ops,
+                     ops, tbuf, q_out, 0);
+}
+
+int hbo_linear_fp8(uint32_t m, uint32_t n, uint32_t kb_total, const uint8_t* a,
+                   const uint8_t* w, uint32_t n_pieces, const hbo_piece* pieces, int onto,
+                   uint32_t* c, uint32_t n_ops, const hbo_ep_op* ops, const uint64_t* tbuf,
+                   uint8_t* q_out) {
+  const uint32_t mode = MODE_FP4;
+  return linear_impl(m, n, kb_total, a, 1, &w, &mode, n_pieces, pieces, onto, c, n_ops, ops,
+                     tbuf, q_out, 1);
 }
 
 /* ------------------------------------------------------------------ */

@@ -14,6 +14,9 @@
  * load this library, and only as the checker.  The product library
  * (libhotarubi_gpu.so) never links or calls it.
  *
+ * The MXFP8 functions restate no reference code (the reference has no FP8
+ * activation format); they are this build's definition of that extension.
+ *
  * Every function here is pinned by at least one of: the reference's own
  * known-answer tests (tests/golden/), the reference FP32 sources compiled
  * from /root/reference into oracle/_ref, closed-form checks in
@@ -202,6 +205,20 @@ int hbo_linear(uint32_t m, uint32_t n, uint32_t kb_total, const uint8_t* a,
                const hbo_piece* pieces, int onto, uint32_t* c,
                uint32_t n_ops, const hbo_ep_op* ops, const uint64_t* tbuf,
                uint8_t* q_out);
+
+/* MXFP8 E4M3 activations (no counterpart in the reference; this build's
+ * definition, see hb_oracle.c): E4M3 code -> integer in units of 2^-9, the
+ * block value of S = sum A_int * W_int rounded once to FP32, the OCP MX
+ * encoder, and the linear fold over one MXFP4 weight plane. */
+int32_t hbo_fp8_int(uint8_t code);
+uint32_t hbo_block_value_fp8(int32_t sum, uint32_t a_scale, uint32_t w_scale);
+uint8_t hbo_quantize_fp8(uint32_t bits, int32_t x);
+int hbo_encode_mxfp8(const uint32_t* x, uint32_t rows, uint32_t cols, uint8_t* q,
+                     int32_t* e);
+int hbo_linear_fp8(uint32_t m, uint32_t n, uint32_t kb_total, const uint8_t* a,
+                   const uint8_t* w, uint32_t n_pieces, const hbo_piece* pieces, int onto,
+                   uint32_t* c, uint32_t n_ops, const hbo_ep_op* ops, const uint64_t* tbuf,
+                   uint8_t* q_out);
 
 /* Batched forms for the tests. */
 void hbo_fp32_add_n(const uint32_t* a, const uint32_t* b, uint32_t* out, uint64_t n);

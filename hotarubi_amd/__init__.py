@@ -37,6 +37,7 @@ WORD_BYTES = {ABUF: 132, WBUF: 144, FBUF: 128, PBUF: 128, TBUF: 8}
 EXACT, FAST = 0, 1
 PANELS = 2  # hb_linear_desc.flags bit: the W planes are weight panels
 W8_PANELS = 4  # flags bit: a W8 layer's planes are W8 panels (w[0] = w[1])
+A_FP8 = 8  # flags bit: A holds MXFP8 E4M3 codes (hb_encode_mxfp8), one MXFP4 plane
 EP_ADDP, EP_MULP, EP_SCALE, EP_COPY, EP_RELU, EP_ACT, EP_ACT_MUL = 3, 4, 5, 6, 7, 8, 9
 EP_ADD = 0x100
 MAX_PIECES, MAX_OPS = 16, 8
@@ -49,7 +50,8 @@ EXPORTS = (
     "hb_onchip_upload", "hb_onchip_download", "hb_onchip_device_ptr", "hb_gemm_decode",
     "hb_gemm_encode", "hb_gemm_check", "hb_gemm_access", "hb_gemm_exec", "hb_gemm_exec_async",
     "hb_gemm_cycles", "hb_vec_exec", "hb_linear", "hb_linear_async",
-    "hb_linear_batched_async", "hb_encode_mxint8", "hb_split8", "hb_split8_async",
+    "hb_linear_batched_async", "hb_encode_mxint8", "hb_encode_mxfp8", "hb_split8",
+    "hb_split8_async",
     "hb_t32_split8", "hb_t32_split8_async", "hb_rows", "hb_rows_async",
     "hb_row_load", "hb_row_load_async", "hb_row_store", "hb_row_store_async",
     "hb_gacc", "hb_gacc_async", "hb_panel_bytes", "hb_pack_weights", "hb_unpack_weights",
@@ -190,6 +192,7 @@ def lib():
             "hb_linear_group_async": (i, [vp, C.POINTER(_LinearDesc), u32]),
             "hb_linear_noalloc_async": (i, [vp, C.POINTER(_LinearDesc), u32]),
             "hb_encode_mxint8": (i, [vp, vp, u32, u32, vp]),
+            "hb_encode_mxfp8": (i, [vp, vp, u32, u32, vp]),
             "hb_gacc": (i, [vp, C.POINTER(_GaccDesc)]),
             "hb_gacc_async": (i, [vp, C.POINTER(_GaccDesc)]),
             "hb_row_load": (i, [vp, vp, C.c_uint64, u32, u32, u32, vp, vp]),
@@ -392,11 +395,12 @@ def _ptr(t) -> int | None:
 
 def linear_desc(m, n, kb_total, a, planes, modes, c, pieces=None, onto=False, ops=(),
                 tbuf=None, q_out=None, mode=EXACT, a_stride=0, panels=False,
-                w8_panels=False) -> _LinearDesc:
+                w8_panels=False, a_fp8=False) -> _LinearDesc:
     """Build an hb_linear_desc from device buffers (torch tensors or addresses).
 
     planes/modes: [w] with [0] (FP4) or [w_hi, w_lo] with [1, 2] (W8);
     w8_panels: planes = [p, p] for the W8 panels p of hb_pack_w8.
+    a_fp8: A holds MXFP8 E4M3 words (hb_encode_mxfp8); planes = [w], modes [0].
     pieces: (kb_offset, kb) or, with a_stride (A words per quad) nonzero,
     (kb_offset, kb, a_word): LinearPiece (kernels.hpp:69-74) with its A
     place as a word offset from `a`.
@@ -433,7 +437,8 @@ def linear_desc(m, n, kb_total, a, planes, modes, c, pieces=None, onto=False, op
             d.ops[i].x2 = _ptr(arg)
     d.tbuf = _ptr(tbuf)
     d.q_out = _ptr(q_out)
-    d.flags = mode | (PANELS if panels else 0) | (W8_PANELS if w8_panels else 0)
+    d.flags = mode | (PANELS if panels else 0) | (W8_PANELS if w8_panels else 0) | \
+        (A_FP8 if a_fp8 else 0)
     return d
 
 
@@ -679,3 +684,9 @@ def encode_mxint8(x, rows: int, cols: int, out, ctx: Context | None = None) -> N
     """EncodeMxint8 + PackAbuf of a device fp32 [rows][cols] into DDR words."""
     ctx = ctx or default_context()
     _check(lib().hb_encode_mxint8(ctx.handle, _ptr(x), rows, cols, _ptr(out)))
+
+
+def encode_mxfp8(x, rows: int, cols: int, out, ctx: Context | None = None) -> None:
+    """hb_encode_mxfp8: a device fp32 [rows][cols] as MXFP8 E4M3 DDR words."""
+    ctx = ctx or default_context()
+    _check(lib().hb_encode_mxfp8(ctx.handle, _ptr(x), rows, cols, _ptr(out)))

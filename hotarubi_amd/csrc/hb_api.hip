@@ -519,9 +519,13 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g, bool* mixed) {
   if (!d->a || !d->c) return Fail(HB_EINVAL, "null A or C");
   if (d->n_ops > HB_MAX_EP_OPS) return Fail(HB_EINVAL, "n_ops = %u", d->n_ops);
   if (d->q_out && d->n % 32 != 0) return Fail(HB_EINVAL, "quantized output needs n %% 32 == 0");
-  if (d->flags & ~(uint32_t)(HB_LINEAR_FAST | HB_LINEAR_PANELS | HB_LINEAR_W8_PANELS) ||
+  const bool fp8 = (d->flags & HB_LINEAR_A_FP8) != 0;
+  if (d->flags &
+          ~(uint32_t)(HB_LINEAR_FAST | HB_LINEAR_PANELS | HB_LINEAR_W8_PANELS | HB_LINEAR_A_FP8) ||
       (panels && w8p))
     return Fail(HB_EINVAL, "flags = %u", d->flags);
+  if (fp8 && (d->n_planes != 1 || d->modes[0] != 0 || w8p))
+    return Fail(HB_EINVAL, "MXFP8 activations take one MXFP4 plane (modes {0})");
   for (uint32_t l = 0; panels && l < d->n_planes; ++l)
     if (reinterpret_cast<uintptr_t>(d->w[l]) % 16 != 0)
       return Fail(HB_EINVAL, "weight panels must be 16-byte aligned");
@@ -582,6 +586,7 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g, bool* mixed) {
   g->total_steps = (uint32_t)steps;
   g->w_panels = panels ? 1u : 0u;
   g->w_fp6 = w8p ? 1u : 0u;
+  g->a_fp8 = fp8 ? 1u : 0u;
   g->w_steps = (d->kb_total + 1) / 2;
   g->acc = d->onto ? 1u : 0u;
   g->tbuf = d->tbuf;
@@ -920,7 +925,8 @@ int hb_linear_group_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) 
     bool mixed = false;
     if (int rc = LinearArgs(&d[i], &grp.g[i], &mixed)) return rc;
     const hb::GemmArgs& g = grp.g[i];
-    fuse = fuse && !mixed && (d[i].flags & HB_LINEAR_FAST) && !g.w_fp6 && hb::FastEligible(g) &&
+    fuse = fuse && !mixed && (d[i].flags & HB_LINEAR_FAST) && !g.w_fp6 && !g.a_fp8 &&
+           hb::FastEligible(g) &&
            hb::SplitEligible(g, 1) && g.n_planes == grp.g[0].n_planes &&
            (g.n_pieces > 1) == (grp.g[0].n_pieces > 1);
   }
@@ -1079,18 +1085,34 @@ int hb_unpack_w8(hb_ctx* ctx, const void* panels, uint32_t n, uint32_t kb_total,
   return W8Convert(ctx, nullptr, nullptr, n, kb_total, panels, nullptr, w_hi, w_lo);
 }
 
-int hb_encode_mxint8(hb_ctx* ctx, const float* x, uint32_t rows, uint32_t cols, void* out) {
+}  // extern "C"
+
+namespace {
+
+int EncodeMx(hb_ctx* ctx, const float* x, uint32_t rows, uint32_t cols, void* out, bool fp8) {
   if (int rc = Enter(ctx)) return rc;
   if (!x || !out || rows < 1 || cols < 1) return Fail(HB_EINVAL, "bad encode arguments");
   HB_HIP(hipMemsetAsync(ctx->d_flag, 0, sizeof(uint32_t), ctx->stream));
   hipError_t err = hb::LaunchEncodeMxint8(x, rows, cols, static_cast<uint8_t*>(out),
-                                          ctx->d_flag, ctx->stream);
+                                          ctx->d_flag, ctx->stream, fp8);
   if (err != hipSuccess) return HipFail(err, "encode launch");
   uint32_t flag = 0;
   HB_HIP(hipMemcpyAsync(&flag, ctx->d_flag, sizeof flag, hipMemcpyDeviceToHost, ctx->stream));
   HB_HIP(hipStreamSynchronize(ctx->stream));
-  if (flag) return Fail(HB_EINVAL, "MXINT8 input is infinite or NaN");
+  if (flag) return Fail(HB_EINVAL, "%s input is infinite or NaN", fp8 ? "MXFP8" : "MXINT8");
   return HB_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hb_encode_mxint8(hb_ctx* ctx, const float* x, uint32_t rows, uint32_t cols, void* out) {
+  return EncodeMx(ctx, x, rows, cols, out, false);
+}
+
+int hb_encode_mxfp8(hb_ctx* ctx, const float* x, uint32_t rows, uint32_t cols, void* out) {
+  return EncodeMx(ctx, x, rows, cols, out, true);
 }
 
 }  // extern "C"

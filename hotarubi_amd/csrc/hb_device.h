@@ -299,4 +299,37 @@ __device__ __forceinline__ uint32_t SlowLinear(const GemmArgs& g, const uint8_t*
   return acc;
 }
 
+// SlowLinear for MXFP8 E4M3 activations over one MXFP4 plane (DDR words or
+// weight panels): each block's exact sum of Fp8Int(a) x WeightValue(w),
+// BlockValueFp8, folded with the reference's add in its order.
+__device__ __forceinline__ uint32_t SlowLinearFp8(const GemmArgs& g, const uint8_t* a,
+                                                  const uint8_t* w, uint32_t acc, uint32_t row,
+                                                  uint32_t col) {
+  const bool panels = g.w_panels != 0;
+  const uint32_t quad = row >> 2, t = row & 3;
+  const WLaneOff wo = WLane(g, col, panels);
+  for (uint32_t p = 0; p < g.n_pieces; ++p)
+    for (uint32_t b = 0; b < g.piece_kb[p]; ++b) {
+      const uint32_t blk = g.piece_off[p] + b;
+      const uint8_t* aw = a + ((size_t)quad * g.a_row + blk) * kDdrWord;
+      const uint8_t* codes;
+      uint32_t wscale;
+      if (panels) {
+        codes = w + wo.codes + WBlockCodes(g, blk, true);
+        wscale = w[wo.scale + WBlockScale(g, blk, true) + wo.shift / 8];
+      } else {
+        const uint8_t* ww = w + ((size_t)(col >> 3) * g.kb_total + blk) * kDdrWord;
+        codes = ww + (col & 7) * 16;
+        wscale = ww[128 + (col & 7)];
+      }
+      int32_t sum = 0;
+      for (uint32_t k = 0; k < 32; ++k) {
+        const uint32_t byte = codes[k >> 1];
+        sum += Fp8Int(aw[t * 32 + k]) * WeightValue((k & 1) ? (byte >> 4) : byte, kModeFp4);
+      }
+      acc = AddBits(acc, BlockValueFp8(sum, aw[128 + t], wscale));
+    }
+  return acc;
+}
+
 }  // namespace hb

@@ -169,4 +169,65 @@ HB_HD int8_t QuantizeInt8(uint32_t bits, int32_t e, bool* bad) {
   return (int8_t)v;
 }
 
+// ---- MXFP8 E4M3 activations (no counterpart in the reference) ----
+// An E4M3 code (OCP E4M3FN: bias 7, no infinities, max 448) as an integer
+// in units of 2^-9: m for exponent field 0, (8 + m) << (e - 1) otherwise
+// (the NaN codes 0x7F / 0xFF read as +-480; they are not valid input).
+HB_HD int32_t Fp8Int(uint32_t code) {
+  const uint32_t e = (code >> 3) & 15u, m = code & 7u;
+  const int32_t u = e == 0 ? (int32_t)m : (int32_t)((8u + m) << (e - 1u));
+  return (code & 0x80u) ? -u : u;
+}
+
+// A block's exact sum S = sum Fp8Int(a) * WeightValue(w) against MXFP4 (28
+// bits at most), S * 2^(a_scale + w_scale - 264) rounded once to FP32 by
+// the reference's Round / Pack (RNE; below normal -> +0; overflow -> inf).
+HB_HD uint32_t BlockValueFp8(int32_t sum, uint32_t a_scale, uint32_t w_scale) {
+  if (sum == 0) return 0u;
+  const uint32_t sign = sum < 0 ? 1u : 0u;
+  const uint32_t mag = (uint32_t)(sum < 0 ? -sum : sum);
+  const int msb = BitWidth32(mag) - 1;
+  const int32_t exponent = (int32_t)(a_scale + w_scale) - 264 + msb + 127;
+  if (msb <= 23) return Pack(sign, exponent, (mag << (23 - msb)) & 0x7FFFFFu);
+  const int sh = msb - 23;
+  return Round(sign, exponent, mag >> sh, ((mag >> (sh - 1)) & 1u) != 0,
+               (mag & ((1u << (sh - 1)) - 1u)) != 0);
+}
+
+// OCP MX encoding of one element at block exponent x: x-scaled value
+// rounded to nearest even on the E4M3 grid, saturated to +-448; a zero
+// magnitude encodes as 0.  Inf/NaN encodes as 0 with *bad set.
+HB_HD uint8_t QuantizeFp8(uint32_t bits, int32_t x, bool* bad) {
+  const uint32_t field = ExpField(bits);
+  if (field == 0xFFu) {
+    *bad = true;
+    return 0;
+  }
+  const uint64_t sig = field == 0 ? (bits & 0x7FFFFFu) : ((bits & 0x7FFFFFu) | 0x800000u);
+  if (sig == 0) return 0;
+  const int bw = BitWidth64(sig);
+  const int64_t ev = (field == 0 ? -149 : (int64_t)field - 150) - x;  // |y| = sig 2^ev
+  int64_t qe = (int64_t)bw - 1 + ev - 3;                                // the grid step
+  qe = qe < -9 ? -9 : qe;
+  const int64_t s = qe - ev;
+  uint64_t mant = 0;
+  if (s <= 0) {
+    mant = sig << (-s);
+  } else if (s <= 40) {
+    const uint64_t kept = sig >> s, rest = sig & ((1ull << s) - 1ull), half = 1ull << (s - 1);
+    mant = kept + ((rest > half || (rest == half && (kept & 1u))) ? 1u : 0u);
+  }
+  uint64_t u = qe + 9 > 30 ? ~0ull : mant << (qe + 9);  // units of 2^-9
+  if (mant != 0 && (qe + 9 > 30 || u > 229376u)) u = 229376u;
+  if (u == 0) return 0;
+  uint32_t code;
+  if (u < 8) {
+    code = (uint32_t)u;
+  } else {
+    const int top = BitWidth64(u) - 1;
+    code = ((uint32_t)(top - 2) << 3) | ((uint32_t)(u >> (top - 3)) & 7u);
+  }
+  return (uint8_t)(code | ((bits >> 31) ? 0x80u : 0u));
+}
+
 }  // namespace hb

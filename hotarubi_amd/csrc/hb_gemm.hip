@@ -707,10 +707,45 @@ void FreeWorkspace(Workspace& ws) {
   ws = Workspace{};
 }
 
+// MXFP8 E4M3 activations (one MXFP4 plane): in fast mode a layer of up to
+// kSplitMidRows rows runs the single-launch split kernel with A straight
+// into the FP8 x FP4 matrix cores; every other layer (exact mode, batches,
+// more rows) is folded exactly per output by the epilogue kernel, one
+// launch per layer (which meets the fast-mode tolerance too).
+hipError_t LaunchFp8Linear(const GemmArgs& in, uint32_t batch, bool fast, hipStream_t stream) {
+  GemmArgs args = in;
+  args.ws = nullptr;
+  args.splits = 1;
+  args.split_steps = 0;
+  if (fast && batch == 1 && args.quads * 4 <= kSplitMidRows) {
+    SplitPlan(args);
+    args.fast_ep = 1u;
+    return LaunchSplitLinear(args, stream);
+  }
+  args.fast_ep = 0u;
+  for (uint32_t z = 0; z < batch; ++z) {
+    GemmArgs one = args;
+    one.a += z * args.a_batch;
+    one.w[0] += z * args.w_batch;
+    one.w[1] = one.w[0];
+    one.c += z * args.c_batch;
+    if (one.q_out != nullptr) one.q_out += z * args.q_batch;
+    for (uint32_t o = 0; o < args.n_ops; ++o) {
+      if (one.op_vec[o] != nullptr) one.op_vec[o] += z * args.op_vec_batch[o];
+      if (one.op_x2[o] != nullptr) one.op_x2[o] += z * args.op_x2_batch[o];
+    }
+    one.a_batch = one.w_batch = one.c_batch = one.q_batch = 0;
+    const hipError_t err = LaunchEpilogue(one, stream);
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
 hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace& ws,
                         hipStream_t stream, FixedScratch* fixed) {
   // W8 panels: their own kernel, every shape and mode.
   if (in.w_fp6) return LaunchW8Linear(in, batch, fast, stream);
+  if (in.a_fp8) return LaunchFp8Linear(in, batch, fast, stream);
   GemmArgs args = in;
   args.ws = nullptr;
   args.splits = 1;

@@ -76,6 +76,8 @@ struct GemmArgs {
   uint32_t w_fp6;
   // tile order of BandTile: column tiles in bands of this width (0: LogicalTile)
   uint32_t band;
+  // A holds MXFP8 E4M3 codes (HB_LINEAR_A_FP8; one MXFP4 weight plane)
+  uint32_t a_fp8;
 };
 
 // Weight panels (hb_pack_weights): one plane of n columns x kb_total
@@ -362,8 +364,9 @@ struct VecPass {
 hipError_t LaunchVecPass(const VecPass& pass, uint8_t* abuf, uint32_t* fbuf,
                          const uint32_t* pbuf, const uint64_t* tbuf, uint32_t* temp,
                          hipStream_t stream);
+// fp8: MXFP8 E4M3 codes (OCP MX rule) instead of MXINT8, in the same words.
 hipError_t LaunchEncodeMxint8(const float* x, uint32_t rows, uint32_t cols, uint8_t* out,
-                              uint32_t* bad_flag, hipStream_t stream);
+                              uint32_t* bad_flag, hipStream_t stream, bool fp8 = false);
 
 // Row programs of the VEC library (12 SOFTMAX, 22 LAYERNORM, 34 RMSNORM):
 // the register values of quad 0's slot and the per-quad steps.

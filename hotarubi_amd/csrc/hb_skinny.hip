@@ -400,7 +400,7 @@ typedef float f32x16s __attribute__((ext_vector_type(16)));
 // and after a second barrier the second layer's finishers read them from
 // x2_lds as op x2_op's [m][n] operand.  Every wave of the workgroup calls
 // this once (barriers).
-template <bool kW8, bool kMulti>
+template <bool kW8, bool kMulti, bool kA8 = false>
 __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint32_t split,
                                           uint32_t nwaves, float (*lds_part)[16 * 64],
                                           uint32_t* lds_flag,
@@ -432,15 +432,34 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
 
   auto load = [&](RawSplit<kW8>& rw, uint32_t st) __attribute__((always_inline)) {
     const uint32_t idx = 2 * st + hb;
-    rw.nib = (st < s_end && idx < nblocks) ? 0x0F0F0F0Fu : 0u;
     const uint32_t ublk = SkinnyBlockOf<kMulti>(g, min(idx, nblocks - 1));
     const uint8_t* p = a + (size_t)ublk * kDdrWord + a_off;
-    const u32x4 v0 = *reinterpret_cast<const u32x4*>(p);
-    const u32x4 v1 = *reinterpret_cast<const u32x4*>(p + 16);
+    if constexpr (kA8) {
+      // 8-bit A operands take K in 16-wide halves per lane: registers 0-3
+      // of lane half h are K [16 h, 16 h + 16), registers 4-7 K [32 + 16 h,
+      // + 16), and each 32-wide K range is scaled by its lane half's byte.
+      // So lane half h holds bytes [16 h, 16 h + 16) of both blocks of the
+      // step (block 2 st in 0-3, 2 st + 1 in 4-7) and the scale of block
+      // 2 st + h.  nib: bit 0 / 1 set when block 2 st / 2 st + 1 is in range.
+      rw.nib = (st < s_end ? 1u : 0u) | ((st < s_end && 2 * st + 1 < nblocks) ? 2u : 0u);
+      const uint32_t b0 = SkinnyBlockOf<kMulti>(g, min(2 * st, nblocks - 1));
+      const uint32_t b1 = SkinnyBlockOf<kMulti>(g, min(2 * st + 1, nblocks - 1));
+      const u32x4 v0 = *reinterpret_cast<const u32x4*>(a + (size_t)b0 * kDdrWord + a_off + 16 * hb);
+      const u32x4 v1 = *reinterpret_cast<const u32x4*>(a + (size_t)b1 * kDdrWord + a_off + 16 * hb);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      rw.a[i] = v0[i];
-      rw.a[4 + i] = v1[i];
+      for (int i = 0; i < 4; ++i) {
+        rw.a[i] = v0[i];
+        rw.a[4 + i] = v1[i];
+      }
+    } else {
+      rw.nib = (st < s_end && idx < nblocks) ? 0x0F0F0F0Fu : 0u;
+      const u32x4 v0 = *reinterpret_cast<const u32x4*>(p);
+      const u32x4 v1 = *reinterpret_cast<const u32x4*>(p + 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        rw.a[i] = v0[i];
+        rw.a[4 + i] = v1[i];
+      }
     }
     rw.sa = *reinterpret_cast<const uint32_t*>(p + as_delta);
     const uint32_t wbc = WBlockCodes(g, ublk), wbs = WBlockScale(g, ublk);
@@ -479,6 +498,18 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
     }
     const uint32_t ea = __builtin_amdgcn_ubfe(rw.sa, ashift, 8);
     unsafe |= ea - kSafeLo > kSafeHi - kSafeLo;
+    if constexpr (kA8) {  // MXFP8: the code bytes are the FP8 operand (see load), scale ea
+      const uint32_t keep0 = (rw.nib & 1u) ? ~0u : 0u, keep1 = (rw.nib & 2u) ? ~0u : 0u;
+      i32x8 a8;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a8[i] = (int)(rw.a[i] & keep0);
+        a8[4 + i] = (int)(rw.a[4 + i] & keep1);
+      }
+      acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b[0], acc, 0, 4, 0, (int)ea, 0,
+                                                            (int)sb);
+      return;
+    }
     const int sa = (int)((ea - 1u) | ((ea - 5u) << 8));
     i32x8 ap[2];
 #pragma unroll
@@ -589,8 +620,10 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
       const uint32_t row = row_of(e);
       const float init = row < g.m ? pre_init[e] : 0.0f;
       y[i] = init + sum[e] + 0.0f;
-      if (slow && col_in && (row >> 2) < g.quads)  // a scale byte left the window: exactly
-        y[i] = __uint_as_float(SlowLinear(g, a, w0, w1, __float_as_uint(init), row, col));
+      if (slow && col_in && (row >> 2) < g.quads) {  // a scale byte left the window: exactly
+        y[i] = __uint_as_float(kA8 ? SlowLinearFp8(g, a, w0, __float_as_uint(init), row, col)
+                                   : SlowLinear(g, a, w0, w1, __float_as_uint(init), row, col));
+      }
     }
     for (uint32_t op = 0; op < g.n_ops; ++op) {
       const uint32_t kind = g.op_kind[op];
@@ -662,12 +695,12 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
   }
 }
 
-template <bool kW8, bool kMulti>
+template <bool kW8, bool kMulti, bool kA8 = false>
 __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
   __shared__ float lds_part[kMaxSplitWaves][16 * 64];
   __shared__ uint32_t lds_flag[kMaxSplitWaves];
   TouchArgs(&g, sizeof g);
-  SplitTile<kW8, kMulti>(g, XcdLogical(blockIdx.x, gridDim.x),
+  SplitTile<kW8, kMulti, kA8>(g, XcdLogical(blockIdx.x, gridDim.x),
                          __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
                          blockDim.x / 64, lds_part, lds_flag, false, nullptr, nullptr, 0);
 }
@@ -755,6 +788,9 @@ hipError_t LaunchSplitLinear(const GemmArgs& args, hipStream_t stream) {
   if (w8) {
     if (multi) hipLaunchKernelGGL((SplitKernel<true, true>), grid, block, 0, stream, args);
     else hipLaunchKernelGGL((SplitKernel<true, false>), grid, block, 0, stream, args);
+  } else if (args.a_fp8) {
+    if (multi) hipLaunchKernelGGL((SplitKernel<false, true, true>), grid, block, 0, stream, args);
+    else hipLaunchKernelGGL((SplitKernel<false, false, true>), grid, block, 0, stream, args);
   } else {
     if (multi) hipLaunchKernelGGL((SplitKernel<false, true>), grid, block, 0, stream, args);
     else hipLaunchKernelGGL((SplitKernel<false, false>), grid, block, 0, stream, args);

@@ -207,8 +207,15 @@ typedef struct hb_ep_op {
 /* flags: HB_LINEAR_EXACT or HB_LINEAR_FAST, optionally | HB_LINEAR_PANELS
  * (the W planes are weight panels from hb_pack_weights, not DDR words) or
  * | HB_LINEAR_W8_PANELS (a W8 layer's planes are W8 panels from hb_pack_w8;
- * w[0] and w[1] both point at them). */
-enum { HB_LINEAR_EXACT = 0, HB_LINEAR_FAST = 1, HB_LINEAR_PANELS = 2, HB_LINEAR_W8_PANELS = 4 };
+ * w[0] and w[1] both point at them); | HB_LINEAR_A_FP8: A holds MXFP8 E4M3
+ * codes (hb_encode_mxfp8) instead of MXINT8, against one MXFP4 plane. */
+enum {
+  HB_LINEAR_EXACT = 0,
+  HB_LINEAR_FAST = 1,
+  HB_LINEAR_PANELS = 2,
+  HB_LINEAR_W8_PANELS = 4,
+  HB_LINEAR_A_FP8 = 8
+};
 enum { HB_MAX_PIECES = 16, HB_MAX_EP_OPS = 8, HB_MAX_GROUP = 4 };
 
 /* C = A x W^T as the emitted instruction sequence computes it:
@@ -251,7 +258,16 @@ typedef struct hb_linear_desc {
    * computed exactly.  | HB_LINEAR_PANELS: w[] are weight panels.
    * | HB_LINEAR_W8_PANELS: w[0] = w[1] = W8 panels (one piece over every
    * block; a, w 16-byte aligned); exact mode then folds each output on its
-   * own, correct but slow: use DDR words for exact work. */
+   * own, correct but slow: use DDR words for exact work.
+   * | HB_LINEAR_A_FP8 (no counterpart in the reference, which quantizes
+   * activations to MXINT8 only): A's 32 code bytes per row and block are
+   * OCP E4M3 (E4M3FN; the NaN codes 0x7F / 0xFF are not valid input), its
+   * scale bytes E8M0; one MXFP4 plane (modes {0}), DDR words or panels.
+   * Exact: each block's exact sum of products, S * 2^-9 * 2^-1 in integer
+   * units, is rounded once to FP32 (RNE, below normal -> +0) and the blocks
+   * fold as above.  Fast: one layer of up to 1,024 rows on FP8 x FP4
+   * matrix cores, within the fast-mode bound; other fast layers (batches,
+   * more rows) fold exactly per output. */
   uint32_t flags;
   /* 0: A is [ceil(m/4)][kb_total] words.  Otherwise A words per quad, and
    * each piece's blocks start at its a_word (see hb_piece); every A word a
@@ -514,6 +530,13 @@ int hb_rows_async(hb_ctx* ctx, const hb_rows_desc* desc);
  * as 0 and the call returns HB_EINVAL after the launch. */
 int hb_encode_mxint8(hb_ctx* ctx, const float* x, uint32_t rows,
                      uint32_t cols, void* out);
+/* The MXFP8 E4M3 encoding into the same word layout (no counterpart in the
+ * reference): per row and 32-column block, the OCP MX rule -- block
+ * exponent floor(log2 max|x|) - 8, clamped to [-127, 127] (0 for a zero
+ * block), elements x * 2^-exponent rounded to nearest even on the E4M3
+ * grid and saturated to +-448.  Inf/NaN: HB_EINVAL, as hb_encode_mxint8. */
+int hb_encode_mxfp8(hb_ctx* ctx, const float* x, uint32_t rows,
+                    uint32_t cols, void* out);
 
 /* Weight preparation, the compiler's conversions on device (for a runtime
  * that loads checkpoints straight into GPU memory).  A weight matrix row is

@@ -1,0 +1,201 @@
+"""MXFP8 E4M3 activations (HB_LINEAR_A_FP8, no counterpart in the
+reference) on an MI355X against the oracle's definition (hb_oracle.c,
+pinned in test_oracle_fp8.py):
+
+  * hb_encode_mxfp8 byte for byte against the oracle's OCP MX encoder
+    (zero, subnormal and saturating blocks, ragged rows and K, Inf
+    rejected);
+  * exact mode bitwise: ops with requantize, pieces, `onto`, weight panels,
+    a batch of layers;
+  * fast mode (FP8 x FP4 matrix cores) within the MXFP8 fast bound
+    (check_fp8_fast) at config 1's sweep M in {1, 16, 128, 1024} (K = 2560,
+    N = 960) and M = 141, with ops and requantize, and with scale bytes
+    outside the fast window (those tiles are computed exactly, bitwise);
+  * the descriptor rule (one MXFP4 plane).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import helpers
+import hotarubi_amd as hb
+import oracle
+from test_gpu_bench_routes import DEV, dev, host, mxfp4_planes, say, to_panels
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("rows,cols", [(4, 32), (13, 50), (128, 2560), (1001, 96)])
+def test_encode_mxfp8(gpu, rows, cols):
+    rng = np.random.default_rng(700 + rows)
+    x = (rng.standard_normal((rows, cols)) * 2.0 ** rng.integers(-30, 30, (rows, 1))).astype(np.float32)
+    x[0, :min(32, cols)] = 0.0
+    if rows > 2:
+        x[1, :min(32, cols)] = np.float32(1e-41)           # subnormal block
+        x[2, 0] = np.float32(1.9 * 2.0 ** 20)              # scaled past 448: saturates
+    quads, blocks = (rows + 3) // 4, (cols + 31) // 32
+    out = torch.full((quads * blocks, 144), 0xA5, dtype=torch.uint8, device=DEV)
+    say("encode_mxfp8", dict(rows=rows, cols=cols))
+    hb.encode_mxfp8(dev(x), rows, cols, out, ctx=gpu)
+    xp = np.zeros((quads * 4, cols), np.float32)
+    xp[:rows] = x
+    q, e = oracle.encode_mxfp8(oracle.f32_bits(xp))
+    assert np.array_equal(host(out), oracle.pack_abuf(q.view(np.int8), e))
+
+
+def test_encode_mxfp8_rejects_inf(gpu):
+    x = np.ones((4, 32), np.float32)
+    x[2, 5] = np.inf
+    out = torch.zeros((32, 144), dtype=torch.uint8, device=DEV)
+    with pytest.raises(hb.HbError) as err:
+        hb.encode_mxfp8(dev(x), 4, 32, out, ctx=gpu)
+    assert err.value.code == hb.HB_EINVAL and "MXFP8" in err.value.message
+
+
+def fp8_layer(gpu, m, n, kb, mode, ops_fn=None, quantize=False, tbuf=None, seed=0,
+              pieces=None, onto=False, panels=False, w_lo=-10, w_hi=-2, a_scale=1.0):
+    rng = np.random.default_rng(seed)
+    a = helpers.activations_fp8(rng, m, kb * 32, a_scale)[1]
+    code, e = helpers.mxfp4_weights(rng, n, kb * 32, w_lo, w_hi)
+    planes = [oracle.pack_wbuf(code, e)]
+    w_dev = [dev(planes[0])]
+    if panels:
+        w_dev = [to_panels(gpu, w_dev[0], n, kb)]
+    ops = ops_fn(rng, m, n) if ops_fn else []
+    dev_ops = [(k, dev(v.view(np.float32)) if isinstance(v, np.ndarray) else v) for k, v in ops]
+    c0 = helpers.random_fp32_words(rng, (m, n), 118, 128) if onto else np.zeros((m, n), np.uint32)
+    c_d = dev(c0.view(np.float32))
+    q_d = torch.zeros(((m + 3) // 4 * (n // 32), 144), dtype=torch.uint8, device=DEV) \
+        if quantize else None
+    tb_d = dev(tbuf.view(np.int64)) if tbuf is not None else None
+    say("fp8 layer", dict(m=m, n=n, kb=kb, mode=mode, ops=[o[0] for o in ops], quantize=quantize,
+                          pieces=pieces, onto=onto, panels=panels))
+    hb.linear(gpu, a=dev(a), planes=w_dev, modes=[0], c=c_d, m=m, n=n, kb_total=kb, ops=dev_ops,
+              tbuf=tb_d, q_out=q_d, mode=mode, pieces=pieces, onto=onto, panels=panels,
+              a_fp8=True)
+    got = host(c_d).view(np.uint32)
+    gq = host(q_d) if quantize else None
+    want, wq = helpers.oracle_linear_mt(m, n, kb, a, planes, [0], ops=ops, tbuf=tbuf,
+                                        quantize=quantize, pieces=pieces,
+                                        onto=c0 if onto else None, a_fp8=True)
+    fp8_layer.abs_sums = (lambda: fp8_abs_sums(m, n, kb, a, planes[0]))
+    return got, gq, want, wq
+
+
+FP8_INT = np.array([oracle.fp8_int(c) for c in range(256)], np.float64)
+E2M1_INT = np.array([0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12], np.float64)
+
+
+def fp8_abs_sums(m, n, kb, a_words, w_words):
+    """sum over blocks of |block value| per output (the scale of the fast
+    path's accumulation error), from the DDR words."""
+    aw = np.asarray(a_words).reshape(-1, kb, 144)
+    ww = np.asarray(w_words).reshape(n // 8, kb, 144)
+    tot = np.zeros((m, n))
+    for b in range(kb):
+        codes = aw[:, b, :128].reshape(-1, 4, 32).reshape(-1, 32)[:m]
+        ea = aw[:, b, 128:132].reshape(-1)[:m].astype(np.int64)
+        ai = FP8_INT[codes]
+        nib = ww[:, b, :128].reshape(n // 8, 8, 16)
+        wc = np.stack([nib & 15, nib >> 4], -1).reshape(n, 32)
+        ew = ww[:, b, 128:136].reshape(-1).astype(np.int64)
+        s = np.abs(ai @ E2M1_INT[wc].T)
+        tot += s * np.exp2((ea[:, None] + ew[None, :] - 264).astype(np.float64))
+    return tot
+
+
+def check_fp8_fast(got, want, abs_sums, gq=None, wq=None):
+    """MXFP8 fast-mode bound, an envelope measured on the matrix cores (not
+    a proof): their sum of an instruction's 64 FP8 x FP4 products keeps
+    about 15 bits below its largest term (E4M3 spans 17 binades), where the
+    MXINT8 path's FP6 planes sum exactly.  Measured worst: 1.44e-5 per row
+    and 2^-14.8 of sum |block value| per element; checked with margin: per
+    output row max |gpu - ref| <= 1e-4 max |ref|, per element |gpu - ref| <=
+    2^-13 sum |block value|.  (Exact mode is bitwise.)"""
+    g, w = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
+    err = np.abs(g - w)
+    row = np.abs(w).max(axis=1, keepdims=True)
+    r1 = float((err / np.maximum(row, 1e-300)).max())
+    r2 = float((err / np.maximum(abs_sums, 1e-300)).max())
+    say("fp8 fast error", dict(normwise=r1, per_element_log2=float(np.log2(max(r2, 1e-300)))))
+    assert r1 <= 1e-4 and r2 <= 2.0 ** -13, (r1, r2)
+    if gq is not None:
+        gqb = gq.reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
+        wqb = wq.reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
+        assert np.abs(gqb - wqb).max() <= 1 and (gqb != wqb).mean() < 0.01
+
+
+def per_channel(r, m, n):
+    return [(hb.EP_MULP, np.asarray(r.uniform(0.5, 2.0, n), np.float32).view(np.uint32)),
+            (hb.EP_ADDP, np.asarray(r.normal(0, 0.1, n), np.float32).view(np.uint32))]
+
+
+@pytest.mark.parametrize("m,n,kb,kw", [
+    (50, 256, 23, dict(ops_fn=lambda r, m, n: per_channel(r, m, n) + [(hb.EP_ACT, None)],
+                       quantize=True, tbuf=helpers.activation_table("silu"))),
+    (141, 320, 30, dict(pieces=[(0, 12), (12, 18)], onto=True)),
+    (64, 512, 16, dict(panels=True, quantize=True)),
+    (200, 96, 7, dict(ops_fn=lambda r, m, n: [(hb.EP_ADD, helpers.random_fp32_words(r, (m, n), 118, 128))]))])
+def test_exact_bitwise(gpu, m, n, kb, kw):
+    got, gq, want, wq = fp8_layer(gpu, m, n, kb, hb.EXACT, seed=710 + m, **kw)
+    assert np.array_equal(got, want)
+    if gq is not None:
+        assert np.array_equal(gq, wq)
+
+
+def test_exact_batched(gpu):
+    rng = np.random.default_rng(720)
+    m, n, kb, layers = 36, 128, 6, 3
+    a = [helpers.activations_fp8(rng, m, kb * 32)[1] for _ in range(layers)]
+    w = [mxfp4_planes(rng, n, kb)[0][0] for _ in range(layers)]
+    a_d, w_d = dev(np.concatenate(a)), dev(np.concatenate(w))
+    c = torch.zeros((layers, m, n), dtype=torch.float32, device=DEV)
+    descs = [hb.linear_desc(m, n, kb, a_d[i * len(a[0]):(i + 1) * len(a[0])],
+                            [w_d[i * len(w[0]):(i + 1) * len(w[0])]], [0], c[i], mode=hb.EXACT,
+                            a_fp8=True) for i in range(layers)]
+    say("fp8 exact batched", dict(layers=layers))
+    hb.linear_batched(descs, gpu)
+    got = host(c).view(np.uint32)
+    for i in range(layers):
+        want, _ = oracle.linear(m, n, kb, a[i], [w[i]], [0], a_fp8=True)
+        assert np.array_equal(got[i], want)
+
+
+@pytest.mark.parametrize("m", [1, 16, 128, 1024])
+def test_fast_config1_sweep(gpu, m):
+    got, _, want, _ = fp8_layer(gpu, m, 960, 80, hb.FAST, seed=730 + m)
+    check_fp8_fast(got, want, fp8_layer.abs_sums())
+
+
+def test_fast_plain_141(gpu):
+    got, _, want, _ = fp8_layer(gpu, 141, 960, 30, hb.FAST, seed=741)
+    check_fp8_fast(got, want, fp8_layer.abs_sums())
+
+
+def test_fast_ops_requantize(gpu):
+    got, gq, want, wq = fp8_layer(gpu, 141, 960, 30, hb.FAST, per_channel, quantize=True,
+                                  seed=740)
+    g, w = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
+    row = np.abs(w).max(axis=1, keepdims=True)
+    assert (np.abs(g - w) <= 1e-4 * row).all()
+    gqb = gq.reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
+    wqb = wq.reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
+    assert np.abs(gqb - wqb).max() <= 1 and (gqb != wqb).mean() < 0.01
+
+
+def test_fast_out_of_window_scales_exact(gpu):
+    """W scale bytes 40..60 (below the fast window): every tile is folded
+    exactly, so the result is the exact one, bit for bit."""
+    got, _, want, _ = fp8_layer(gpu, 50, 256, 12, hb.FAST, seed=750, w_lo=-87, w_hi=-67)
+    assert np.array_equal(got, want)
+
+
+def test_fp8_needs_one_mxfp4_plane(gpu):
+    a = torch.zeros((16, 144), dtype=torch.uint8, device=DEV)
+    w = torch.zeros((8 * 1, 144), dtype=torch.uint8, device=DEV)
+    c = torch.zeros((4, 64), dtype=torch.float32, device=DEV)
+    with pytest.raises(hb.HbError) as err:
+        hb.linear(gpu, a=a, planes=[w, w], modes=[1, 2], c=c, m=4, n=64, kb_total=1, a_fp8=True)
+    assert err.value.code == hb.HB_EINVAL and "MXFP8" in err.value.message

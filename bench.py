@@ -167,7 +167,7 @@ class Workload:
     layers read the panels."""
 
     def __init__(self, hb, torch, ctx, m, n, kb, w8, layers, mode, epilogue=False, seed=1,
-                 panels=False):
+                 panels=False, a_fp8=False):
         dev = "cuda:0"
         self.m, self.n, self.kb, self.w8, self.layers = m, n, kb, w8, layers
         self.n_vectors = 2 if epilogue else 0
@@ -177,7 +177,7 @@ class Workload:
         self.a = torch.empty((L, quads * kb, 144), dtype=torch.uint8, device=dev)
         for i in range(L):
             x = torch.randn((m, kb * 32), generator=g, device=dev)
-            hb.encode_mxint8(x, m, kb * 32, self.a[i], ctx=ctx)
+            (hb.encode_mxfp8 if a_fp8 else hb.encode_mxint8)(x, m, kb * 32, self.a[i], ctx=ctx)
             del x
         planes = 2 if w8 else 1
         w = [torch.randint(0, 256, (L, n // 8 * kb, 144), generator=g, device=dev,
@@ -207,7 +207,7 @@ class Workload:
         modes = [1, 2] if w8 else [0]
         self.descs = [hb.linear_desc(m, n, kb, self.a[i], [p[i] for p in self.w], modes,
                                      self.c[i], ops=[(k, t[i]) for k, t in ops_t], mode=mode,
-                                     panels=panels)
+                                     panels=panels, a_fp8=a_fp8)
                       for i in range(L)]
         torch.cuda.synchronize()
 
@@ -809,7 +809,7 @@ def time_chain(torch, ctx, work, steps=10, graph=True):
     eager = t0.elapsed_time(t1) / steps
     out = {"m": work.m, "gemms": len(work.descs), "gops": round(work.ops / 1e9, 3),
            "eager_ms": round(eager, 4)}
-    if work.grouped and len(work.plan) < len(work.descs):
+    if getattr(work, "grouped", False) and len(work.plan) < len(work.descs):
         out["launch_calls"] = len(work.plan)
         work.grouped = False  # the same chain, one call per layer, for comparison
         for _ in range(2):
@@ -920,12 +920,12 @@ def summarize(work, ms, mfma_class, line=None):
     return tops, roof
 
 
-def single_layer_latency(hb, torch, ctx, stream, m, n, kb, launches=50):
+def single_layer_latency(hb, torch, ctx, stream, m, n, kb, launches=50, a_fp8=False):
     """Milliseconds per launch of one MXFP4 layer (fast mode, weights in
     panels), launched back to back on one stream: its one-launch latency,
     as a chain of dependent layers sees it (a launch starts when the one
     before it has ended)."""
-    work = Workload(hb, torch, ctx, m, n, kb, False, 1, hb.FAST, seed=9, panels=True)
+    work = Workload(hb, torch, ctx, m, n, kb, False, 1, hb.FAST, seed=9, panels=True, a_fp8=a_fp8)
     d = work.descs[0]
     settle(lambda: hb.launch(d, ctx), torch, 0.05)
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -1322,6 +1322,16 @@ def main():
                         "on one stream, weights in panels",
             **{f"M={m}": single_layer_latency(hb, torch, ctx, stream, m, n, kb)
                for m in (1, 16, 128, 1024)}}
+        # config 1 with MXFP8 E4M3 activations (OCP MX encoding; no reference
+        # counterpart): one layer per launch on the FP8 x FP4 matrix cores
+        fp8 = {"workload": f"one MXFP4 layer K={kb * 32} N={n} per launch, activations MXFP8 "
+                           "E4M3 (hb_encode_mxfp8), weights in panels, fast mode"}
+        for m in (1, 16, 128, 1024):
+            ms_l = single_layer_latency(hb, torch, ctx, stream, m, n, kb, a_fp8=True)
+            nbytes = layer_bytes(m, n, kb, 4)
+            fp8[f"M={m}"] = {"ms": ms_l, "tops": round(2.0 * m * n * kb * 32 / (ms_l * 1e-3) / 1e12, 3),
+                             "hbm_frac": round(nbytes / (ms_l * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        out["mxfp8_single_layer"] = fp8
         # W8 layer with per-channel scale and bias, fast and exact
         L8 = 128
         w8 = {"workload": f"W8 linear M=64 K=960 N=2560 + MULP + ADDP, {L8} layers per step"}

@@ -676,7 +676,7 @@ namespace {
 // 256 of 2 by 9-13% (the split sums written and read again cost more than the
 // parallelism gains); 32 workgroups, or no split, lost 50-70% at M = 141.
 constexpr uint32_t kSmallGrid = 128, kTargetWorkgroups = 128, kMinSplitSteps = 4;
-constexpr uint32_t kSplitMidRows = 1024;
+constexpr uint32_t kSplitMidRows = 1024, kSplitMidWork = 65536;
 }  // namespace
 
 hipError_t GrowWorkspace(Workspace& ws, size_t bytes, hipStream_t stream) {
@@ -786,9 +786,14 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   // A layer of up to kSplitMidRows rows whose 128-row grid is small: the
   // single-launch split kernel's 32 x 32 tiles (enough workgroups, no
   // partial sums through memory, no second launch) instead of K splits of
-  // 128-row tiles and the epilogue kernel (SparseDrive-S's head at 928
-  // rows: 2x faster; at 1,600 rows and more the 128-row tiles win).
-  if (small && fastk && args.quads * 4 <= kSplitMidRows) {
+  // 128-row tiles and the epilogue kernel, while rows x K blocks stays
+  // within kSplitMidWork (measured, one layer per launch: 928 x 512 x 512
+  // 7.3 against 16.1 us, 512 x 2560 x 960 18.1 against 25.9 us, 768 rows
+  // even, 1024 x 2560 x 960 34.3 against 28.9 us).
+  uint32_t blocks = 0;
+  for (uint32_t p = 0; p < args.n_pieces; ++p) blocks += args.piece_kb[p];
+  if (small && fastk && args.quads * 4 <= kSplitMidRows &&
+      args.quads * 4 * blocks <= kSplitMidWork) {
     SplitPlan(args);
     args.fast_ep = 1u;
     return LaunchSplitLinear(args, stream);

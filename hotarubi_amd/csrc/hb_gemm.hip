@@ -778,7 +778,7 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
   // workgroup, which holds every row.
   if (fastk && args.quads * 4 <= 16) return LaunchLinearSkinny(args, batch, stream);
   uint32_t gx, gy;
-  if (fastk) FastGrid(args, &gx, &gy, &args.tile_rows);
+  if (fastk) FastGrid(args, batch, &gx, &gy, &args.tile_rows);
   else ExactGrid(args, &gx, &gy);
   args.gx = gx;
   args.gy = gy;

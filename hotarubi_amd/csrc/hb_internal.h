@@ -256,9 +256,12 @@ hipError_t LaunchLinear(const GemmArgs& args, uint32_t batch, bool fast, Workspa
 // Fast path (hb_fast.hip): block-scaled f8f6f4 MFMA for one FP4 plane or
 // the W8 planes (hi, lo), in that order.
 bool FastEligible(const GemmArgs& args);
-// Tile grid of the fast kernel for `args`: column tiles, row tiles, rows per
-// tile.
-void FastGrid(const GemmArgs& args, uint32_t* gx, uint32_t* gy, uint32_t* tile_rows);
+// Tile grid of the fast kernel for `args` in a launch of `layers` such
+// layers: column tiles, row tiles, rows per tile.
+void FastGrid(const GemmArgs& args, uint32_t layers, uint32_t* gx, uint32_t* gy,
+              uint32_t* tile_rows);
+// Launches the fast kernel over args.gx x args.gy tiles of args.tile_rows
+// rows (FastGrid's) and `batch` layers or K splits.
 hipError_t LaunchLinearFast(const GemmArgs& args, uint32_t batch, hipStream_t stream);
 // Streaming MXFP4 kernel (hb_fast4.hip) for 128-row tiles of plain layers
 // (no ops, no requantize, no K splits); `args` carries the tile grid.

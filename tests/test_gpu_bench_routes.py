@@ -12,8 +12,10 @@ tools/iss/lane.cpp):
   * the SigLIP-style W8 MLP, up 768->3072 with MULP, ADDP, GELU and the
     requantize and down 3072->768 with MULP and ADDP, at M=2048, both modes;
   * SmolVLA prefix layers at batch 32 (M=4512: q with requantize, k with
-    requantize, down with the residual add) and the action expert's
-    720->2048 gate with ACT_MUL(up) and requantize at batch 32 (M=1600);
+    requantize, down with the residual add) and the action expert's layers
+    at batch 32 (M=1600: q with requantize, down with the residual add, both
+    K-split over 64-row tiles; the 720->2048 gate with ACT_MUL(up) and
+    requantize, 200 unsplit 64-row tiles);
   * A operands whose codes cover all 256 int8 values, -128 included, through
     every fast route and the exact kernel.
 
@@ -208,6 +210,18 @@ def test_prefix_b32_down_residual(gpu):
     single_layer(gpu, 4512, 960, 80, False, hb.FAST,
                  lambda r, m, n: [(hb.EP_ADD, helpers.random_fp32_words(r, (m, n), 118, 128))],
                  seed=95)
+
+
+def test_expert_b32_q_requantize(gpu):
+    """720 -> 960 at M=1600: 100 tiles of 64 rows, K split, epilogue kernel."""
+    single_layer(gpu, 1600, 960, 23, False, hb.FAST, quantize=True, seed=98)
+
+
+def test_expert_b32_down_residual(gpu):
+    """2048 -> 720 at M=1600: 75 tiles of 64 rows, K split over 64 blocks."""
+    single_layer(gpu, 1600, 720, 64, False, hb.FAST,
+                 lambda r, m, n: [(hb.EP_ADD, helpers.random_fp32_words(r, (m, n), 118, 128))],
+                 seed=99)
 
 
 def test_expert_b32_gate_act_mul_requantize(gpu):

@@ -78,7 +78,7 @@ def run_both(gpu, m, n, kb, a, planes, modes, mode, ops=(), layers=1):
 
 def test_two_calls_in_a_row_second_smaller(gpu):
     rng = np.random.default_rng(11)
-    # 1100 x 512 x 512 MXFP4: more than 1,024 rows on 18 tiles of 128 x 256,
+    # 1100 x 512 x 512 MXFP4: more than 1,024 rows on 36 tiles of 64 x 256,
     # so K splits through the array (2 splits, ~4.5 MB of partial sums)
     m, n, kb = 1100, 512, 16
     a, planes, modes = mxfp4_layer(rng, m, n, kb)
@@ -177,11 +177,11 @@ def test_graph_capture_of_a_new_shape(gpu):
 
 
 def test_oversize_layer_is_rejected(gpu):
-    # 2048 x 1024 x 2048 MXFP4: 64 tiles of 128 x 256 (more than 1,024 rows,
-    # so the K-split route), 2 K splits, ~16.8 MB of partial sums, over the
-    # 8 MiB array
+    # 2048 x 512 x 2048 MXFP4: 64 tiles of 64 x 256 (more than 1,024 rows,
+    # so the K-split route), 2 K splits: 8 MiB of partial sums, plus the
+    # split counters and flags, over the 8 MiB array
     rng = np.random.default_rng(15)
-    m, n, kb = 2048, 1024, 64
+    m, n, kb = 2048, 512, 64
     a = helpers.activations(rng, m, kb * 32)[1]
     w = torch.zeros((n // 8 * kb, 144), dtype=torch.uint8, device=DEV)
     c = torch.zeros((m, n), dtype=torch.float32, device=DEV)

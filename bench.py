@@ -306,9 +306,13 @@ class Chain:
         self.plan.append([len(self.descs) - 1])
         self.ops += 2.0 * self.m * n * kb * 32
         vectors = sum(1 for k, _ in ops if k in (self.hb.EP_ADDP, self.hb.EP_MULP))
-        out = self.m * n * (1 + 1 / 32) if q is not None else 4 * self.m * n
-        self.bytes += layer_bytes(self.m, n, kb, 8 if len(planes) == 2 else 4, vectors) - \
-            4 * self.m * n + out + (4 * self.m * n if onto else 0)
+        # C (fp32) is written whether or not the layer requantizes; the
+        # MXINT8 words (codes and scale bytes) come on top, and every [m][n]
+        # operand (ADD, ACT_MUL) and an `onto` C are read in full
+        matrices = sum(1 for k, _ in ops if k in (self.hb.EP_ADD, self.hb.EP_ACT_MUL))
+        self.bytes += layer_bytes(self.m, n, kb, 8 if len(planes) == 2 else 4, vectors) + \
+            (self.m * n * (1 + 1 / 32) if q is not None else 0) + \
+            4 * self.m * n * (matrices + (1 if onto else 0))
 
     def group(self, k):
         """The last k layers added form one group launch (layers the model

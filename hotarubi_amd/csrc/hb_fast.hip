@@ -451,18 +451,28 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
         if (row_h + row_step(i) < g.m && col < g.n) c_r[off_l] = __float_as_uint(y[i]);
       }
       if (q_out != nullptr) {  // MXINT8 requantize over the 32 lanes holding a row's block
-        const uint32_t nb = g.n >> 5, blk = (col - (l & 31)) >> 5;
+        // Values i < 4 are rows row_h .. row_h + 3, i >= 4 rows row_h + 8 ..
+        // row_h + 11 (row_h is a multiple of 4): quads row_h / 4 and
+        // row_h / 4 + 2, one DDR word each.  Per word: the 4 block maxima
+        // (their lane moves overlap), one bounds check and address, the 4
+        // rows' codes, then lanes 0..15 write bytes 128..143 (the 4 scale
+        // bytes, 12 zero bytes) with one store.
+        const uint32_t nb = g.n >> 5, blk = (col - (l & 31)) >> 5, c32 = l & 31;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t v = __float_as_uint(y[i]), row = row_h + row_step(i);
-          const uint32_t x = HalfMax32(ExpField(v));
-          if ((row >> 2) < g.quads && blk < nb) {
-            uint8_t* word = q_out + ((size_t)(row >> 2) * nb + blk) * kDdrWord;
-            word[(row & 3) * 32 + (l & 31)] = QuantizeElement(v, x);
-            if ((l & 31) == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(x);
-            if ((l & 31) < 12 && (row & 3) == 0) word[132 + (l & 31)] = 0;
+        for (int h = 0; h < 2; ++h) {
+          uint32_t x[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) x[r] = HalfMax32(ExpField(__float_as_uint(y[4 * h + r])));
+          const uint32_t quad = (row_h >> 2) + 2 * h;
+          if (quad < g.quads && blk < nb) {
+            uint8_t* word = q_out + ((size_t)quad * nb + blk) * kDdrWord;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              word[r * 32 + c32] = QuantizeElementHw(__float_as_uint(y[4 * h + r]), x[r]);
+            const uint32_t sb = ScaleByteOf(x[0]) | ScaleByteOf(x[1]) << 8 |
+                               ScaleByteOf(x[2]) << 16 | ScaleByteOf(x[3]) << 24;
+            if (c32 < 16) word[128 + c32] = c32 < 4 ? (uint8_t)(sb >> (8 * c32)) : 0;
           }
-          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }

@@ -578,7 +578,7 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
 #pragma unroll
             for (int v = 0; v < 4; ++v)
               word[v * 32 + jj * 16 + row16] =
-                  QuantizeElement(__float_as_uint(res[i][4 * (jb + jj) + v]), emax[v]);
+                  QuantizeElementHw(__float_as_uint(res[i][4 * (jb + jj) + v]), emax[v]);
           const uint32_t e_own =
               row16 == 0 ? emax[0] : row16 == 1 ? emax[1] : row16 == 2 ? emax[2] : emax[3];
           if (row16 < 4) word[128 + row16] = (uint8_t)ScaleByteOf(e_own);

@@ -358,7 +358,7 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
       if (in) {
         const uint32_t nb = g.n >> 5, c32 = col & 31;
         uint8_t* word = q_out + ((size_t)(row >> 2) * nb + (col >> 5)) * kDdrWord;
-        word[(row & 3) * 32 + c32] = QuantizeElement(y, e);
+        word[(row & 3) * 32 + c32] = QuantizeElementHw(y, e);
         if (c32 == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(e);
         if (c32 < 12 && (row & 3) == 0) word[132 + c32] = 0;
       }
@@ -666,15 +666,16 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
       for (int i = 0; i < 4; ++i)
         ex[i] = HalfMax32((row_of(4 * j + i) >> 2) < g.quads && col_in
                               ? ExpField(__float_as_uint(y[i])) : 0u);
+      // the 4 values are rows 0..3 of one quad: one DDR word; lanes 0..15
+      // then write its bytes 128..143 (4 scale bytes, 12 zeros) in one store
+      const uint32_t quad = row_of(4 * j) >> 2;
+      if (quad < g.quads && col_in) {
+        uint8_t* word = g.q_out + ((size_t)quad * (g.n >> 5) + (col >> 5)) * kDdrWord;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t row = row_of(4 * j + i);
-        if ((row >> 2) < g.quads && col_in) {
-          uint8_t* word = g.q_out + ((size_t)(row >> 2) * (g.n >> 5) + (col >> 5)) * kDdrWord;
-          word[(row & 3) * 32 + r32] = QuantizeElement(__float_as_uint(y[i]), ex[i]);
-          if (r32 == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(ex[i]);
-          if (r32 < 12 && (row & 3) == 0) word[132 + r32] = 0;
-        }
+        for (int i = 0; i < 4; ++i) word[i * 32 + r32] = QuantizeElementHw(__float_as_uint(y[i]), ex[i]);
+        const uint32_t sb = ScaleByteOf(ex[0]) | ScaleByteOf(ex[1]) << 8 |
+                           ScaleByteOf(ex[2]) << 16 | ScaleByteOf(ex[3]) << 24;
+        if (r32 < 16) word[128 + r32] = r32 < 4 ? (uint8_t)(sb >> (8 * r32)) : 0;
       }
     }
     if (y_lds) {

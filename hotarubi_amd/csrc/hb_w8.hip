@@ -482,7 +482,7 @@ void W8Kernel(GemmArgs g) {
       uint32_t packed = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        packed |= (uint32_t)QuantizeElement(__float_as_uint(y[4 * i + j]), x) << (8 * j);
+        packed |= (uint32_t)QuantizeElementHw(__float_as_uint(y[4 * i + j]), x) << (8 * j);
       if ((row >> 2) < g.quads && blk < nb) {
         uint8_t* word = q_out + ((size_t)(row >> 2) * nb + blk) * kDdrWord;
         uint8_t* dst = word + (row & 3) * 32 + 4 * cg;

@@ -156,15 +156,18 @@ def w8_layer(gpu, m, n, kb, mode, ops_fn=None, quantize=False, tbuf=None, all_co
             helpers.check_fast(got[i], want, gq[i] if quantize else None, wq, bound=bound)
 
 
-# ---- the tile widths (2, 3 and 4 panels: chosen by column count) ----
+# ---- the tile widths (1 to 4 panels, chosen by rows and column count) ----
 
 @pytest.mark.parametrize("m,n,kb", [
-    (128, 256, 12),    # 4 panels, one tile
+    (128, 256, 12),    # 1 panel per tile, 4 tiles
     (256, 768, 24),    # out-proj width
     (128, 2304, 8),    # QKV width
     (200, 72, 3),      # a partial last panel and tile, odd blocks
     (1, 96, 5),        # one row
-    (131, 512, 1)])    # one block
+    (131, 512, 1),     # one block
+    (2048, 1536, 4),   # 2 panels per tile (192 tiles)
+    (2048, 2304, 5),   # 3 panels (192 tiles), odd blocks
+    (2048, 4096, 4)])  # 4 panels (256 tiles)
 def test_fast_shapes(gpu, m, n, kb):
     w8_layer(gpu, m, n, kb, hb.FAST, seed=m + n + kb)
 

@@ -382,6 +382,12 @@ int Rows(hb_ctx* ctx, const hb_rows_desc* d, bool sync) {
   if (!d->x || (d->y == nullptr) == (d->q_out == nullptr))
     return Fail(HB_EINVAL, "need x and exactly one of y, q_out");
   if (d->q_out && d->cols % 32 != 0) return Fail(HB_EINVAL, "q_out needs cols %% 32 == 0");
+  // fp32 rows and vectors are read and written as words, the DDR words'
+  // codes as dwords
+  const void* bufs[] = {d->x, d->y, d->q_out, d->gamma, d->beta};
+  for (const void* ptr : bufs)
+    if (reinterpret_cast<uintptr_t>(ptr) % 4 != 0)
+      return Fail(HB_EINVAL, "row buffers must be 4-byte aligned");
   if (d->entry != HB_ROWS_SOFTMAX && !d->gamma) return Fail(HB_EINVAL, "the norm needs gamma");
   if (d->entry == HB_ROWS_LAYERNORM && !d->beta) return Fail(HB_EINVAL, "LAYERNORM needs beta");
   // the program reads beta from PBUF word p_base + n8/4: a separate row only

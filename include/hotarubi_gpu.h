@@ -506,8 +506,9 @@ int hb_gacc_async(hb_ctx* ctx, const hb_gacc_desc* desc);
  *   q_out   MXINT8 DDR words [ceil(rows/4)][cols/32] x 144 B (PackAbuf,
  *           the A of hb_linear); cols a multiple of 32.  Exactly one of y,
  *           q_out.
- * Rows of the last quad past `rows` are computed as zero rows (they reach
- * q_out's last words, not y).  Bitwise the NPU's result. */
+ * Every buffer is 4-byte aligned (HB_EINVAL otherwise).  Rows of the last
+ * quad past `rows` are computed as zero rows (they reach q_out's last words,
+ * not y).  Bitwise the NPU's result. */
 enum { HB_ROWS_SOFTMAX = 12, HB_ROWS_LAYERNORM = 22, HB_ROWS_RMSNORM = 34 };
 typedef struct hb_rows_desc {
   uint32_t entry, rows, cols, aux, imm;

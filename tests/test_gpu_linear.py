@@ -436,6 +436,26 @@ def test_fast_out_of_window_scales_recompute_exactly(gpu, w8):
 
 
 @pytest.mark.parametrize("w8", [False, True])
+def test_fast_k_split_64_row_tiles_out_of_window(gpu, w8):
+    """1100 x 512 x 512: more than 1,024 rows on 36 tiles of 64 rows, so K
+    splits whose partial sums and window flags go to the epilogue kernel.
+    Rows 64..127 (the second row tile) carry an out-of-window scale byte:
+    that row tile recomputes exactly, bit for bit; the rest stays within
+    the fast-mode tolerance."""
+    rng = np.random.default_rng(66 + w8)
+    m, n, k = 1100, 512, 512
+    kb, a, planes, modes = make_layer(rng, m, n, k, w8)
+    a = a.copy()
+    a.reshape(-1, kb, 144)[16:32, 3, 128] = 60   # rows 64..127
+    got, _ = run_linear(gpu, m, n, kb, a, planes, modes, mode=hb.FAST)
+    want, _ = oracle_linear(m, n, kb, a, planes, modes)
+    assert_bits(got[64:128], want[64:128])
+    g, w = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
+    row_scale = np.abs(w).max(axis=1, keepdims=True)
+    assert (np.abs(g - w) <= 1e-5 * row_scale).all()
+
+
+@pytest.mark.parametrize("w8", [False, True])
 def test_fast_skinny_out_of_window_and_onto(gpu, w8):
     """A layer of at most 64 rows (one workgroup holds all rows): a weight
     scale byte out of the window makes that workgroup's columns exact, bit

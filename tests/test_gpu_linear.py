@@ -455,6 +455,24 @@ def test_fast_k_split_64_row_tiles_out_of_window(gpu, w8):
     assert (np.abs(g - w) <= 1e-5 * row_scale).all()
 
 
+def test_fast_96_row_tiles_out_of_window(gpu):
+    """4512 x 960 x 960 MXFP4: 188 tiles of 96 rows (128-row tiles would
+    leave CUs idle, 64-row tiles take two rounds).  Rows 96..191 (the second
+    row tile) carry an out-of-window scale byte: that row tile recomputes
+    exactly, bit for bit; the rest stays within the fast-mode tolerance."""
+    rng = np.random.default_rng(67)
+    m, n, k = 4512, 960, 960
+    kb, a, planes, modes = make_layer(rng, m, n, k, False)
+    a = a.copy()
+    a.reshape(-1, kb, 144)[24:48, 5, 128] = 60   # rows 96..191
+    got, _ = run_linear(gpu, m, n, kb, a, planes, modes, mode=hb.FAST)
+    want, _ = helpers.oracle_linear_mt(m, n, kb, a, planes, modes)
+    assert_bits(got[96:192], want[96:192])
+    g, w = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
+    row_scale = np.abs(w).max(axis=1, keepdims=True)
+    assert (np.abs(g - w) <= 1e-5 * row_scale).all()
+
+
 @pytest.mark.parametrize("w8", [False, True])
 def test_fast_skinny_out_of_window_and_onto(gpu, w8):
     """A layer of at most 64 rows (one workgroup holds all rows): a weight

@@ -999,10 +999,10 @@ def bench_lines(hb, torch, ctx):
                           wl(128, n, kb, False, 256, F, panels=True)),
         "headline_exact": ("MXFP4 M=128 K=2560 N=960 x256 layers, exact, DDR words",
                            wl(128, n, kb, False, 256, E)),
-        "sweep_m1": ("MXFP4 M=1 K=2560 N=960 x256 layers, fast, DDR words",
-                     wl(1, n, kb, False, 256, F, seed=3)),
-        "sweep_m16": ("MXFP4 M=16 K=2560 N=960 x256 layers, fast, DDR words",
-                      wl(16, n, kb, False, 256, F, seed=3)),
+        "sweep_m1": ("MXFP4 M=1 K=2560 N=960 x256 layers, fast, weights in panels",
+                     wl(1, n, kb, False, 256, F, seed=3, panels=True)),
+        "sweep_m16": ("MXFP4 M=16 K=2560 N=960 x256 layers, fast, weights in panels",
+                      wl(16, n, kb, False, 256, F, seed=3, panels=True)),
         "sweep_m1024": ("MXFP4 M=1024 K=2560 N=960 x64 layers, fast, weights in panels",
                         wl(1024, n, kb, False, 64, F, seed=3, panels=True)),
         "w8_fast": ("W8 M=64 K=960 N=2560 + MULP + ADDP x128 layers, fast",
@@ -1307,9 +1307,8 @@ def main():
         del w2
         # M sweep (fast MXFP4), enough layers per step to exceed the caches
         sweep = {}
-        # (M=1 and 16 read DDR words: the skinny kernel's per-lane loads
-        # of a batch of layers do better over them than over panels)
-        for m, L, pan in ((1, 256, False), (16, 256, False), (1024, 64, True)):
+        # (weights in panels, packed once, untimed, as for the headline)
+        for m, L, pan in ((1, 256, True), (16, 256, True), (1024, 64, True)):
             ws = Workload(hb, torch, ctx, m, n, kb, False, L, hb.FAST, seed=3, panels=pan)
             mss = time_steps(hb, torch, ctx, stream, ws, extra_steps, extra_warm, settle_s=0.2)
             ts, rs = summarize(ws, mss, "fp6_fp4", f"sweep_m{m}")

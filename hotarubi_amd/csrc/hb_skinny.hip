@@ -180,21 +180,24 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
   const uint32_t ashift = 8 * (r16 & 3), as_delta = 128 - (r16 & 3) * 32;
   const uint32_t cl = r16 & 7, wshift_ddr = 8 * (cl & 3), ws_delta = 128 + (cl & 4) - cl * 16;
   uint32_t a_off[kMT], w_off[kNT];
-  [[maybe_unused]] uint32_t ws_off[kPanels ? kNT : 1], wshift[kPanels ? kNT : 1];
 #pragma unroll
   for (int mi = 0; mi < kMT; ++mi) {
     const uint32_t quad = min((mi * 16 + r16) >> 2, g.quads - 1);
     a_off[mi] = quad * a_row + (r16 & 3) * 32;
   }
+  // Panels: the workgroup's 64 columns are one panel (col0 is a multiple of
+  // 64; columns past n are zero codes there), column nj * 16 + r16 of it,
+  // so column tile nj's offsets are column tile 0's plus constants: codes
+  // + 256 nj, scale dword + 32 (nj % 2), scale byte shift + 8 (nj / 2).
+  // Three registers per lane instead of three per column tile.
+  static_assert(!kPanels || kCols == (int)kPanelCols, "one panel per workgroup");
+  [[maybe_unused]] WLaneOff pw{};
+  if constexpr (kPanels) {
+    pw = WLane(g, col0 + r16, true);
+  } else {
 #pragma unroll
-  for (int nj = 0; nj < kNT; ++nj) {
-    const uint32_t grp = min((col0 + nj * 16 + r16) >> 3, g.groups - 1);
-    if constexpr (kPanels) {
-      const WLaneOff wo = WLane(g, grp * 8 + cl);
-      w_off[nj] = wo.codes;
-      ws_off[nj] = wo.scale;
-      wshift[nj] = wo.shift;
-    } else {
+    for (int nj = 0; nj < kNT; ++nj) {
+      const uint32_t grp = min((col0 + nj * 16 + r16) >> 3, g.groups - 1);
       w_off[nj] = grp * word_row + cl * 16;
     }
   }
@@ -226,14 +229,14 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
 #pragma unroll
       for (int pl = 0; pl < kWP; ++pl) {
         const uint8_t* wp = pl ? w1 : w0;
-        const uint8_t* wc = wp + wbc + w_off[nj];
+        const uint8_t* wc = wp + wbc + (kPanels ? pw.codes + 256u * nj : w_off[nj]);
         const u32x4 v = *reinterpret_cast<const u32x4*>(wc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) rw.w[nj][pl][i] = v[i];
         // (DDR words: the scale as an offset from the codes' address, so no
         // per-tile sum stays live across the K loop)
         rw.sw[nj][pl] = *reinterpret_cast<const uint32_t*>(
-            kPanels ? wp + wbs + ws_off[kPanels ? nj : 0] : wc + ws_delta);
+            kPanels ? wp + wbs + pw.scale + 32u * (nj % 2) : wc + ws_delta);
       }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -250,7 +253,7 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
     uint32_t sb[kNT];
 #pragma unroll
     for (int nj = 0; nj < kNT; ++nj) {
-      const uint32_t sh = kPanels ? wshift[kPanels ? nj : 0] : wshift_ddr;
+      const uint32_t sh = kPanels ? pw.shift + 8u * (nj / 2) : wshift_ddr;
       const uint32_t ewh = __builtin_amdgcn_ubfe(rw.sw[nj][0], sh, 8);
       unsafe |= ewh - kSafeLo > kSafeHi - kSafeLo;
       if constexpr (kW8) {

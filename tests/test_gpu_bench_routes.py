@@ -6,7 +6,8 @@ tools/iss/lane.cpp):
   * batched MXFP4 M=128 K=2560 N=960 (the headline): one tile per workgroup
     (2 layers) and the persistent multi-tile route (80 layers, 320 tiles);
   * batched M=1024 (10 layers, 320 tiles);
-  * batched M=1 and M=16 (the skinny route with a layer index per workgroup);
+  * batched M=1 and M=16 (the skinny route with a layer index per workgroup),
+    over DDR words and over weight panels (the bench's layout);
   * the SparseDrive-S stage-1 im2col shape K=576 N=64 at 16,384 rows (128
     row tiles: the streaming route, not the small-layer split), both modes;
   * the SigLIP-style W8 MLP, up 768->3072 with MULP, ADDP, GELU and the
@@ -126,9 +127,10 @@ def test_headline_batched_m1024(gpu):
     batched_layers(gpu, 1024, 960, 80, 10, (0, 9), hb.FAST, seed=1024)
 
 
+@pytest.mark.parametrize("panels", [False, True])
 @pytest.mark.parametrize("m", [1, 16])
-def test_skinny_batched(gpu, m):
-    batched_layers(gpu, m, 960, 80, 6, range(6), hb.FAST, seed=m)
+def test_skinny_batched(gpu, m, panels):
+    batched_layers(gpu, m, 960, 80, 6, range(6), hb.FAST, seed=m, panels=panels)
 
 
 @pytest.mark.parametrize("mode", [hb.FAST, hb.EXACT])

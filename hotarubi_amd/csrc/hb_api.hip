@@ -936,11 +936,6 @@ int hb_linear_group_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) 
            hb::SplitEligible(g, 1) && g.n_planes == grp.g[0].n_planes &&
            (g.n_pieces > 1) == (grp.g[0].n_pieces > 1);
   }
-  if (!fuse) {  // one launch per layer, in order
-    for (uint32_t i = 0; i < count; ++i)
-      if (int rc = LinearBatched(ctx, &d[i], 1)) return rc;
-    return HB_OK;
-  }
   // Fused pairs: a later layer whose ACT_MUL reads an earlier one's C over
   // the same m x n folds beside it in its workgroups and reads its values
   // there.
@@ -948,7 +943,7 @@ int hb_linear_group_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) 
   uint32_t partner[hb::kMaxGroup], pair_op[hb::kMaxGroup];
   bool second[hb::kMaxGroup] = {};
   for (uint32_t i = 0; i < count; ++i) partner[i] = kNone;
-  for (uint32_t j = 1; j < count; ++j)
+  for (uint32_t j = 1; j < count && fuse; ++j)
     for (uint32_t o = 0; o < d[j].n_ops && !second[j]; ++o) {
       if (d[j].ops[o].op != HB_EP_ACT_MUL) continue;
       for (uint32_t i = 0; i < j; ++i)
@@ -960,6 +955,21 @@ int hb_linear_group_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) 
           break;
         }
     }
+  // Every ACT_MUL over an earlier layer's C must have become that layer's
+  // pair: a second consumer of one producer, or a consumer of a pair's
+  // second layer, would read C while the producer's workgroups still write
+  // it in the shared launch.  Such a group runs one layer at a time.
+  for (uint32_t j = 1; j < count && fuse; ++j)
+    for (uint32_t o = 0; o < d[j].n_ops && fuse; ++o) {
+      if (d[j].ops[o].op != HB_EP_ACT_MUL) continue;
+      for (uint32_t i = 0; i < j && fuse; ++i)
+        if (d[j].ops[o].x2 == d[i].c && !(partner[i] == j && pair_op[i] == o)) fuse = false;
+    }
+  if (!fuse) {  // one launch per layer, in order
+    for (uint32_t i = 0; i < count; ++i)
+      if (int rc = LinearBatched(ctx, &d[i], 1)) return rc;
+    return HB_OK;
+  }
   // Split plans: a lone layer's as its own launch would take (at most
   // kMaxSplitWaves splits), a pair's layers at most half that each (they
   // share a workgroup).  Where the grid would not fit the CUs in one round,

@@ -165,6 +165,26 @@ def test_group_falls_back_in_order(gpu, case):
     gate.check_oracle(x2_bits=grp[0][0])
 
 
+@pytest.mark.parametrize("case", ["two_consumers", "chain"])
+def test_group_unpaired_consumers_run_in_order(gpu, case):
+    """ACT_MUL dependencies a pair cannot hold: one producer read by two gates
+    (the second gate cannot be its pair too), and a chain up -> gate -> third
+    (the third reads the C of a pair's second layer).  The group runs one
+    launch per layer, in order, so every consumer reads its producer's
+    finished C: the results equal the one-by-one launches bit for bit."""
+    rng = np.random.default_rng(560)
+    up = Layer(rng, 50, 1024, 12)
+    gate = Layer(rng, 50, 1024, 12, act_mul=True, a=up.a, a_d=up.a_d)
+    third = Layer(rng, 50, 1024, 12, quantize=True, act_mul=True, a=up.a, a_d=up.a_d)
+    x2_of = {1: 0, 2: 0} if case == "two_consumers" else {1: 0, 2: 1}
+    say("group unpaired consumers", dict(case=case))
+    sep, grp = run_both(gpu, [up, gate, third], x2_of)
+    same(sep, grp)
+    up.check_oracle()
+    gate.check_oracle(x2_bits=grp[0][0])
+    third.check_oracle(x2_bits=grp[x2_of[2]][0])
+
+
 def test_group_rejections(gpu):
     rng = np.random.default_rng(550)
     ly = Layer(rng, 8, 64, 2)

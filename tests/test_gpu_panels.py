@@ -85,6 +85,130 @@ def test_single_layer_many_tiles(gpu):
     single_layer(gpu, 16384, 64, 18, False, hb.FAST, seed=504, bound=True, panels=True)
 
 
+# ---- the panel streaming kernel's persistent schedule: more tiles than CUs ----
+#
+# With more tiles than the grid's 256 workgroups every workgroup runs several
+# tiles in sequence from one load ring: the next tile's first steps are in
+# flight while the current tile's last steps compute, and its accumulators
+# are stored (or recomputed exactly) between them.  These launches use the
+# bench's shapes.  Layer i holds data set i % sets (sets coprime to the
+# schedule's strides), so every tile of the launch is checked: the oracle
+# computes each data set once, and every other layer holding the same data set
+# must equal that layer bit for bit (the kernel is deterministic per tile).
+
+def replicated_layers(gpu, m, n, kb, layers, sets, check, onto=False, bad=None, seed=0):
+    """`layers` MXFP4 layers over panels in one batched fast launch; layer i
+    holds data set i % sets.  `check`: the data sets the oracle computes (the
+    rest are compared bitwise with their representative only when checked).
+    bad = (layer, word, byte): that layer gets a data set of its own, equal to
+    its set's but with one weight scale byte set outside the fast window (its
+    tile is recomputed by the exact fold in the middle of the workgroup's
+    stream)."""
+    rng = np.random.default_rng(seed)
+    a_sets, w_sets, c_sets = [], [], []
+    for _ in range(sets):
+        a_sets.append(helpers.activations(rng, m, kb * 32)[1])
+        w_sets.append(mxfp4_w(rng, n, kb))
+        c_sets.append(helpers.random_fp32_words(rng, (m, n), 118, 128) if onto else None)
+    set_of = [i % sets for i in range(layers)]
+    w_bad = None
+    if bad is not None:
+        layer, word, byte = bad
+        w_bad = w_sets[set_of[layer]].copy()
+        w_bad.reshape(-1, 144)[word, 128 + byte] = 200
+    pb = hb.panel_bytes(n, kb)
+    a_d = torch.empty((layers,) + a_sets[0].shape, dtype=torch.uint8, device=DEV)
+    w_p = torch.empty((layers, pb), dtype=torch.uint8, device=DEV)
+    c_d = torch.zeros((layers, m, n), dtype=torch.float32, device=DEV)
+    w_dev = [dev(w) for w in w_sets]
+    wb_dev = dev(w_bad) if w_bad is not None else None
+    for i in range(layers):
+        a_d[i].copy_(dev(a_sets[set_of[i]]))
+        src = wb_dev if bad is not None and i == bad[0] else w_dev[set_of[i]]
+        hb.pack_weights(src, n, kb, w_p[i], ctx=gpu)
+        if onto:
+            c_d[i].copy_(dev(c_sets[set_of[i]].view(np.float32)))
+    descs = [hb.linear_desc(m, n, kb, a_d[i], [w_p[i]], [0], c_d[i], mode=hb.FAST, panels=True,
+                            onto=onto) for i in range(layers)]
+    torch.cuda.synchronize()
+    tiles = layers * ((m + 127) // 128) * ((n + 319) // 320)
+    say("stream schedule", dict(m=m, n=n, kb=kb, layers=layers, sets=sets, tiles=tiles,
+                                onto=onto, bad=bad))
+    hb.linear_batched(descs, gpu)
+    got = host(c_d).view(np.uint32)
+    rep = {}
+    for i in range(layers):
+        if bad is not None and i == bad[0]:
+            continue
+        s = set_of[i]
+        if s in rep:
+            assert np.array_equal(got[i], got[rep[s]]), (i, rep[s])
+        else:
+            rep[s] = i
+    for s in check:
+        want, _ = helpers.oracle_linear_mt(m, n, kb, a_sets[s], [w_sets[s]], [0], onto=c_sets[s])
+        helpers.check_fast(got[rep[s]], want,
+                           bound=None if onto else
+                           helpers.block_abs_sums(m, n, kb, a_sets[s], [w_sets[s]], [0]))
+    if bad is not None:
+        layer = bad[0]
+        s = set_of[layer]
+        want, _ = helpers.oracle_linear_mt(m, n, kb, a_sets[s], [w_bad], [0], onto=c_sets[s])
+        helpers.check_fast(got[layer], want)
+        # the tile holding the bad byte is recomputed bitwise; the layer's
+        # other tiles are the plain fast result
+        if not onto:
+            exact_cols = _tile_cols_of_word(n, kb, bad[1])
+            ex, _ = helpers.oracle_linear_mt(m, n, kb, a_sets[s], [w_bad], [0])
+            assert np.array_equal(got[layer][:, exact_cols], ex[:, exact_cols])
+            other = np.setdiff1d(np.arange(n), np.arange(n)[exact_cols])
+            assert np.array_equal(got[layer][:, other], got[rep[s]][:, other])
+    return got
+
+
+def mxfp4_w(rng, n, kb):
+    code, e = helpers.mxfp4_weights(rng, n, kb * 32)
+    return oracle.pack_wbuf(code, e)
+
+
+def _tile_cols_of_word(n, kb, word):
+    """The 320-column tile holding DDR weight word `word` (group word // kb)."""
+    c0 = (word // kb) * 8 // 320 * 320
+    return slice(c0, min(c0 + 320, n))
+
+
+def test_stream_headline_launch(gpu):
+    """The bench's launch: M=128 K=2560 N=960, 256 layers, 768 tiles (3 per
+    workgroup); 17 data sets, every layer checked."""
+    replicated_layers(gpu, 128, 960, 80, 256, 17, range(17), seed=600)
+
+
+def test_stream_m1024_launch(gpu):
+    """The M=1024 sweep's launch: 64 layers, 1,536 tiles (6 per workgroup)."""
+    replicated_layers(gpu, 1024, 960, 80, 64, 5, range(5), seed=601)
+
+
+def test_stream_many_tiles_onto(gpu):
+    """From C, 300 tiles: each tile's accumulators start from its C words
+    while the previous tile's last steps are still in the ring."""
+    replicated_layers(gpu, 128, 960, 80, 100, 7, range(7), onto=True, seed=602)
+
+
+def test_stream_many_tiles_exact_recompute_mid_stream(gpu):
+    """One weight scale byte outside the window in the middle column tile of
+    layer 150 of 256 (tile 451 of 768): that tile is recomputed by the exact
+    fold while the ring streams on, and the workgroup's next tile follows."""
+    kb = 80
+    word = 50 * kb + 40  # column group 50 (column tile 1), block 40
+    replicated_layers(gpu, 128, 960, kb, 256, 13, range(3), bad=(150, word, 3), seed=603)
+
+
+def test_stream_many_tiles_partial_panel(gpu):
+    """N=200 (a partial last panel, three of a tile's five panels past the
+    layer) at M=1024 over 40 layers: 320 tiles."""
+    replicated_layers(gpu, 1024, 200, 5, 40, 3, range(3), seed=604)
+
+
 # ---- the other kernels over panels ----
 
 @pytest.mark.parametrize("m", [1, 16])

@@ -243,9 +243,12 @@ class Chain:
     with E8M0 exponents in [lo, hi]; W8 weights are two nibble planes of
     random codes sharing the scale byte 133 (MXINT8 of int8 values)."""
 
-    def __init__(self, hb, torch, m, mode, seed, w8_panels=False):
+    def __init__(self, hb, torch, m, mode, seed, w8_panels=False, panels=False):
         self.hb, self.torch, self.m, self.mode = hb, torch, m, mode
         self.w8_panels = w8_panels  # W8 layers over W8 panels (packed once, here)
+        # every weight plane (MXFP4, or each W8 nibble plane) in weight panels
+        # (hb_pack_weights, once, here), the layout fast-mode kernels stream
+        self.panels = panels
         self.dev = "cuda:0"
         self.g = torch.Generator(device=self.dev).manual_seed(seed)
         self.quads = (m + 3) // 4
@@ -291,26 +294,44 @@ class Chain:
         self.keep.append(tb)
         return tb
 
-    def add(self, n, kb, a, planes, c, ops=(), q=None, onto=False, tbuf=None):
+    def add(self, n, kb, a, planes, c, ops=(), q=None, onto=False, tbuf=None, c_out=True):
+        """c_out=False: the model keeps only the requantized words q; the
+        fp32 C this build writes as well is not counted in the algorithmic
+        bytes (the NPU leaves it in its on-chip FBUF)."""
         modes = [1, 2] if len(planes) == 2 else [0]
         w8p = self.w8_panels and len(planes) == 2
+        pan_flag = False
+        if w8p or self.panels:
+            # the packers run on the default context's own stream: the weight
+            # words drawn on torch's stream must be complete first
+            self.torch.cuda.synchronize()
         if w8p:
             pan = self.torch.empty((self.hb.w8_panel_bytes(n, kb),), dtype=self.torch.uint8,
                                    device=self.dev)
             self.hb.pack_w8(planes[0], planes[1], n, kb, pan)
             self.keep.append(pan)
             planes = [pan, pan]
+        elif self.panels:
+            packed = []
+            for p in planes:
+                pan = self.torch.empty((self.hb.panel_bytes(n, kb),), dtype=self.torch.uint8,
+                                       device=self.dev)
+                self.hb.pack_weights(p, n, kb, pan)
+                self.keep.append(pan)
+                packed.append(pan)
+            planes, pan_flag = packed, True
         self.descs.append(self.hb.linear_desc(self.m, n, kb, a, planes, modes, c, ops=ops,
                                               tbuf=tbuf, q_out=q, onto=onto, mode=self.mode,
-                                              w8_panels=w8p))
+                                              w8_panels=w8p, panels=pan_flag))
         self.plan.append([len(self.descs) - 1])
         self.ops += 2.0 * self.m * n * kb * 32
         vectors = sum(1 for k, _ in ops if k in (self.hb.EP_ADDP, self.hb.EP_MULP))
-        # C (fp32) is written whether or not the layer requantizes; the
-        # MXINT8 words (codes and scale bytes) come on top, and every [m][n]
-        # operand (ADD, ACT_MUL) and an `onto` C are read in full
+        # C (fp32) counts where the model stores it; the MXINT8 words (codes
+        # and scale bytes) come on top, and every [m][n] operand (ADD,
+        # ACT_MUL) and an `onto` C are read in full
         matrices = sum(1 for k, _ in ops if k in (self.hb.EP_ADD, self.hb.EP_ACT_MUL))
-        self.bytes += layer_bytes(self.m, n, kb, 8 if len(planes) == 2 else 4, vectors) + \
+        self.bytes += layer_bytes(self.m, n, kb, 8 if len(planes) == 2 else 4, vectors) - \
+            (0 if c_out or q is None else 4 * self.m * n) + \
             (self.m * n * (1 + 1 / 32) if q is not None else 0) + \
             4 * self.m * n * (matrices + (1 if onto else 0))
 
@@ -351,8 +372,8 @@ class ExpertStep(Chain):
 
     WIDTH, KB, Q, KV, HID, KBQ, KBH, LAYERS, CHUNK, ACT = 720, 23, 960, 320, 2048, 30, 64, 16, 50, 32
 
-    def __init__(self, hb, torch, batch, mode):
-        super().__init__(hb, torch, self.CHUNK * batch, mode, 11 + batch)
+    def __init__(self, hb, torch, batch, mode, panels=False):
+        super().__init__(hb, torch, self.CHUNK * batch, mode, 11 + batch, panels=panels)
         tb = self.table("silu")
         x = [self.f32(self.WIDTH) for _ in range(3)]
         for layer in range(self.LAYERS):
@@ -401,8 +422,8 @@ class PrefixStep(Chain):
 
     HIDDEN, KB, KV, INTER, KBI, LAYERS, TOKENS = 960, 30, 320, 2560, 80, 16, 141
 
-    def __init__(self, hb, torch, batch, mode):
-        super().__init__(hb, torch, self.TOKENS * batch, mode, 23 + batch)
+    def __init__(self, hb, torch, batch, mode, panels=False):
+        super().__init__(hb, torch, self.TOKENS * batch, mode, 23 + batch, panels=panels)
         tb = self.table("silu")
         x = [self.f32(self.HIDDEN) for _ in range(3)]
         for _ in range(self.LAYERS):
@@ -750,8 +771,8 @@ class SparseDriveHead(Chain):
 
     ROWS, TEMP, D, DQ, FF, BLOCKS = 928, 608, 256, 512, 1024, 6
 
-    def __init__(self, hb, torch, frames, mode):
-        super().__init__(hb, torch, self.ROWS * frames, mode, 51 + frames)
+    def __init__(self, hb, torch, frames, mode, panels=False):
+        super().__init__(hb, torch, self.ROWS * frames, mode, 51 + frames, panels=panels)
         kd, kq, kf = self.D // 32, self.DQ // 32, self.FF // 32
         rows = self.m
         for blk in range(self.BLOCKS):
@@ -759,7 +780,7 @@ class SparseDriveHead(Chain):
                 x = self.a_words(kq)
                 for part in range(3):  # q over the anchors, k and v over the keys
                     keys = self.TEMP * frames if (temporal and part) else rows
-                    sub = Chain(hb, torch, keys, mode, 61 + part)
+                    sub = Chain(hb, torch, keys, mode, 61 + part, panels=panels)
                     sub.keep, sub.descs, sub.plan = self.keep, self.descs, self.plan
                     sub.add(self.DQ, kq, sub.a_words(kq) if keys != rows else x,
                             sub.w8(self.DQ, kq), sub.f32(self.DQ),
@@ -789,10 +810,105 @@ class SparseDriveConv(Chain):
 
     M, K, N = 6 * 64 * 176, 576, 64
 
-    def __init__(self, hb, torch, mode):
-        super().__init__(hb, torch, self.M, mode, 31)
+    def __init__(self, hb, torch, mode, panels=False):
+        super().__init__(hb, torch, self.M, mode, 31, panels=panels)
         kb = self.K // 32
         self.add(self.N, kb, self.a_words(kb), [self.w_words(self.N, kb)], self.f32(self.N))
+        torch.cuda.synchronize()
+
+
+class SparseDriveBackbone(Chain):
+    """SparseDrive-S image backbone (ResNet-50) as the GEMM chain the
+    reference compiler emits for it (tools/compiler/sparsedrive_encoder.cpp:
+    stem 571-640, bottlenecks 817-874, EmitConv 187-475), over 6 cameras at
+    256 x 704 input per frame:
+
+      stem: 7x7 stride-2 conv as a W8 GEMM, 128 x 352 positions per camera,
+            K = 192, N = 64, + bias + ReLU, fp32 out (the max-pool reads it);
+      4 stages of {3, 4, 6, 3} bottleneck blocks, mid width {64, 128, 256,
+      512}, output 4 x mid, positions {64 x 176, 32 x 88, 16 x 44, 8 x 22}
+      per camera; per block:
+        conv1  1x1, K = cin (block 0) or 4 x mid, N = mid, + bias, ReLU,
+               MXINT8 out only (over the input positions in block 0);
+        conv2  3x3 im2col, K = 9 x mid, N = mid, stride 2 in block 0 of
+               stages 2-4, + bias, ReLU, MXINT8 out only;
+        conv3  1x1, K = mid, N = 4 x mid, + bias, ReLU, fp32 and MXINT8
+               out; block 0 also folds the downsample 1x1 (strided) over
+               the block's input as a second K range (bias = the two
+               biases' sum), later blocks start from the residual (the
+               previous block's fp32 output, updated in place).
+
+    MXFP4 weights (E8M0 exponents -10..-2) and the W8 stem; 1x1 convs read
+    the previous layer's MXINT8 words, 3x3 convs and the concatenated
+    downsample operand read synthetic im2col words of their shape (the
+    gather is the DMA engine's, not a GEMM).  The fp32 C of conv1 and conv2
+    goes to one scratch tensor and is not counted in the bytes."""
+
+    CAMS, STEM_H, STEM_W = 6, 128, 352
+    STAGES = ((3, 64, 1), (4, 128, 2), (6, 256, 2), (3, 512, 2))
+
+    def __init__(self, hb, torch, frames, mode, panels=True):
+        rows0 = frames * self.CAMS * self.STEM_H * self.STEM_W
+        super().__init__(hb, torch, rows0, mode, 71 + frames, panels=panels)
+        self.frames = frames
+        relu = (hb.EP_RELU, None)
+
+        def rows(r):
+            self.m, self.quads = r, (r + 3) // 4
+
+        def bias(n):
+            return (hb.EP_ADDP, self.vec(n, 0.1))
+
+        # stem (W8), fp32 out
+        self.add(64, 6, self.a_words(6), self.w8(64, 6), self.f32(64), ops=[bias(64), relu])
+        r = frames * self.CAMS * (self.STEM_H // 2) * (self.STEM_W // 2)
+        rows(r)
+        x8 = self.a_words(2)  # the max-pool's MXINT8 output, 64 channels
+        cin = 64
+        scratch_elems = 0
+        plan = []
+        rin = r
+        for blocks, mid, stride in self.STAGES:
+            rout = rin // (stride * stride)
+            for j in range(blocks):
+                r1 = rin if j == 0 else rout
+                scratch_elems = max(scratch_elems, r1 * mid, rout * mid)
+            plan.append((blocks, mid, stride, rin, rout))
+            rin = rout
+        self.scratch = torch.empty((scratch_elems,), dtype=torch.float32, device=self.dev)
+        self.keep.append(self.scratch)
+        for blocks, mid, stride, rin, rout in plan:
+            cout = 4 * mid
+            y32 = None
+            for j in range(blocks):
+                r1 = rin if j == 0 else rout
+                k1 = cin if j == 0 else cout
+                # conv1 over the block's input positions
+                rows(r1)
+                t1 = self.a_words(mid // 32)
+                self.add(mid, k1 // 32, x8, [self.w_words(mid, k1 // 32)],
+                         self.scratch[:r1 * mid].view(r1, mid), ops=[bias(mid), relu], q=t1,
+                         c_out=False)
+                # conv2: 3x3 im2col at the output positions
+                rows(rout)
+                t2 = self.a_words(mid // 32)
+                kb2 = 9 * mid // 32
+                self.add(mid, kb2, self.a_words(kb2), [self.w_words(mid, kb2)],
+                         self.scratch[:rout * mid].view(rout, mid), ops=[bias(mid), relu],
+                         q=t2, c_out=False)
+                # conv3 (+ downsample in block 0, + residual after)
+                y8 = self.a_words(cout // 32)
+                if j == 0:
+                    kb3 = (mid + cin) // 32
+                    y32 = self.f32(cout)
+                    self.add(cout, kb3, self.a_words(kb3), [self.w_words(cout, kb3)], y32,
+                             ops=[bias(cout), relu], q=y8)
+                else:
+                    self.add(cout, mid // 32, t2, [self.w_words(cout, mid // 32)], y32,
+                             ops=[bias(cout), relu], q=y8, onto=True)
+                x8 = y8
+            cin = cout
+        self.m = rows0
         torch.cuda.synchronize()
 
 
@@ -1023,6 +1139,12 @@ def bench_lines(hb, torch, ctx):
         "sparsedrive_head_f16": ("SparseDrive-S det head GEMMs, 6 blocks, 16 frames (14848 "
                                  "anchor rows), W8 attention + MXFP4 FFN, fast",
                                  lambda: ChainLine(SparseDriveHead(hb, torch, 16, F))),
+        "backbone_f1": ("SparseDrive-S ResNet-50 backbone GEMM chain (stem + 16 bottlenecks, "
+                        "49 GEMMs), 6 cameras, 1 frame, fast, weights in panels",
+                        lambda: ChainLine(SparseDriveBackbone(hb, torch, 1, F))),
+        "backbone_f16": ("SparseDrive-S ResNet-50 backbone GEMM chain (stem + 16 bottlenecks, "
+                         "49 GEMMs), 6 cameras, 16 frames, fast, weights in panels",
+                         lambda: ChainLine(SparseDriveBackbone(hb, torch, 16, F))),
         "expert_b1": ("SmolVLA action-expert step GEMM chain, B=1 (M=50), fast, grouped",
                       lambda: ChainLine(ExpertStep(hb, torch, 1, F))),
         "expert_b32": ("SmolVLA action-expert step GEMM chain, B=32 (M=1600), fast, grouped",
@@ -1396,6 +1518,26 @@ def main():
                                                   "roofline": roof}
                 del wk
         out["sparsedrive_head"] = head
+        # SparseDrive-S backbone: every bottleneck's GEMMs and the stem
+        bb = {"workload": "SparseDrive-S ResNet-50 backbone GEMM chain over 6 cameras at "
+                          "256x704: stem 7x7/2 (W8, K=192, N=64, bias + ReLU), 16 bottlenecks "
+                          "(stages of 3/4/6/3, mid 64/128/256/512): conv1 1x1 and conv2 3x3 "
+                          "im2col (MXFP4, bias + ReLU + requantize), conv3 1x1 (MXFP4, bias + "
+                          "ReLU, fp32 + requantize; downsample folded as a second K range in "
+                          "block 0, residual start after), 49 GEMMs per frame"}
+        for frames, modes in ((1, (("fast", hb.FAST, "fp6_fp4"), ("exact", hb.EXACT, "bf16"))),
+                              (16, (("fast", hb.FAST, "fp6_fp4"),))):
+            for name, md, cls in modes:
+                wk = SparseDriveBackbone(hb, torch, frames, md, panels=md == hb.FAST)
+                t = time_chain(torch, ctx, wk, steps=5 if frames == 1 else 3, graph=False)
+                tops, roof = chain_summary(wk, t["eager_ms"], cls,
+                                           f"backbone_f{frames}" if md == hb.FAST else None)
+                bb.setdefault(f"frames={frames}", {})[name] = {
+                    "value": tops, "unit": "TOPS", "ms_per_pass": t["eager_ms"],
+                    "gemms": t["gemms"], "rows_stage1": frames * 6 * 64 * 176,
+                    "weights": "panels" if md == hb.FAST else "DDR words", "roofline": roof}
+                del wk
+        out["sparsedrive_backbone"] = bb
         ctx.set_stream(stream.cuda_stream)
 
     if not args.quick and args.only in (None, "smolvla"):

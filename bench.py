@@ -43,7 +43,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 # Dense MFMA peaks (TFLOP/s or TOPS) of the instruction class each kernel uses.
-MFMA_PEAK = {"bf16": 2500.0, "fp6_fp4": 10100.0, "int8": 5000.0}
+MFMA_PEAK = {"bf16": 2500.0, "fp6_fp4": 10100.0, "int8": 5000.0, "fp8": 5000.0}
 METRIC = "quantized GEMM TOPS & % MFMA/HBM roofline (W8, MXFP4); SmolVLA step ms"
 PROFILES = os.path.join(ROOT, "profiles")
 
@@ -1121,6 +1121,14 @@ def bench_lines(hb, torch, ctx):
                       wl(16, n, kb, False, 256, F, seed=3, panels=True)),
         "sweep_m1024": ("MXFP4 M=1024 K=2560 N=960 x64 layers, fast, weights in panels",
                         wl(1024, n, kb, False, 64, F, seed=3, panels=True)),
+        "fp8_m1": ("MXFP8 x MXFP4 M=1 K=2560 N=960 x256 layers, fast, weights in panels",
+                   wl(1, n, kb, False, 256, F, seed=5, panels=True, a_fp8=True)),
+        "fp8_m16": ("MXFP8 x MXFP4 M=16 K=2560 N=960 x256 layers, fast, weights in panels",
+                    wl(16, n, kb, False, 256, F, seed=5, panels=True, a_fp8=True)),
+        "fp8_m128": ("MXFP8 x MXFP4 M=128 K=2560 N=960 x256 layers, fast, weights in panels",
+                     wl(128, n, kb, False, 256, F, seed=5, panels=True, a_fp8=True)),
+        "fp8_m1024": ("MXFP8 x MXFP4 M=1024 K=2560 N=960 x64 layers, fast, weights in panels",
+                      wl(1024, n, kb, False, 64, F, seed=5, panels=True, a_fp8=True)),
         "w8_fast": ("W8 M=64 K=960 N=2560 + MULP + ADDP x128 layers, fast",
                     wl(64, 2560, 30, True, 128, F, epilogue=True, seed=4)),
         "w8_exact": ("W8 M=64 K=960 N=2560 + MULP + ADDP x128 layers, exact",
@@ -1457,6 +1465,19 @@ def main():
             fp8[f"M={m}"] = {"ms": ms_l, "tops": round(2.0 * m * n * kb * 32 / (ms_l * 1e-3) / 1e12, 3),
                              "hbm_frac": round(nbytes / (ms_l * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         out["mxfp8_single_layer"] = fp8
+        # config 1's sweep with MXFP8 activations, batched as the MXINT8 sweep
+        sweep8 = {"workload": f"MXFP8 E4M3 x MXFP4 linear K={kb * 32} N={n}, activations "
+                              "hb_encode_mxfp8 of N(0,1), weights in panels, fast mode (two "
+                              "exponent planes per block on the FP8 x FP4 matrix cores)"}
+        for m, L in ((1, 256), (16, 256), (128, 256), (1024, 64)):
+            ws = Workload(hb, torch, ctx, m, n, kb, False, L, hb.FAST, seed=5, panels=True,
+                          a_fp8=True)
+            mss = time_steps(hb, torch, ctx, stream, ws, extra_steps, extra_warm, settle_s=0.2)
+            ts, rs = summarize(ws, mss, "fp8", f"fp8_m{m}")
+            sweep8[f"M={m}"] = {"value": round(ts, 3), "unit": "TOPS", "layers": L,
+                                "ms_per_step": round(mss, 4), "roofline": rs}
+            del ws
+        out["mxfp8_fast_m_sweep"] = sweep8
         # W8 layer with per-channel scale and bias, fast and exact
         L8 = 128
         w8 = {"workload": f"W8 linear M=64 K=960 N=2560 + MULP + ADDP, {L8} layers per step"}

@@ -722,6 +722,11 @@ hipError_t LaunchFp8Linear(const GemmArgs& in, uint32_t batch, bool fast, hipStr
     args.fast_ep = 1u;
     return LaunchSplitLinear(args, stream);
   }
+  // batches and larger plain layers over weight panels: the streaming kernel
+  if (fast && StreamEligible(args)) {
+    args.fast_ep = 1u;
+    return LaunchStream(args, batch, stream);
+  }
   args.fast_ep = 0u;
   for (uint32_t z = 0; z < batch; ++z) {
     GemmArgs one = args;

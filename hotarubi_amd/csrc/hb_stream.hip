@@ -32,6 +32,14 @@
 // hand (the loads are issued from inline asm, which the compiler's own
 // waits do not see).  Loads past the last step repeat a valid address, so
 // every wave issues the same number of loads every step.
+//
+// MXFP8 activations (kA8, HB_LINEAR_A_FP8): the same ring and loads; the
+// code bytes are the MFMA's FP8 A operand with scale byte ea.  8-bit A
+// operands take K in 16-wide halves per lane (registers 0-3 of lane half h
+// are K [16 h, 16 h + 16) of the step's first block, registers 4-7 the same
+// of its second, each 32-wide K range scaled by its lane half's byte), so a
+// lane reads bytes [16 h, 16 h + 16) of its row in both blocks.  Each step's
+// codes go through two MFMAs per n-tile, split by exponent (fp8::Split).
 #include <utility>
 
 #include "hb_device.h"
@@ -97,6 +105,9 @@ __device__ __forceinline__ Schedule TilesOf(uint32_t total) {
 // bytes (ea - 1 | (ea - 5) << 8) and abad, the lane's A scale byte left the
 // window; and the raw A codes and scale dword of a later step of the same
 // parity, loaded ahead of their conversion.
+// For MXFP8 (kA8) the converted A is the step's 8 code dwords with blocks
+// past the layer zeroed (h holds dwords 0-5, r dwords 6-7), split into the
+// exponent planes as the MFMAs issue.
 struct Ops {
   u32x4 b[kNT];
   uint32_t sw[kTP];
@@ -107,6 +118,7 @@ struct Ops {
   uint32_t sd;
 };
 
+template <bool kA8>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void StreamKernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_ring[kD * kSlot];
@@ -229,18 +241,32 @@ void StreamKernel(GemmArgs g) {
   };
   auto read_a = [&](Ops& o, uint32_t slot) __attribute__((always_inline)) {
     const uint8_t* abuf = lds_ring + slot * kSlot;
-    o.x0 = *reinterpret_cast<const u32x4*>(abuf + (h * kBM + r) * 32);
-    o.x1 = *reinterpret_cast<const u32x4*>(abuf + (h * kBM + r) * 32 + 16);
+    if constexpr (kA8) {  // bytes [16 h, 16 h + 16) of the row in both blocks
+      o.x0 = *reinterpret_cast<const u32x4*>(abuf + r * 32 + 16 * h);
+      o.x1 = *reinterpret_cast<const u32x4*>(abuf + (kBM + r) * 32 + 16 * h);
+    } else {
+      o.x0 = *reinterpret_cast<const u32x4*>(abuf + (h * kBM + r) * 32);
+      o.x1 = *reinterpret_cast<const u32x4*>(abuf + (h * kBM + r) * 32 + 16);
+    }
     o.sd = *reinterpret_cast<const uint32_t*>(abuf + kACodes + (h * (kBM / 4) + r / 4) * 16);
   };
   // Convert the raw A held in o, of step (k, s).
   auto convert = [&](Ops& o, uint32_t k, uint32_t s) __attribute__((always_inline)) {
     const bool live = k < sc.count && 2 * s < nbh;
+    const uint32_t ea = __builtin_amdgcn_ubfe(o.sd, 8 * (r & 3), 8);
+    o.abad = live && ea - kSafeLo > kSafeHi - kSafeLo ? 1u : 0u;
+    if constexpr (kA8) {  // blocks 2 s (dwords 0-3) and 2 s + 1 (4-7) where they exist
+      const uint32_t keep0 = k < sc.count && 2 * s < nblocks ? ~0u : 0u;
+      const uint32_t keep1 = k < sc.count && 2 * s + 1 < nblocks ? ~0u : 0u;
+      o.h = u32x6{o.x0[0] & keep0, o.x0[1] & keep0, o.x0[2] & keep0, o.x0[3] & keep0,
+                  o.x1[0] & keep1, o.x1[1] & keep1};
+      o.r = u32x6{o.x1[2] & keep1, o.x1[3] & keep1, 0u, 0u, 0u, 0u};
+      o.sa = (int)ea;
+      return;
+    }
     const uint32_t x[8] = {o.x0[0], o.x0[1], o.x0[2], o.x0[3], o.x1[0], o.x1[1], o.x1[2], o.x1[3]};
     SplitA(x, live ? 0xFFFFFFFFu : 0u, o.h, o.r);
-    const uint32_t ea = __builtin_amdgcn_ubfe(o.sd, 8 * (r & 3), 8);
     o.sa = (int)(((ea - 5u) << 8) | ((ea - 1u) & 0xFFu));
-    o.abad = live && ea - kSafeLo > kSafeHi - kSafeLo ? 1u : 0u;
   };
 
   float* const xp = lds_xpose[w];
@@ -290,7 +316,8 @@ void StreamKernel(GemmArgs g) {
           const uint32_t col = tl.col0 + j * 32 + (lane & 31);
           if (row >= g.m || col >= g.n) continue;
           uint32_t* out = c + (size_t)row * g.n + col;
-          *out = SlowLinear(g, a, w0, w0, g.acc ? *out : 0u, row, col);
+          *out = kA8 ? SlowLinearFp8(g, a, w0, g.acc ? *out : 0u, row, col)
+                     : SlowLinear(g, a, w0, w0, g.acc ? *out : 0u, row, col);
         }
       return;
     }
@@ -369,10 +396,26 @@ void StreamKernel(GemmArgs g) {
             (uint32_t)(((sq >> 8) & 0xFFu) - kSafeLo > kSafeHi - kSafeLo);
     }
     bad |= wb;
-    const i32x8 ah = {(int)use.h[0], (int)use.h[1], (int)use.h[2], (int)use.h[3],
-                      (int)use.h[4], (int)use.h[5], 0, 0};
-    const i32x8 ar = {(int)use.r[0], (int)use.r[1], (int)use.r[2], (int)use.r[3],
-                      (int)use.r[4], (int)use.r[5], 0, 0};
+    i32x8 ah, ar;
+    if constexpr (kA8) {  // the exponent planes: ah (exponents 0..7), then ar (8..15)
+      const uint32_t x[8] = {use.h[0], use.h[1], use.h[2], use.h[3],
+                             use.h[4], use.h[5], use.r[0], use.r[1]};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint32_t lo, hi;
+        fp8::Split(x[i], lo, hi);
+        ah[i] = (int)lo;
+        ar[i] = (int)hi;
+      }
+    } else {
+      ah = i32x8{(int)use.h[0], (int)use.h[1], (int)use.h[2], (int)use.h[3],
+                 (int)use.h[4], (int)use.h[5], 0, 0};
+      ar = i32x8{(int)use.r[0], (int)use.r[1], (int)use.r[2], (int)use.r[3],
+                 (int)use.r[4], (int)use.r[5], 0, 0};
+    }
+    // A's format (cbsz): FP6 E2M3 planes, or FP8 E4M3; its op_sel picks the
+    // plane's scale byte in sa (FP6), or the one byte ea (FP8)
+    constexpr int kAFmt = kA8 ? 0 : 2, kSelR = kA8 ? 0 : 1;
     // plane h over the n-tiles, then plane r (branch-free: n-tiles past the
     // layer compute outputs that are not stored)
     Unroll<kNT>([&](auto t_c) {
@@ -380,14 +423,16 @@ void StreamKernel(GemmArgs g) {
       const i32x8 bt = {(int)use.b[kT][0], (int)use.b[kT][1], (int)use.b[kT][2],
                         (int)use.b[kT][3], 0, 0, 0, 0};
       acc[kT] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          ah, bt, acc[kT], 2, 4, 0, use.sa, kT % 2, (int)(use.sw[kT / 2] >> (16 * (lane & 1))));
+          ah, bt, acc[kT], kAFmt, 4, 0, use.sa, kT % 2,
+          (int)(use.sw[kT / 2] >> (16 * (lane & 1))));
     });
     Unroll<kNT>([&](auto t_c) {
       constexpr int kT = decltype(t_c)::value;
       const i32x8 bt = {(int)use.b[kT][0], (int)use.b[kT][1], (int)use.b[kT][2],
                         (int)use.b[kT][3], 0, 0, 0, 0};
       acc[kT] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          ar, bt, acc[kT], 2, 4, 1, use.sa, kT % 2, (int)(use.sw[kT / 2] >> (16 * (lane & 1))));
+          ar, bt, acc[kT], kAFmt, 4, kSelR, use.sa, kT % 2,
+          (int)(use.sw[kT / 2] >> (16 * (lane & 1))));
     });
     // the step's MFMAs and the conversion are issued here, before the next
     // barrier, so they overlap the next step's loads and LDS reads
@@ -423,9 +468,12 @@ bool StreamEligible(const GemmArgs& args) {
   const bool aligned = reinterpret_cast<uintptr_t>(args.c) % 16 == 0 && args.c_batch % 4 == 0 &&
                        reinterpret_cast<uintptr_t>(args.a) % 16 == 0 && args.a_batch % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(args.w[0]) % 16 == 0 && args.w_batch % 16 == 0;
+  // MXINT8 layers of up to 64 rows have the skinny and split kernels;
+  // MXFP8 layers of any row count stream here
   return args.w_panels && args.n_planes == 1 && args.modes[0] == kModeFp4 && aligned &&
          args.n_ops == 0 && args.q_out == nullptr && args.n_pieces == 1 &&
-         args.piece_off[0] == 0 && args.piece_kb[0] == args.kb_total && args.quads * 4 > 64;
+         args.piece_off[0] == 0 && args.piece_kb[0] == args.kb_total &&
+         (args.a_fp8 || args.quads * 4 > 64);
 }
 
 hipError_t LaunchStream(const GemmArgs& in, uint32_t batch, hipStream_t stream) {
@@ -447,7 +495,8 @@ hipError_t LaunchStream(const GemmArgs& in, uint32_t batch, hipStream_t stream) 
   args.gz = batch;
   const uint32_t tiles = args.gx * args.gy * args.gz;
   const dim3 grid(tiles < (uint32_t)cus[dev] ? tiles : (uint32_t)cus[dev]), block(256);
-  hipLaunchKernelGGL(StreamKernel, grid, block, 0, stream, args);
+  if (args.a_fp8) hipLaunchKernelGGL(StreamKernel<true>, grid, block, 0, stream, args);
+  else hipLaunchKernelGGL(StreamKernel<false>, grid, block, 0, stream, args);
   return hipGetLastError();
 }
 

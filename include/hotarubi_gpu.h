@@ -265,9 +265,13 @@ typedef struct hb_linear_desc {
    * scale bytes E8M0; one MXFP4 plane (modes {0}), DDR words or panels.
    * Exact: each block's exact sum of products, S * 2^-9 * 2^-1 in integer
    * units, is rounded once to FP32 (RNE, below normal -> +0) and the blocks
-   * fold as above.  Fast: one layer of up to 1,024 rows on FP8 x FP4
-   * matrix cores, within the fast-mode bound; other fast layers (batches,
-   * more rows) fold exactly per output. */
+   * fold as above.  Fast, within the fast-mode bound above (each block's
+   * codes go to the FP8 x FP4 matrix cores as two planes split by
+   * exponent, so every instruction sums its products without loss): one
+   * layer of up to 1,024 rows (ops, requantize, pieces, DDR words or
+   * panels); batches and larger layers that are plain (no ops, no
+   * requantize, one piece) with the weights in panels.  Other fast MXFP8
+   * layers fold exactly per output (correct, slower). */
   uint32_t flags;
   /* 0: A is [ceil(m/4)][kb_total] words.  Otherwise A words per quad, and
    * each piece's blocks start at its a_word (see hb_piece); every A word a

@@ -7,10 +7,13 @@ pinned in test_oracle_fp8.py):
     rejected);
   * exact mode bitwise: ops with requantize, pieces, `onto`, weight panels,
     a batch of layers;
-  * fast mode (FP8 x FP4 matrix cores) within the MXFP8 fast bound
+  * fast mode (FP8 x FP4 matrix cores, each block's codes in two
+    exponent planes) within the fast-mode bound of the MXINT8 path
     (check_fp8_fast) at config 1's sweep M in {1, 16, 128, 1024} (K = 2560,
-    N = 960) and M = 141, with ops and requantize, and with scale bytes
-    outside the fast window (those tiles are computed exactly, bitwise);
+    N = 960) one layer per launch and batched (the streaming kernel, more
+    tiles than CUs, from C, a partial panel, a mid-stream exact recompute),
+    and M = 141, with ops and requantize, and with scale bytes outside the
+    fast window (those tiles are computed exactly, bitwise);
   * the descriptor rule (one MXFP4 plane).
 """
 from __future__ import annotations
@@ -107,24 +110,24 @@ def fp8_abs_sums(m, n, kb, a_words, w_words):
 
 
 def check_fp8_fast(got, want, abs_sums, gq=None, wq=None):
-    """MXFP8 fast-mode bound, an envelope measured on the matrix cores (not
-    a proof): their sum of an instruction's 64 FP8 x FP4 products keeps
-    about 15 bits below its largest term (E4M3 spans 17 binades), where the
-    MXINT8 path's FP6 planes sum exactly.  Measured worst: 1.44e-5 per row
-    and 2^-14.8 of sum |block value| per element; checked with margin: per
-    output row max |gpu - ref| <= 1e-4 max |ref|, per element |gpu - ref| <=
-    2^-13 sum |block value|.  (Exact mode is bitwise.)"""
+    """The fast-mode bound of the MXINT8 path, an envelope measured on the
+    matrix cores (not a proof): per output row max |gpu - ref| <= 1e-5 max
+    |ref|, per element |gpu - ref| <= 2^-17 sum |block value| (+ one
+    rounding of the result).  The matrix cores sum an instruction's FP8 x
+    FP4 products exactly only while they span few binades, so each block's
+    codes go through two MFMAs split by exponent (measured worst 3.3e-7 per
+    row and 2^-21.6 per element; one MFMA over the whole E4M3 range gave
+    1.7e-5 and 2^-14.3).  (Exact mode is bitwise.)"""
     g, w = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
     err = np.abs(g - w)
     row = np.abs(w).max(axis=1, keepdims=True)
     r1 = float((err / np.maximum(row, 1e-300)).max())
     r2 = float((err / np.maximum(abs_sums, 1e-300)).max())
     say("fp8 fast error", dict(normwise=r1, per_element_log2=float(np.log2(max(r2, 1e-300)))))
-    assert r1 <= 1e-4 and r2 <= 2.0 ** -13, (r1, r2)
+    assert r1 <= 1e-5, r1
+    assert (err <= 2.0 ** -17 * abs_sums + 2.0 ** -23 * np.abs(w) + 1e-30).all(), r2
     if gq is not None:
-        gqb = gq.reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
-        wqb = wq.reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
-        assert np.abs(gqb - wqb).max() <= 1 and (gqb != wqb).mean() < 0.01
+        helpers.check_requantized(gq, wq)
 
 
 def per_channel(r, m, n):
@@ -177,12 +180,7 @@ def test_fast_plain_141(gpu):
 def test_fast_ops_requantize(gpu):
     got, gq, want, wq = fp8_layer(gpu, 141, 960, 30, hb.FAST, per_channel, quantize=True,
                                   seed=740)
-    g, w = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
-    row = np.abs(w).max(axis=1, keepdims=True)
-    assert (np.abs(g - w) <= 1e-4 * row).all()
-    gqb = gq.reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
-    wqb = wq.reshape(-1, 144)[:, :128].view(np.int8).astype(np.int32)
-    assert np.abs(gqb - wqb).max() <= 1 and (gqb != wqb).mean() < 0.01
+    helpers.check_fast(got, want, gq, wq)
 
 
 def test_fast_out_of_window_scales_exact(gpu):
@@ -199,3 +197,88 @@ def test_fp8_needs_one_mxfp4_plane(gpu):
     with pytest.raises(hb.HbError) as err:
         hb.linear(gpu, a=a, planes=[w, w], modes=[1, 2], c=c, m=4, n=64, kb_total=1, a_fp8=True)
     assert err.value.code == hb.HB_EINVAL and "MXFP8" in err.value.message
+
+
+# ---- batches over weight panels: the streaming kernel ----
+
+def fp8_batch(gpu, m, n, kb, layers, sets, onto=False, bad=None, seed=0):
+    """`layers` MXFP8 x MXFP4 layers (weights in panels) in one fast batched
+    launch; layer i holds data set i % sets.  The oracle computes each set
+    once and every layer holding it must equal it bit for bit.  bad =
+    (layer, word): that layer's weights get one scale byte outside the
+    fast window in DDR word `word` (the tile holding it is recomputed by
+    the exact fold, bitwise, in the middle of the workgroup's stream)."""
+    rng = np.random.default_rng(seed)
+    a_sets, w_sets, c_sets = [], [], []
+    for _ in range(sets):
+        a_sets.append(helpers.activations_fp8(rng, m, kb * 32)[1])
+        w_sets.append(mxfp4_planes(rng, n, kb)[0][0])
+        c_sets.append(helpers.random_fp32_words(rng, (m, n), 118, 128) if onto else None)
+    set_of = [i % sets for i in range(layers)]
+    w_bad = None
+    if bad is not None:
+        w_bad = w_sets[set_of[bad[0]]].copy()
+        w_bad.reshape(-1, 144)[bad[1], 128 + 2] = 200
+    pb = hb.panel_bytes(n, kb)
+    a_d = torch.empty((layers,) + a_sets[0].shape, dtype=torch.uint8, device=DEV)
+    w_p = torch.empty((layers, pb), dtype=torch.uint8, device=DEV)
+    c_d = torch.zeros((layers, m, n), dtype=torch.float32, device=DEV)
+    w_dev = [dev(w) for w in w_sets]
+    for i in range(layers):
+        a_d[i].copy_(dev(a_sets[set_of[i]]))
+        src = dev(w_bad) if bad is not None and i == bad[0] else w_dev[set_of[i]]
+        hb.pack_weights(src, n, kb, w_p[i], ctx=gpu)
+        if onto:
+            c_d[i].copy_(dev(c_sets[set_of[i]].view(np.float32)))
+    descs = [hb.linear_desc(m, n, kb, a_d[i], [w_p[i]], [0], c_d[i], mode=hb.FAST, panels=True,
+                            onto=onto, a_fp8=True) for i in range(layers)]
+    torch.cuda.synchronize()
+    say("fp8 batch", dict(m=m, n=n, kb=kb, layers=layers, sets=sets, onto=onto, bad=bad))
+    hb.linear_batched(descs, gpu)
+    got = host(c_d).view(np.uint32)
+    rep = {}
+    for i in range(layers):
+        if bad is not None and i == bad[0]:
+            continue
+        if set_of[i] in rep:
+            assert np.array_equal(got[i], got[rep[set_of[i]]]), i
+        else:
+            rep[set_of[i]] = i
+    for s in range(sets):
+        want, _ = helpers.oracle_linear_mt(m, n, kb, a_sets[s], [w_sets[s]], [0], onto=c_sets[s],
+                                           a_fp8=True)
+        if onto:
+            g, w = got[rep[s]].view(np.float32).astype(np.float64), want.view(np.float32)
+            row = np.abs(w.astype(np.float64)).max(axis=1, keepdims=True)
+            assert (np.abs(g - w) <= 1e-5 * row).all()
+        else:
+            check_fp8_fast(got[rep[s]], want, fp8_abs_sums(m, n, kb, a_sets[s], w_sets[s]))
+    if bad is not None:
+        layer, word = bad
+        s = set_of[layer]
+        want, _ = helpers.oracle_linear_mt(m, n, kb, a_sets[s], [w_bad], [0], onto=c_sets[s],
+                                           a_fp8=True)
+        c0 = (word // kb) * 8 // 320 * 320
+        cols = slice(c0, min(c0 + 320, n))
+        assert np.array_equal(got[layer][:, cols], want[:, cols])
+        others = np.setdiff1d(np.arange(n), np.arange(n)[cols])
+        assert np.array_equal(got[layer][:, others], got[rep[s]][:, others])
+
+
+@pytest.mark.parametrize("m,layers,sets", [(1, 256, 5), (16, 256, 5), (128, 256, 7),
+                                           (1024, 64, 3)])
+def test_fast_batched_config1(gpu, m, layers, sets):
+    """Config 1's sweep batched as bench.py times it: K = 2560, N = 960,
+    768 tiles (1,536 at M = 1024) over 256 workgroups."""
+    fp8_batch(gpu, m, 960, 80, layers, sets, seed=800 + m)
+
+
+def test_fast_batched_onto_partial_panel(gpu):
+    """From C, N = 200 (a partial last panel), odd block count, 300 tiles."""
+    fp8_batch(gpu, 1000, 200, 7, 40, 3, onto=True, seed=810)
+
+
+def test_fast_batched_exact_recompute_mid_stream(gpu):
+    """One weight scale byte outside the window in layer 150's middle column
+    tile: that tile is folded exactly, the rest of the stream is fast."""
+    fp8_batch(gpu, 128, 960, 80, 256, 11, bad=(150, 50 * 80 + 41), seed=811)

@@ -193,7 +193,10 @@ void StreamKernel(GemmArgs g) {
   uint32_t dbase[kOps], alim[kOps];
 #pragma unroll
   for (int k = 0; k < kOps; ++k) alim[k] = (nblocks - 1) * kDdrWord + pcol[k] % kDdrWord;
-  auto issue_next = [&]() __attribute__((always_inline)) {
+  // issue_prepare: the step to load next (its source offsets, its slot);
+  // issue_op(k2): the wave's load k2 of it; issue_advance: move the cursor.
+  uint32_t is_s = 0, is_slot = 0;
+  auto issue_prepare = [&]() __attribute__((always_inline)) {
     const uint32_t k = min(dk, sc.count - 1);
     if (k != dcached) {  // uniform: once per tile
       dcached = k;
@@ -207,22 +210,29 @@ void StreamKernel(GemmArgs g) {
                          : min(tl.p0 + pq[k2], n_panels - 1) * steps * kPanelChunk + pcol[k2];
       }
     }
-    const uint32_t s = dk < sc.count ? min(ds, steps - 1) : steps - 1;
-    const uint32_t slot = ring + dslot * kSlot;
-#pragma unroll
-    for (int k2 = 0; k2 < kOps; ++k2) {
-      const uint32_t i = w * kOps + k2;
-      const bool is_a = i < (uint32_t)kALoads;  // uniform
-      const uint32_t off = is_a ? dbase[k2] + min(s * (2 * kDdrWord) + pcol[k2], alim[k2])
-                                : dbase[k2] + s * kPanelChunk;
-      const uint32_t lds = is_a ? slot + i * 1024 : slot + kSlotW + (i - kALoads) * 1024;
-      Dma16(is_a ? da : dw, off, __builtin_amdgcn_readfirstlane(lds));
-    }
+    is_s = dk < sc.count ? min(ds, steps - 1) : steps - 1;
+    is_slot = ring + dslot * kSlot;
+  };
+  auto issue_op = [&](int k2) __attribute__((always_inline)) {
+    const uint32_t i = w * kOps + k2;
+    const bool is_a = i < (uint32_t)kALoads;  // uniform
+    const uint32_t off = is_a ? dbase[k2] + min(is_s * (2 * kDdrWord) + pcol[k2], alim[k2])
+                              : dbase[k2] + is_s * kPanelChunk;
+    const uint32_t lds = is_a ? is_slot + i * 1024 : is_slot + kSlotW + (i - kALoads) * 1024;
+    Dma16(is_a ? da : dw, off, __builtin_amdgcn_readfirstlane(lds));
+  };
+  auto issue_advance = [&]() __attribute__((always_inline)) {
     if (++ds == esteps) {
       ds = 0;
       ++dk;
     }
     dslot = dslot + 1 == kD ? 0u : dslot + 1;
+  };
+  auto issue_next = [&]() __attribute__((always_inline)) {
+    issue_prepare();
+#pragma unroll
+    for (int k2 = 0; k2 < kOps; ++k2) issue_op(k2);
+    issue_advance();
   };
 
   // Reads from ring slot `slot`: the W chunks' B operands and scale dwords;
@@ -370,7 +380,8 @@ void StreamKernel(GemmArgs g) {
   // set of u's parity): wait for this wave's loads of step u + 2, barrier
   // (every wave's loads of step u + 2 landed; every wave done reading slot
   // u: step u's W was read in step u - 1, its A in step u - 2), refill slot
-  // u with step u + kD; read step u + 1's W into `oth` and step u + 2's raw
+  // u with step u + kD (the loads spread between the step's MFMAs); read
+  // step u + 1's W into `oth` and step u + 2's raw
   // A into `use`; convert step u + 1's raw A (read in step u - 1, held in
   // `oth`) while the matrix cores run step u's 20 MFMAs.
   uint32_t slot = 0;
@@ -379,7 +390,7 @@ void StreamKernel(GemmArgs g) {
     WaitVm<(kD - 3) * kOps>();
     WaitLds();
     __syncthreads();
-    issue_next();
+    issue_prepare();  // this step's loads go out between its MFMAs, below
     const uint32_t s1 = slot + 1 == kD ? 0u : slot + 1;
     const uint32_t s2 = s1 + 1 == kD ? 0u : s1 + 1;
     read_w(oth, s1);
@@ -418,31 +429,33 @@ void StreamKernel(GemmArgs g) {
     constexpr int kAFmt = kA8 ? 0 : 2, kSelR = kA8 ? 0 : 1;
     // plane h over the n-tiles, then plane r (branch-free: n-tiles past the
     // layer compute outputs that are not stored)
-    Unroll<kNT>([&](auto t_c) {
-      constexpr int kT = decltype(t_c)::value;
+    auto mfma = [&](auto t_c, const i32x8& av, auto sel_c) __attribute__((always_inline)) {
+      constexpr int kT = decltype(t_c)::value, kSel = decltype(sel_c)::value;
       const i32x8 bt = {(int)use.b[kT][0], (int)use.b[kT][1], (int)use.b[kT][2],
                         (int)use.b[kT][3], 0, 0, 0, 0};
-      acc[kT] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          ah, bt, acc[kT], kAFmt, 4, 0, use.sa, kT % 2,
-          (int)(use.sw[kT / 2] >> (16 * (lane & 1))));
+      const int sb = (int)(use.sw[kT / 2] >> (16 * (lane & 1)));
+      acc[kT] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bt, acc[kT], kAFmt, 4, kSel,
+                                                                use.sa, kT % 2, sb);
+    };
+    // The step's loads of step u + kD go out between the MFMAs (one after
+    // every 2 kNT / kOps of them): a load waits to issue while the CU's
+    // outstanding requests are at their limit, and the MFMAs issued before
+    // it keep the matrix cores busy meanwhile, so the loads refill the
+    // CU's request queue through the whole step.
+    constexpr int kEvery = 2 * kNT / kOps;
+    static_assert(2 * kNT % kOps == 0, "loads spread evenly over the MFMAs");
+    Unroll<2 * kNT>([&](auto u_c) {
+      constexpr int kU = decltype(u_c)::value;
+      if constexpr (kU < kNT) mfma(std::integral_constant<int, kU>{}, ah, std::integral_constant<int, 0>{});
+      else mfma(std::integral_constant<int, kU - kNT>{}, ar, std::integral_constant<int, kSelR>{});
+      // Volatile asms keep their order, and the MFMA builtins (pure) would
+      // otherwise move freely: an empty asm after each MFMA that takes the
+      // previous MFMA's accumulators (complete by now, as this one runs)
+      // holds every MFMA between its neighbours, and the loads in place.
+      if constexpr (kU > 0) asm volatile("" ::"a"(acc[(kU - 1) % kNT]));
+      if constexpr (kU % kEvery == kEvery - 1) issue_op(kU / kEvery);
     });
-    Unroll<kNT>([&](auto t_c) {
-      constexpr int kT = decltype(t_c)::value;
-      const i32x8 bt = {(int)use.b[kT][0], (int)use.b[kT][1], (int)use.b[kT][2],
-                        (int)use.b[kT][3], 0, 0, 0, 0};
-      acc[kT] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          ar, bt, acc[kT], kAFmt, 4, kSelR, use.sa, kT % 2,
-          (int)(use.sw[kT / 2] >> (16 * (lane & 1))));
-    });
-    // the step's MFMAs and the conversion are issued here, before the next
-    // barrier, so they overlap the next step's loads and LDS reads
-    // issue order: the LDS reads, then each MFMA followed by a share of the
-    // step's vector ALU work, which runs while the MFMA does
-    __builtin_amdgcn_sched_group_barrier(0x100, 17, 0);
-    Unroll<2 * kNT>([&](auto) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-    });
+    issue_advance();
 #pragma unroll
     for (int t = 0; t < kNT; ++t) asm volatile("" : "+a"(acc[t]));
     asm volatile("" : "+v"(oth.h), "+v"(oth.r), "+v"(oth.sa), "+v"(oth.abad));

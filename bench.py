@@ -295,9 +295,9 @@ class Chain:
         return tb
 
     def add(self, n, kb, a, planes, c, ops=(), q=None, onto=False, tbuf=None, c_out=True):
-        """c_out=False: the model keeps only the requantized words q; the
-        fp32 C this build writes as well is not counted in the algorithmic
-        bytes (the NPU leaves it in its on-chip FBUF)."""
+        """c_out=False: the model keeps only the requantized words q (the
+        NPU leaves the fp32 result in its on-chip FBUF): not counted in the
+        algorithmic bytes; with c None the layer does not write it either."""
         modes = [1, 2] if len(planes) == 2 else [0]
         w8p = self.w8_panels and len(planes) == 2
         pan_flag = False
@@ -841,8 +841,8 @@ class SparseDriveBackbone(Chain):
     MXFP4 weights (E8M0 exponents -10..-2) and the W8 stem; 1x1 convs read
     the previous layer's MXINT8 words, 3x3 convs and the concatenated
     downsample operand read synthetic im2col words of their shape (the
-    gather is the DMA engine's, not a GEMM).  The fp32 C of conv1 and conv2
-    goes to one scratch tensor and is not counted in the bytes."""
+    gather is the DMA engine's, not a GEMM).  conv1 and conv2 keep only
+    their MXINT8 words (C = NULL), as the compiler stores only those."""
 
     CAMS, STEM_H, STEM_W = 6, 128, 352
     STAGES = ((3, 64, 1), (4, 128, 2), (6, 256, 2), (3, 512, 2))
@@ -865,18 +865,12 @@ class SparseDriveBackbone(Chain):
         rows(r)
         x8 = self.a_words(2)  # the max-pool's MXINT8 output, 64 channels
         cin = 64
-        scratch_elems = 0
         plan = []
         rin = r
         for blocks, mid, stride in self.STAGES:
             rout = rin // (stride * stride)
-            for j in range(blocks):
-                r1 = rin if j == 0 else rout
-                scratch_elems = max(scratch_elems, r1 * mid, rout * mid)
             plan.append((blocks, mid, stride, rin, rout))
             rin = rout
-        self.scratch = torch.empty((scratch_elems,), dtype=torch.float32, device=self.dev)
-        self.keep.append(self.scratch)
         for blocks, mid, stride, rin, rout in plan:
             cout = 4 * mid
             y32 = None
@@ -886,16 +880,14 @@ class SparseDriveBackbone(Chain):
                 # conv1 over the block's input positions
                 rows(r1)
                 t1 = self.a_words(mid // 32)
-                self.add(mid, k1 // 32, x8, [self.w_words(mid, k1 // 32)],
-                         self.scratch[:r1 * mid].view(r1, mid), ops=[bias(mid), relu], q=t1,
-                         c_out=False)
+                self.add(mid, k1 // 32, x8, [self.w_words(mid, k1 // 32)], None,
+                         ops=[bias(mid), relu], q=t1, c_out=False)
                 # conv2: 3x3 im2col at the output positions
                 rows(rout)
                 t2 = self.a_words(mid // 32)
                 kb2 = 9 * mid // 32
-                self.add(mid, kb2, self.a_words(kb2), [self.w_words(mid, kb2)],
-                         self.scratch[:rout * mid].view(rout, mid), ops=[bias(mid), relu],
-                         q=t2, c_out=False)
+                self.add(mid, kb2, self.a_words(kb2), [self.w_words(mid, kb2)], None,
+                         ops=[bias(mid), relu], q=t2, c_out=False)
                 # conv3 (+ downsample in block 0, + residual after)
                 y8 = self.a_words(cout // 32)
                 if j == 0:

@@ -522,7 +522,11 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g, bool* mixed) {
                                     : (uint64_t)(d->n / 8) * d->kb_total * hb::kDdrWord;
   if (a_end * hb::kDdrWord > (1ull << 32) || w_bytes > (1ull << 32))
     return Fail(HB_EINVAL, "A or W spans more than 4 GiB");
-  if (!d->a || !d->c) return Fail(HB_EINVAL, "null A or C");
+  if (!d->a) return Fail(HB_EINVAL, "null A");
+  // C may be left out (null) where the layer keeps only its requantized
+  // words: the fp32 result then stays in the kernel, as in the NPU's FBUF
+  if (!d->c && (!d->q_out || d->onto))
+    return Fail(HB_EINVAL, "null C needs q_out and no onto");
   if (d->n_ops > HB_MAX_EP_OPS) return Fail(HB_EINVAL, "n_ops = %u", d->n_ops);
   if (d->q_out && d->n % 32 != 0) return Fail(HB_EINVAL, "quantized output needs n %% 32 == 0");
   const bool fp8 = (d->flags & HB_LINEAR_A_FP8) != 0;
@@ -632,6 +636,7 @@ int LinearBatched(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count,
                   x.n_planes == d0.n_planes && x.flags == d0.flags && x.onto == d0.onto &&
                   x.n_pieces == d0.n_pieces && x.n_ops == d0.n_ops && x.tbuf == d0.tbuf &&
                   (x.q_out != nullptr) == (d0.q_out != nullptr) &&
+                  (x.c != nullptr) == (d0.c != nullptr) &&
                   Diff(d0.a, x.a) == i * g.a_batch && Diff(d0.w[0], x.w[0]) == i * g.w_batch &&
                   (x.n_planes < 2 || Diff(d0.w[1], x.w[1]) == i * g.w_batch) &&
                   Diff(d0.c, x.c) == i * g.c_batch * 4 &&
@@ -652,7 +657,10 @@ int LinearBatched(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count,
     if (g.w_fp6 && (g.a_batch % 16 != 0 || g.w_batch % 16 != 0))
       return Fail(HB_EINVAL, "W8 panels: layers' A and panels must be 16-byte aligned");
   }
-  if (mixed) return LinearChain(ctx, d, count, fixed);
+  if (mixed) {  // the runs of the chain meet in C
+    if (!d[0].c) return Fail(HB_EINVAL, "pieces at different A offsets need C");
+    return LinearChain(ctx, d, count, fixed);
+  }
   hipError_t err = hb::LaunchLinear(g, count, (d[0].flags & HB_LINEAR_FAST) != 0, ctx->ws,
                                     ctx->stream, fixed);
   if (err == hipErrorOutOfMemory && fixed != nullptr && fixed->need > fixed->bytes)

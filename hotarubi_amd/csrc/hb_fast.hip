@@ -445,10 +445,12 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
         }
         EpApplyFastN(kind, g.op_imm[o], y, x2, p, lds_act);
       }
+      if (g.c != nullptr) {  // uniform
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        uint32_t* c_r = c + row_step(i) * g.n;  // uniform
-        if (row_h + row_step(i) < g.m && col < g.n) c_r[off_l] = __float_as_uint(y[i]);
+        for (int i = 0; i < 8; ++i) {
+          uint32_t* c_r = c + row_step(i) * g.n;  // uniform
+          if (row_h + row_step(i) < g.m && col < g.n) c_r[off_l] = __float_as_uint(y[i]);
+        }
       }
       if (q_out != nullptr) {  // MXINT8 requantize over the 32 lanes holding a row's block
         // Values i < 4 are rows row_h .. row_h + 3, i >= 4 rows row_h + 8 ..

@@ -550,7 +550,7 @@ __global__ __launch_bounds__(kThreads) void GemmTileKernel(GemmArgs g) {
     for (int e = 0; e < 16; ++e) {
       const uint32_t row = row_l + i * 16 + (e & 3), col = col_l + (e >> 2) * 16;
       const bool in_tile = (row >> 2) < g.quads && (col >> 3) < g.groups;
-      if (in_tile && (!kLinear || row < g.m))
+      if (in_tile && (!kLinear || (row < g.m && g.c != nullptr)))
         *CElem<kLinear>(g, c, row, col) = __float_as_uint(res[i][e]);
     }
 

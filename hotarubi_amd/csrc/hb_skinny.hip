@@ -354,7 +354,7 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void Skinn
         y = __float_as_uint(EpApplyFast(kind, g.op_imm[op], __uint_as_float(y),
                                         __uint_as_float(x2), __uint_as_float(pv), lds_act));
       }
-      if (row < g.m) c[(size_t)row * g.n + col] = y;
+      if (row < g.m && g.c != nullptr) c[(size_t)row * g.n + col] = y;
     }
     if (q_out != nullptr) {
       const uint32_t e = HalfMax32(in ? ExpField(y) : 0u);
@@ -661,7 +661,7 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
       }
       EpApplyFastN<false>(kind, g.op_imm[op], y, x2, pv, act);
     }
-    if (col_in) {
+    if (col_in && g.c != nullptr) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t row = row_of(4 * j + i);

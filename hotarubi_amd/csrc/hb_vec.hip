@@ -164,7 +164,7 @@ __global__ __launch_bounds__(256) void EpilogueKernel(GemmArgs g) {
                                                   g.tbuf + 512))
                     : EpApply(kind, g.op_imm[o], y, x2, p, g.tbuf + 512);
   }
-  if (in && row < g.m) g.c[at] = y;
+  if (in && row < g.m && g.c != nullptr) g.c[at] = y;
   if (g.q_out != nullptr) {  // n % 32 == 0: a 32-lane half is all in or all out
     const uint32_t e = HalfMax32(in ? ExpField(y) : 0u);
     if (in) {

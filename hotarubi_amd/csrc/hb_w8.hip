@@ -455,7 +455,7 @@ void W8Kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t row = row_w + rs + 8 * i;
-      if (row < g.m && col < g.n) {
+      if (row < g.m && col < g.n && g.c != nullptr) {
         uint32_t* out = c + (size_t)row * g.n + col;
         if (c_vec) {
           *reinterpret_cast<float4*>(out) = float4{y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]};

@@ -312,13 +312,27 @@ void StreamKernel(GemmArgs g) {
     }
   };
   // Finish the current tile: exact recompute if flagged, else store C.
+  // Finish the current tile: each n-tile's 32 x 32 values (the accumulators,
+  // or the exact fold where a scale byte or an initial C left the window)
+  // through the wave's LDS block, stored as 16-byte rows of 4 columns (rows
+  // at row ^ ((row >> 2) & 1): conflict-free writes and reads); +0 maps -0
+  // (and a flushed denormal) to +0.  A layer with ops or the requantize
+  // takes each lane's 4 columns of 4 rows through the ops in FP32 hardware
+  // arithmetic, C (when kept) and the MXINT8 requantize: a row's 32-column
+  // block is 8 lanes, their largest exponent field by 3 swizzles, one
+  // 4-byte store of codes per lane and row.
   auto end_tile = [&](uint32_t bad) __attribute__((always_inline)) {
-    const uint8_t* a = g.a + tl.z * g.a_batch;
-    const uint8_t* w0 = g.w[0] + tl.z * g.w_batch;
-    uint32_t* c = g.c + tl.z * g.c_batch;
+    const uint32_t z = tl.z;
+    const uint8_t* a = g.a + z * g.a_batch;
+    const uint8_t* w0 = g.w[0] + z * g.w_batch;
+    uint32_t* c = g.c != nullptr ? g.c + z * g.c_batch : nullptr;
+    uint8_t* q = g.q_out != nullptr ? g.q_out + z * g.q_batch : nullptr;
+    // (MXINT8 layers with ops or the requantize take the tile kernel, whose
+    // epilogue runs on 16 waves; the fused path is compiled for MXFP8 only)
+    const bool fused = kA8 && (g.n_ops != 0 || q != nullptr);  // uniform
     const bool slow = __builtin_amdgcn_readfirstlane(
         __builtin_amdgcn_ballot_w64(init_unsafe || bad != 0) != 0);
-    if (slow) {  // a scale byte or an initial C left the window: every output exactly
+    if (slow && !fused) {  // every output exactly, straight to C
       WaitVm<0>();
       for (uint32_t j = 0; j < kNT; ++j)
         for (uint32_t e = 0; e < 16; ++e) {
@@ -331,16 +345,29 @@ void StreamKernel(GemmArgs g) {
         }
       return;
     }
-    // Each MFMA tile through the wave's LDS block, stored as 16-byte rows
-    // of 4 columns (rows at row ^ ((row >> 2) & 1): conflict-free writes and
-    // reads); +0 maps -0 (and a flushed denormal) to +0.
+    if (slow) WaitVm<0>();
+    const uint32_t rows4 = g.quads * 4, nb = g.n >> 5;
     Unroll<kNT>([&](auto jj) {
       constexpr int kJ = decltype(jj)::value;
       if ((uint32_t)kJ >= live_nt) return;
+      if (slow) {  // the exact fold of each output (a layer with ops or requantize)
+        for (uint32_t e = 0; e < 16; ++e) {
+          const uint32_t rl = 8 * (e / 4) + 4 * (lane >> 5) + (e & 3);
+          const uint32_t row = row_w + rl, col = tl.col0 + kJ * 32 + (lane & 31);
+          uint32_t v = 0;
+          if (row < rows4 && col < g.n) {
+            const uint32_t init = g.acc && row < g.m ? c[(size_t)row * g.n + col] : 0u;
+            v = kA8 ? SlowLinearFp8(g, a, w0, init, row, col)
+                    : SlowLinear(g, a, w0, w0, init, row, col);
+          }
+          xp[(rl ^ ((rl >> 2) & 1)) * 32 + (lane & 31)] = __uint_as_float(v);
+        }
+      } else {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const uint32_t row = 8 * (e / 4) + 4 * (lane >> 5) + (e & 3);
-        xp[(row ^ ((row >> 2) & 1)) * 32 + (lane & 31)] = acc[kJ][e] + 0.0f;
+        for (int e = 0; e < 16; ++e) {
+          const uint32_t row = 8 * (e / 4) + 4 * (lane >> 5) + (e & 3);
+          xp[(row ^ ((row >> 2) & 1)) * 32 + (lane & 31)] = acc[kJ][e] + 0.0f;
+        }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -353,13 +380,69 @@ void StreamKernel(GemmArgs g) {
       const uint32_t col = tl.col0 + kJ * 32 + 4 * (lane & 7);
       const uint32_t prow = lane >> 3;
       const uint32_t row = row_w + (prow ^ ((prow >> 2) & 1));
-      float4* out = reinterpret_cast<float4*>(c + (size_t)row * g.n + col);
-      const size_t q_step = (size_t)2 * g.n;  // 8 rows, in float4 units
-      if (col < g.n) {
-        if (row < g.m) out[0] = v0;
-        if (row + 8 < g.m) out[q_step] = v1;
-        if (row + 16 < g.m) out[2 * q_step] = v2;
-        if (row + 24 < g.m) out[3 * q_step] = v3;
+      if (!fused) {
+        float4* out = reinterpret_cast<float4*>(c + (size_t)row * g.n + col);
+        const size_t q_step = (size_t)2 * g.n;  // 8 rows, in float4 units
+        if (col < g.n) {
+          if (row < g.m) out[0] = v0;
+          if (row + 8 < g.m) out[q_step] = v1;
+          if (row + 16 < g.m) out[2 * q_step] = v2;
+          if (row + 24 < g.m) out[3 * q_step] = v3;
+        }
+        return;
+      }
+      // rows row + 8 i, columns col .. col + 3 (n % 8 == 0: all four are
+      // in the layer or none)
+      f32x4_t y[4] = {f32x4_t{v0.x, v0.y, v0.z, v0.w}, f32x4_t{v1.x, v1.y, v1.z, v1.w},
+                      f32x4_t{v2.x, v2.y, v2.z, v2.w}, f32x4_t{v3.x, v3.y, v3.z, v3.w}};
+      const bool col_in = col < g.n;
+      const uint32_t cc = col_in ? col : 0u;
+      for (uint32_t o = 0; o < g.n_ops; ++o) {
+        const uint32_t kind = g.op_kind[o];
+        f32x4_t p = {};
+        if (kind == kEpAddP || kind == kEpMulP) {
+          const uint32_t* pv = g.op_vec[o] + z * g.op_vec_batch[o] + cc;
+          p = f32x4_t{__uint_as_float(pv[0]), __uint_as_float(pv[1]), __uint_as_float(pv[2]),
+                      __uint_as_float(pv[3])};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f32x4_t x2 = {};
+          if ((kind == kEpAdd || kind == kEpActMul) && row + 8 * i < g.m && col_in) {
+            const uint32_t* xv = g.op_x2[o] + z * g.op_x2_batch[o] + (size_t)(row + 8 * i) * g.n + col;
+            x2 = f32x4_t{__uint_as_float(xv[0]), __uint_as_float(xv[1]), __uint_as_float(xv[2]),
+                         __uint_as_float(xv[3])};
+          }
+          EpApplyFastN<false>(kind, g.op_imm[o], y[i], x2, p, g.tbuf + 512);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t r = row + 8 * i;
+        if (c != nullptr && col_in && r < g.m)
+          *reinterpret_cast<float4*>(c + (size_t)r * g.n + col) =
+              float4{y[i][0], y[i][1], y[i][2], y[i][3]};
+        if (q == nullptr) continue;
+        uint32_t e = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) e = max(e, ExpField(__float_as_uint(y[i][k])));
+        // the row's 8 lanes (lanes 8 p .. 8 p + 7): xor 1, 2, 4
+        e = max(e, (uint32_t)__builtin_amdgcn_ds_swizzle((int)e, 0x041F));
+        e = max(e, (uint32_t)__builtin_amdgcn_ds_swizzle((int)e, 0x081F));
+        e = max(e, (uint32_t)__builtin_amdgcn_ds_swizzle((int)e, 0x101F));
+        if (r < rows4 && col_in) {
+          uint8_t* word = q + ((size_t)(r >> 2) * nb + (col >> 5)) * kDdrWord;
+          uint32_t codes = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            codes |= (uint32_t)QuantizeElementHw(__float_as_uint(y[i][k]), e) << (8 * k);
+          *reinterpret_cast<uint32_t*>(word + (r & 3) * 32 + 4 * (lane & 7)) = codes;
+          if ((lane & 7) == 0) word[128 + (r & 3)] = (uint8_t)ScaleByteOf(e);
+          if ((lane & 7) == 1 && (r & 3) == 0) {
+            uint32_t* pad = reinterpret_cast<uint32_t*>(word + 132);
+            pad[0] = pad[1] = pad[2] = 0u;
+          }
+        }
       }
     });
   };
@@ -481,12 +564,16 @@ bool StreamEligible(const GemmArgs& args) {
   const bool aligned = reinterpret_cast<uintptr_t>(args.c) % 16 == 0 && args.c_batch % 4 == 0 &&
                        reinterpret_cast<uintptr_t>(args.a) % 16 == 0 && args.a_batch % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(args.w[0]) % 16 == 0 && args.w_batch % 16 == 0;
-  // MXINT8 layers of up to 64 rows have the skinny and split kernels;
-  // MXFP8 layers of any row count stream here
+  // the requantized words are written 4 bytes at a time
+  const bool q_aligned = args.q_out == nullptr ||
+                         (reinterpret_cast<uintptr_t>(args.q_out) % 4 == 0 && args.q_batch % 4 == 0);
+  // MXINT8 layers of up to 64 rows have the skinny and split kernels, and
+  // with ops or the requantize the tile kernel; MXFP8 layers of any row
+  // count, plain or not, stream here
   return args.w_panels && args.n_planes == 1 && args.modes[0] == kModeFp4 && aligned &&
-         args.n_ops == 0 && args.q_out == nullptr && args.n_pieces == 1 &&
-         args.piece_off[0] == 0 && args.piece_kb[0] == args.kb_total &&
-         (args.a_fp8 || args.quads * 4 > 64);
+         q_aligned && args.n_pieces == 1 && args.piece_off[0] == 0 &&
+         args.piece_kb[0] == args.kb_total &&
+         (args.a_fp8 || (args.quads * 4 > 64 && args.n_ops == 0 && args.q_out == nullptr));
 }
 
 hipError_t LaunchStream(const GemmArgs& in, uint32_t batch, hipStream_t stream) {

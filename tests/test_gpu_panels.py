@@ -19,7 +19,8 @@ import torch
 import helpers
 import hotarubi_amd as hb
 import oracle
-from test_gpu_bench_routes import DEV, batched_layers, dev, host, per_channel, say, single_layer
+from test_gpu_bench_routes import (DEV, batched_layers, dev, host, per_channel, say, single_layer,
+                                    to_panels)
 
 pytestmark = pytest.mark.gpu
 
@@ -250,3 +251,78 @@ def test_pieces_over_panels(gpu, mode):
 @pytest.mark.parametrize("m,w8", [(128, False), (1000, True), (64, False)])
 def test_exact_over_panels(gpu, m, w8):
     single_layer(gpu, m, 320, 13, w8, hb.EXACT, seed=512 + m, panels=True)
+
+
+# ---- the streaming kernel's epilogue: ops, C and the requantize ----
+
+def all_ops(rng, m, n):
+    """Every fast epilogue op kind: MULP, ADDP, SCALE, ADD, ACT (the table's
+    activation), ACT_MUL, RELU, COPY."""
+    vec = lambda lo, hi: np.asarray(rng.uniform(lo, hi, n), np.float32).view(np.uint32)
+    return [(hb.EP_MULP, vec(0.5, 2.0)), (hb.EP_ADDP, vec(-0.1, 0.1)),
+            (hb.EP_SCALE, int(np.float32(0.75).view(np.uint32))),
+            (hb.EP_ADD, helpers.random_fp32_words(rng, (m, n), 118, 126)),
+            (hb.EP_ACT, None),
+            (hb.EP_ACT_MUL, helpers.random_fp32_words(rng, (m, n), 124, 128)),
+            (hb.EP_RELU, None), (hb.EP_COPY, None)]
+
+
+def stream_ops(gpu, m, n, kb, ops_fn, seed, keep_c=True, onto=False, bad=False, fp8=False):
+    """One layer over panels with ops and the requantize, tiles enough to
+    take the streaming kernel (at least one per CU); bad: a few weight
+    scale bytes outside the fast window (their tiles are folded exactly,
+    then the same ops)."""
+    rng = np.random.default_rng(seed)
+    a = helpers.activations_fp8(rng, m, kb * 32)[1] if fp8 else helpers.activations(rng, m, kb * 32)[1]
+    w = mxfp4_w(rng, n, kb)
+    if bad:
+        w.reshape(-1, 144)[::997, 129] = 200
+    ops = ops_fn(rng, m, n)
+    tbuf = helpers.activation_table("silu")
+    c0 = helpers.random_fp32_words(rng, (m, n), 118, 128) if onto else None
+    dev_ops = [(k, dev(v.view(np.float32)) if isinstance(v, np.ndarray) else v) for k, v in ops]
+    c_d = (dev(c0.view(np.float32)) if onto else torch.zeros((m, n), dtype=torch.float32, device=DEV)) \
+        if keep_c else None
+    q_d = torch.full(((m + 3) // 4 * (n // 32), 144), 0xA5, dtype=torch.uint8, device=DEV)
+    say("stream ops", dict(m=m, n=n, kb=kb, ops=[o[0] for o in ops], keep_c=keep_c, onto=onto,
+                           bad=bad, fp8=fp8))
+    hb.linear(gpu, a=dev(a), planes=[to_panels(gpu, dev(w), n, kb)], modes=[0], c=c_d, m=m, n=n,
+              kb_total=kb, ops=dev_ops, tbuf=dev(tbuf.view(np.int64)), q_out=q_d, mode=hb.FAST,
+              panels=True, onto=onto, a_fp8=fp8)
+    gq = host(q_d)
+    want, wq = helpers.oracle_linear_mt(m, n, kb, a, [w], [0], ops=ops, tbuf=tbuf, quantize=True,
+                                        onto=c0, a_fp8=fp8)
+    if keep_c:
+        helpers.check_fast(host(c_d).view(np.uint32), want)
+    helpers.check_requantized(gq, wq)
+
+
+@pytest.mark.parametrize("m", [4096, 4093])
+def test_stream_all_ops_requantize_mxfp8(gpu, m):
+    """The streaming kernel's fused epilogue (MXFP8 layers with ops or the
+    requantize stream): 4096 (and 4093: a partial last quad) x 2560 x 160,
+    32 x 8 = 256 tiles, every op kind, C and the requantize."""
+    stream_ops(gpu, m, 2560, 5, all_ops, seed=620 + m, fp8=True)
+
+
+def test_stream_ops_without_c_mxfp8(gpu):
+    stream_ops(gpu, 4096, 2560, 5, lambda r, m, n: all_ops(r, m, n)[:3], seed=625, keep_c=False,
+               fp8=True)
+
+
+def test_stream_ops_exact_recompute_mxfp8(gpu):
+    stream_ops(gpu, 4096, 2560, 5, lambda r, m, n: all_ops(r, m, n)[:5], seed=626, bad=True,
+               fp8=True)
+
+
+def test_stream_ops_onto_mxfp8(gpu):
+    """From C (a residual start), bias and ReLU."""
+    stream_ops(gpu, 32768, 320, 3, lambda r, m, n: [all_ops(r, m, n)[1], (hb.EP_RELU, None)],
+               seed=627, onto=True, fp8=True)
+
+
+@pytest.mark.parametrize("m", [4096, 4093])
+def test_tile_kernel_all_ops_requantize(gpu, m):
+    """MXINT8 layers with ops over panels take the 128-row tile kernel: every
+    op kind, C and the requantize."""
+    stream_ops(gpu, m, 2560, 5, all_ops, seed=630 + m)

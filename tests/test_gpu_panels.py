@@ -326,3 +326,56 @@ def test_tile_kernel_all_ops_requantize(gpu, m):
     """MXINT8 layers with ops over panels take the 128-row tile kernel: every
     op kind, C and the requantize."""
     stream_ops(gpu, m, 2560, 5, all_ops, seed=630 + m)
+
+
+# ---- the skinny kernel over panels: batches of layers of up to 16 rows ----
+
+def skinny_batch(gpu, m, n, kb, layers, w8=False, pieces=None, bad=False, seed=0):
+    """`layers` layers of m <= 16 rows over weight panels in one fast batched
+    launch (the skinny kernel), each checked against the oracle.  w8: both
+    nibble planes packed as panels; pieces: a piece list; bad: weight scale
+    bytes outside the fast window in each layer (those workgroups fold
+    exactly)."""
+    rng = np.random.default_rng(seed)
+    a_h, w_h = [], []
+    for i in range(layers):
+        a_h.append(helpers.activations(rng, m, kb * 32)[1])
+        planes, modes = (list(helpers.w8_planes_from_int8(rng.integers(-127, 128, (n, kb * 32)))), [1, 2]) \
+            if w8 else ([mxfp4_w(rng, n, kb)], [0])
+        if bad:
+            planes[0].reshape(-1, 144)[::7, 128 + i % 8] = 200
+        w_h.append(planes)
+    a_d = dev(np.stack(a_h))
+    pb = hb.panel_bytes(n, kb)
+    w_p = torch.empty((len(modes), layers, pb), dtype=torch.uint8, device=DEV)
+    for i in range(layers):
+        for l, p in enumerate(w_h[i]):
+            hb.pack_weights(dev(p), n, kb, w_p[l, i], ctx=gpu)
+    c_d = torch.zeros((layers, m, n), dtype=torch.float32, device=DEV)
+    descs = [hb.linear_desc(m, n, kb, a_d[i], [w_p[l, i] for l in range(len(modes))], modes, c_d[i],
+                            mode=hb.FAST, panels=True, pieces=pieces) for i in range(layers)]
+    torch.cuda.synchronize()
+    say("skinny batch", dict(m=m, n=n, kb=kb, layers=layers, w8=w8, pieces=pieces, bad=bad))
+    hb.linear_batched(descs, gpu)
+    got = host(c_d).view(np.uint32)
+    for i in range(layers):
+        want, _ = helpers.oracle_linear_mt(m, n, kb, a_h[i], w_h[i], modes, pieces=pieces)
+        helpers.check_fast(got[i], want)
+
+
+@pytest.mark.parametrize("m,n,kb", [(16, 72, 5), (16, 200, 7), (5, 136, 3)])
+def test_skinny_partial_panel_odd_blocks(gpu, m, n, kb):
+    """n not a multiple of 64 (the last panel partial), odd block counts."""
+    skinny_batch(gpu, m, n, kb, 4, seed=640 + n)
+
+
+def test_skinny_w8_planes_as_panels(gpu):
+    skinny_batch(gpu, 8, 136, 9, 3, w8=True, seed=650)
+
+
+def test_skinny_pieces(gpu):
+    skinny_batch(gpu, 12, 256, 12, 3, pieces=[(4, 5), (0, 4), (9, 3)], seed=651)
+
+
+def test_skinny_out_of_window_scales(gpu):
+    skinny_batch(gpu, 16, 128, 6, 3, bad=True, seed=652)

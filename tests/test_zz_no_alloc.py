@@ -9,7 +9,8 @@ checked bitwise against hb_linear_batched_async's on the same descriptors
   * batched and skinny layers, which need no scratch;
   * capture in a HIP graph, replayed between eager work (the point of the
     entry point: no allocation happens inside the capture, even for a shape
-    never run before);
+    never run before), and a captured layer whose K splits meet in the
+    array replayed between eager calls that overwrite it;
   * a layer whose partial sums exceed the array is rejected with HB_ENOMEM
     before anything is launched.
 
@@ -169,6 +170,63 @@ def test_graph_capture_of_a_new_shape(gpu):
             c2_d.zero_()
             hb.linear_noalloc([desc2], ctx)
             assert np.array_equal(host_u32(c2_d), want2)
+        del g
+    finally:
+        ctx.set_stream(main.cuda_stream)
+        torch.cuda.synchronize()
+        ctx.close()
+
+
+def test_graph_capture_through_the_array(gpu):
+    """A captured layer whose K splits meet in the fixed array (1,100 x 512
+    x 512 fast: more than 1,024 rows on fewer than 128 tiles), replayed
+    between eager calls that overwrite the array (an exact 100-row layer
+    with MULP and ADDP, its epilogue deferred through the array): every
+    replay and every eager call equals hb_linear_batched_async's result."""
+    rng = np.random.default_rng(16)
+    ctx = hb.Context(0)
+    main = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    m, n, kb = 1100, 512, 16
+    a, planes, modes = mxfp4_layer(rng, m, n, kb)
+    a_d, w_d = dev(a), [dev(p) for p in planes]
+    c_d = torch.zeros((m, n), dtype=torch.float32, device=DEV)
+    desc = hb.linear_desc(m, n, kb, a_d, w_d, modes, c_d, mode=hb.FAST)
+    c_ref = torch.zeros((m, n), dtype=torch.float32, device=DEV)
+    desc_ref = hb.linear_desc(m, n, kb, a_d, w_d, modes, c_ref, mode=hb.FAST)
+    m2, n2, kb2 = 100, 256, 8
+    a2, planes2, modes2 = mxfp4_layer(rng, m2, n2, kb2)
+    ops2 = [(hb.EP_MULP, dev(np.asarray(rng.uniform(0.5, 2.0, n2), np.float32))),
+            (hb.EP_ADDP, dev(np.asarray(rng.normal(0, 0.1, n2), np.float32)))]
+    a2_d, w2_d = dev(a2), [dev(p) for p in planes2]
+    c2_d = torch.zeros((m2, n2), dtype=torch.float32, device=DEV)
+    desc2 = hb.linear_desc(m2, n2, kb2, a2_d, w2_d, modes2, c2_d, ops=ops2, mode=hb.EXACT)
+    c2_ref = torch.zeros((m2, n2), dtype=torch.float32, device=DEV)
+    desc2_ref = hb.linear_desc(m2, n2, kb2, a2_d, w2_d, modes2, c2_ref, ops=ops2, mode=hb.EXACT)
+    try:
+        ctx.set_stream(main.cuda_stream)
+        hb.linear_batched([desc_ref], ctx)
+        hb.linear_batched([desc2_ref], ctx)
+        ref, ref2 = host_u32(c_ref), host_u32(c2_ref)
+        want, _ = helpers.oracle_linear_mt(m, n, kb, a, planes, modes)
+        helpers.check_fast(ref, want)
+        ctx.set_stream(side.cuda_stream)
+        hb.linear_noalloc([desc], ctx)  # the shape once, outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        say("capture through the array", dict(m=m, n=n, kb=kb))
+        with torch.cuda.graph(g, stream=side):
+            ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+            hb.linear_noalloc([desc], ctx)
+        ctx.set_stream(main.cuda_stream)
+        for rep in range(3):
+            c2_d.zero_()
+            hb.linear_noalloc([desc2], ctx)  # overwrites the array
+            assert np.array_equal(host_u32(c2_d), ref2), rep
+            c_d.zero_()
+            say("replay", rep)
+            g.replay()
+            assert np.array_equal(host_u32(c_d), ref), rep
         del g
     finally:
         ctx.set_stream(main.cuda_stream)

@@ -529,6 +529,8 @@ int LinearArgs(const hb_linear_desc* d, hb::GemmArgs* g, bool* mixed) {
     return Fail(HB_EINVAL, "null C needs q_out and no onto");
   if (d->n_ops > HB_MAX_EP_OPS) return Fail(HB_EINVAL, "n_ops = %u", d->n_ops);
   if (d->q_out && d->n % 32 != 0) return Fail(HB_EINVAL, "quantized output needs n %% 32 == 0");
+  if (reinterpret_cast<uintptr_t>(d->c) % 4 != 0 || reinterpret_cast<uintptr_t>(d->q_out) % 4 != 0)
+    return Fail(HB_EINVAL, "C and q_out must be 4-byte aligned");
   const bool fp8 = (d->flags & HB_LINEAR_A_FP8) != 0;
   if (d->flags &
           ~(uint32_t)(HB_LINEAR_FAST | HB_LINEAR_PANELS | HB_LINEAR_W8_PANELS | HB_LINEAR_A_FP8) ||

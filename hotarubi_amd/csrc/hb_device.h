@@ -373,4 +373,35 @@ __device__ __forceinline__ uint32_t SlowLinearFp8(const GemmArgs& g, const uint8
   return acc;
 }
 
+// Starts kT accumulator tiles (16 values per lane each) from C.  A tile's
+// 16 loads issue together, before their first wait: with a branch around each load
+// the compiler waits for each in turn (measured on a 128 x 256 tile, 64
+// values per lane: 19 us against 2).  An element outside the m x n output
+// reads C's first word and starts from +0.  at(j, r, row, col) names value
+// r of tile j.  Returns whether a start value's exponent field exceeds 252.
+template <int kT, typename Acc, typename At>
+__device__ __forceinline__ bool AccFromC(Acc (&acc)[kT], const uint32_t* c, uint32_t m,
+                                         uint32_t n, At at) {
+  bool unsafe = false;
+#pragma unroll
+  for (int j = 0; j < kT; ++j) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      uint32_t row, col;
+      at(j, r, row, col);
+      acc[j][r] = __uint_as_float(c[row < m && col < n ? (size_t)row * n + col : 0]);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      uint32_t row, col;
+      at(j, r, row, col);
+      const uint32_t v = row < m && col < n ? __float_as_uint(acc[j][r]) : 0u;
+      acc[j][r] = __uint_as_float(v);
+      unsafe |= ExpField(v) > 252u;
+    }
+    __builtin_amdgcn_sched_barrier(0);  // one tile's loads in flight at a time
+  }
+  return unsafe;
+}
+
 }  // namespace hb

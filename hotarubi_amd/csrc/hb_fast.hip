@@ -346,11 +346,14 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
   constexpr int kWLoads = 512 * F::kWPlanes / kP;
   constexpr int kU = F::kU, kTM = F::kTM, kTN = F::kTN, kWP = F::kWPlanes;
   constexpr int kWavesM = kMT / kTM;  // consumer waves: kWavesM (rows) x 8 / kTN (columns)
+  // waves that run the epilogue: the 2 * kMT producers that convert A (all
+  // producers at 128-row tiles) and the consumers
+  constexpr uint32_t kWaves = 2 * kMT + kBM * 4 / 64;
   static_assert(kWavesM * (8 / kTN) * 64 == kBM * 4 && kTM * kTN == 4, "consumer wave grid");
   static_assert(kU >= 3, "LDS stages");
   __shared__ __attribute__((aligned(16))) Lds<kMT, kW8> lds;
   __shared__ uint64_t lds_act[512];             // activation half of TBUF
-  __shared__ float lds_vec[kMaxOps][kBN];         // the tile's columns of each op vector
+  __shared__ __attribute__((aligned(16))) float lds_vec[kMaxOps][kBN];  // tile's op columns
   __shared__ uint32_t lds_unsafe;
 
   const TileId tile = LogicalTile(g.gx, g.gy, g.gz);
@@ -375,105 +378,113 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
   const uint32_t s0 = split * g.split_steps;  // every split has at least one step
   const uint32_t steps = g.splits > 1 ? min(all_steps - s0, g.split_steps) : all_steps;
 
-  // The epilogue runs from LDS on all 16 waves: the kMT*2 consumer waves'
-  // outputs are at lds.out[cw][e][lane], element e = 16 j + r of MFMA tile j
-  // (row tile j / kTN, column tile j % kTN of wave cw), register r.  Waves
-  // take whole tiles (e0, e1 multiples of 16), so a row's 32 columns of a
-  // tile are the 32 lanes of one half-wave for the requantize.
-  auto epilogue = [&](uint32_t cw, uint32_t l, uint32_t e0, uint32_t e1, bool slow) {
-    const uint32_t cwm = cw % kWavesM, cwn = cw / kWavesM;
-    float* vals = lds.out[cw];
-    auto row_at = [&](uint32_t e) {
-      const uint32_t j = e / 16, r = e % 16;
-      return row0 + (cwm * kTM + j / kTN) * 32 + 4 * (l >> 5) + 8 * (r / 4) + (r & 3);
-    };
-    auto col_at = [&](uint32_t e) { return col0 + (cwn * kTN + (e / 16) % kTN) * 32 + (l & 31); };
-    if (g.splits <= 1 && slow) {
-      for (uint32_t e = e0; e < e1; ++e) {
-        const uint32_t row = row_at(e), col = col_at(e);
-        if ((row >> 2) >= g.quads || col >= g.n) continue;
-        const uint32_t init = (g.acc && row < g.m) ? c[(size_t)row * g.n + col] : 0u;
-        vals[e * 64 + l] = __uint_as_float(SlowLinear(g, a, w0, w1, init, row, col));
+  // The epilogue runs from LDS on kWaves waves of the workgroup: the
+  // consumer waves' outputs are at lds.out[cw][e][lane], element e = 16 j +
+  // r of MFMA tile j (row tile j / kTN, column tile j % kTN of wave cw),
+  // register r.  The unit of work is half an MFMA tile (16 rows x 32
+  // columns); the units inside the output (rows below 4 * quads, columns
+  // below n) are dealt round-robin over the waves, so a narrow layer's few
+  // live columns spread over every wave.  In a unit, lane l takes columns
+  // 4 (l % 8) .. + 3 of rows l / 8 and l / 8 + 8 (n is a multiple of 8, so
+  // 4 columns are in or out together): 16-byte LDS reads, C stores and
+  // operand loads, and a row's 32-column block is the 8 lanes 8 p .. 8 p + 7
+  // (its largest exponent field in 3 swizzles, one 4-byte store of codes
+  // per lane and row).
+  auto epilogue = [&](uint32_t wv, uint32_t l, bool slow) __attribute__((always_inline)) {
+    const uint32_t rows4 = g.quads * 4;
+    const uint32_t nrt = min((uint32_t)kMT, (rows4 - min(row0, rows4) + 31) / 32);
+    const uint32_t nct = min((uint32_t)(kBN / 32), (g.n - min(col0, g.n) + 31) / 32);
+    const uint32_t units = nrt * nct * 2;
+    const uint32_t rr = l >> 3, cc = 4 * (l & 7);
+    const bool c16 = (reinterpret_cast<uintptr_t>(c) & 15u) == 0;  // uniform
+    for (uint32_t u = wv; u < units; u += kWaves) {
+      const uint32_t half = u & 1, ct = (u >> 1) % nct, rt = (u >> 1) / nct;
+      const uint32_t cw = rt / kTM + kWavesM * (ct / kTN), j = (rt % kTM) * kTN + ct % kTN;
+      const uint32_t row_a = row0 + rt * 32 + 16 * half + rr, col = col0 + ct * 32 + cc;
+      // tile rows 16 half + rr and + 8: registers (rr & 3) + 8 half and + 4,
+      // half-wave rr / 4 of the accumulator layout
+      float* src = lds.out[cw] + (j * 16 + (rr & 3) + 8 * half) * 64 + 32 * (rr >> 2) + cc;
+      const bool col_in = col < g.n;
+      if (g.splits <= 1 && slow) {  // the lane's 8 outputs exactly, in place in LDS
+        for (uint32_t t = 0; t < 8; ++t) {
+          const uint32_t row = row_a + 8 * (t >> 2), k = t & 3;
+          if (row >= rows4 || !col_in) continue;
+          const uint32_t init = (g.acc && row < g.m) ? c[(size_t)row * g.n + col + k] : 0u;
+          src[(t >> 2) * 4 * 64 + k] = __uint_as_float(SlowLinear(g, a, w0, w1, init, row, col + k));
+        }
       }
-    }
-    if (g.ws != nullptr) {  // deferred epilogue: this split's sums, rows [0, 4*quads)
-      float* out = g.ws + (size_t)split * g.quads * 4 * g.n;
-      for (uint32_t e = e0; e < e1; ++e) {
-        const uint32_t row = row_at(e), col = col_at(e);
-        if ((row >> 2) < g.quads && col < g.n) out[(size_t)row * g.n + col] = vals[e * 64 + l];
-      }
-      return;
-    }
-    if (g.n_ops == 0 && q_out == nullptr) {  // plain C: a rolled loop, few registers
-      for (uint32_t e = e0; e < e1; ++e) {
-        const uint32_t row = row_at(e), col = col_at(e);
-        if (row < g.m && col < g.n) c[(size_t)row * g.n + col] = __float_as_uint(vals[e * 64 + l]);
-      }
-      return;
-    }
-    // Ops (FP32 hardware arithmetic), C and requantize, half an MFMA tile
-    // (8 of a lane's 16 values) at a time, all in registers: the values and
-    // each op's operands are loaded at once (independent loads, one wait),
-    // and each op is a straight run over the 8 values.  (Whole tiles of 16
-    // with their 16 operands spilled to scratch at 128 registers.)
-    for (uint32_t t0 = e0; t0 < e1; t0 += 8) {
-      // Output r of the tile is row row_l + RowStep(r), column col; this
-      // half's registers are r0 .. r0 + 7 (r0 = 0 or 8), rows row_h +
-      // RowStep(i), i < 8 (RowStep(r0 + i) = 2 r0 + RowStep(i)).  The row
-      // step is uniform, so each access is a uniform base plus one per-lane
-      // 32-bit offset (no per-row 64-bit addresses to keep live).
-      const uint32_t tb = t0 & ~15u, r0 = t0 & 15u;
-      const uint32_t col = col_at(tb), row_h = row_at(tb) + 2 * r0;
-      const uint32_t off_l = row_h * g.n + col;
-      auto row_step = [](int r) { return (uint32_t)(8 * (r / 4) + (r & 3)); };
-      f32x8 y;
+      f32x4_t y[2] = {*reinterpret_cast<const f32x4_t*>(src),
+                      *reinterpret_cast<const f32x4_t*>(src + 4 * 64)};
+      if (g.ws != nullptr) {  // deferred epilogue: this split's sums, rows [0, 4*quads)
+        float* out = g.ws + (size_t)split * rows4 * g.n;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = vals[(t0 + i) * 64 + l];
+        for (int i = 0; i < 2; ++i) {
+          const uint32_t row = row_a + 8 * i;
+          if (row < rows4 && col_in)
+            *reinterpret_cast<f32x4_t*>(out + (size_t)row * g.n + col) = y[i];
+        }
+        continue;
+      }
       for (uint32_t o = 0; o < g.n_ops; ++o) {
         const uint32_t kind = g.op_kind[o];
-        f32x8 x2 = {};
-        float p = 0.0f;
+        f32x4_t p = {}, x2[2] = {};
         if (kind == kEpAdd || kind == kEpActMul) {
-          const uint32_t* src = g.op_x2[o] + z * g.op_x2_batch[o];
+          const uint32_t* src2 = g.op_x2[o] + z * g.op_x2_batch[o];
+          const bool x16 = (reinterpret_cast<uintptr_t>(src2) & 15u) == 0;  // uniform
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const uint32_t* src_r = src + row_step(i) * g.n;  // uniform
-            x2[i] = __uint_as_float(row_h + row_step(i) < g.m && col < g.n ? src_r[off_l] : 0u);
+          for (int i = 0; i < 2; ++i) {
+            const uint32_t row = row_a + 8 * i;
+            if (row >= g.m || !col_in) continue;
+            const uint32_t* xv = src2 + (size_t)row * g.n + col;
+            if (x16) {
+              x2[i] = *reinterpret_cast<const f32x4_t*>(xv);
+            } else {
+#pragma unroll
+              for (int k = 0; k < 4; ++k) x2[i][k] = __uint_as_float(xv[k]);
+            }
           }
         } else if (kind == kEpAddP || kind == kEpMulP) {
-          p = lds_vec[o][col - col0];
+          p = *reinterpret_cast<const f32x4_t*>(&lds_vec[o][col - col0]);
         }
-        EpApplyFastN(kind, g.op_imm[o], y, x2, p, lds_act);
-      }
-      if (g.c != nullptr) {  // uniform
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          uint32_t* c_r = c + row_step(i) * g.n;  // uniform
-          if (row_h + row_step(i) < g.m && col < g.n) c_r[off_l] = __float_as_uint(y[i]);
+        for (int i = 0; i < 2; ++i) EpApplyFastN<false>(kind, g.op_imm[o], y[i], x2[i], p, lds_act);
+      }
+      if (c != nullptr) {  // uniform
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const uint32_t row = row_a + 8 * i;
+          if (row >= g.m || !col_in) continue;
+          uint32_t* cv = c + (size_t)row * g.n + col;
+          if (c16) {
+            *reinterpret_cast<f32x4_t*>(cv) = y[i];
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) cv[k] = __float_as_uint(y[i][k]);
+          }
         }
       }
-      if (q_out != nullptr) {  // MXINT8 requantize over the 32 lanes holding a row's block
-        // Values i < 4 are rows row_h .. row_h + 3, i >= 4 rows row_h + 8 ..
-        // row_h + 11 (row_h is a multiple of 4): quads row_h / 4 and
-        // row_h / 4 + 2, one DDR word each.  Per word: the 4 block maxima
-        // (their lane moves overlap), one bounds check and address, the 4
-        // rows' codes, then lanes 0..15 write bytes 128..143 (the 4 scale
-        // bytes, 12 zero bytes) with one store.
-        const uint32_t nb = g.n >> 5, blk = (col - (l & 31)) >> 5, c32 = l & 31;
+      if (q_out != nullptr) {  // MXINT8 requantize: a row's block is 8 lanes
+        const uint32_t nb = g.n >> 5;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          uint32_t x[4];
+        for (int i = 0; i < 2; ++i) {
+          const uint32_t row = row_a + 8 * i;
+          uint32_t e = 0;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) x[r] = HalfMax32(ExpField(__float_as_uint(y[4 * h + r])));
-          const uint32_t quad = (row_h >> 2) + 2 * h;
-          if (quad < g.quads && blk < nb) {
-            uint8_t* word = q_out + ((size_t)quad * nb + blk) * kDdrWord;
+          for (int k = 0; k < 4; ++k) e = max(e, ExpField(__float_as_uint(y[i][k])));
+          e = max(e, (uint32_t)__builtin_amdgcn_ds_swizzle((int)e, 0x041F));  // xor 1
+          e = max(e, (uint32_t)__builtin_amdgcn_ds_swizzle((int)e, 0x081F));  // xor 2
+          e = max(e, (uint32_t)__builtin_amdgcn_ds_swizzle((int)e, 0x101F));  // xor 4
+          if (row >= rows4 || !col_in) continue;
+          uint8_t* word = q_out + ((size_t)(row >> 2) * nb + (col >> 5)) * kDdrWord;
+          uint32_t codes = 0;
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              word[r * 32 + c32] = QuantizeElementHw(__float_as_uint(y[4 * h + r]), x[r]);
-            const uint32_t sb = ScaleByteOf(x[0]) | ScaleByteOf(x[1]) << 8 |
-                               ScaleByteOf(x[2]) << 16 | ScaleByteOf(x[3]) << 24;
-            if (c32 < 16) word[128 + c32] = c32 < 4 ? (uint8_t)(sb >> (8 * c32)) : 0;
+          for (int k = 0; k < 4; ++k)
+            codes |= (uint32_t)QuantizeElementHw(__float_as_uint(y[i][k]), e) << (8 * k);
+          *reinterpret_cast<uint32_t*>(word + (row & 3) * 32 + cc) = codes;  // (q_out 4-aligned)
+          if ((l & 7) == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(e);
+          if ((l & 7) == 1 && (row & 3) == 0) {  // bytes 132 .. 143 of the word are zero
+            uint32_t* pad = reinterpret_cast<uint32_t*>(word + 132);
+            pad[0] = pad[1] = pad[2] = 0u;
           }
         }
       }
@@ -543,8 +554,7 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
     if (unsafe) lds_unsafe = 1;
     __syncthreads();
     __syncthreads();  // the consumers' outputs are in LDS
-    // producer wave v < 2 * kMT takes tiles 2 and 3 of consumer wave v
-    if (kAWave) epilogue(t >> 6, t & 63, 32, 64, lds_unsafe != 0);
+    if (kAWave) epilogue(t >> 6, t & 63, lds_unsafe != 0);
   };
   if (!consumer) {
     if constexpr (kMT * 2 == kP / 64) {
@@ -566,18 +576,30 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
   auto col_of = [&](uint32_t j) { return col0 + (wn * kTN + j % kTN) * 32 + (lane & 31); };
   f32x16 acc[4];
   bool unsafe = false;
+  if constexpr (!kW8) {
+    if (g.acc && split == 0) {  // uniform: start from C
+      unsafe = AccFromC(acc, c, g.m, g.n, [&](uint32_t j, uint32_t r, uint32_t& row, uint32_t& col) {
+        row = row_of(j, r);
+        col = col_of(j);
+      });
+    } else {
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const uint32_t row = row_of(j, r), col = col_of(j);
-      uint32_t init = 0;
-      if (g.acc && split == 0 && row < g.m && col < g.n) {
-        init = c[(size_t)row * g.n + col];
-        unsafe |= ExpField(init) > 252u;
-      }
-      acc[j][r] = __uint_as_float(init);
+      for (int j = 0; j < 4; ++j) acc[j] = f32x16{};
     }
+  } else {  // (the W8 consumer keeps a per-element branch: its K loop spills more without)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t row = row_of(j, r), col = col_of(j);
+        uint32_t init = 0;
+        if (g.acc && split == 0 && row < g.m && col < g.n) {
+          init = c[(size_t)row * g.n + col];
+          unsafe |= ExpField(init) > 252u;
+        }
+        acc[j][r] = __uint_as_float(init);
+      }
+  }
   if (unsafe) lds_unsafe = 1;
 
   // One step's operands in registers: the wave's A tiles (both planes) and
@@ -698,7 +720,7 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
   if (g.splits > 1 && tid == 0)
     SplitFlags(g)[(split * g.gy + tile.y) * g.gx + tile.x] = slow ? 1u : 0u;
   __syncthreads();  // the outputs are in LDS
-  epilogue(wave, lane, 0, 32, slow);  // tiles 0 and 1 of this wave
+  epilogue(2 * kMT + wave, lane, slow);
 }
 
 template <int kBM, bool kMulti, bool kW8>

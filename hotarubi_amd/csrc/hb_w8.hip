@@ -125,19 +125,12 @@ void W8Kernel(GemmArgs g) {
     // Initial accumulators: +0, or C (before any load into LDS is issued:
     // the compiler's waits for these loads then count nothing else).
     if (g.acc) {
-#pragma unroll
-      for (int j = 0; j < kNT; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const uint32_t row = row_w + 4 * (lane >> 5) + 8 * (e / 4) + (e & 3);
-          const uint32_t col = col0 + j * 32 + (lane & 31);
-          uint32_t init = 0;
-          if (row < g.m && col < g.n) {
-            init = c[(size_t)row * g.n + col];
-            bad |= ExpField(init) > 252u ? 1u : 0u;
-          }
-          acc[j][e] = __uint_as_float(init);
-        }
+      const bool unsafe =
+          AccFromC(acc, c, g.m, g.n, [&](uint32_t j, uint32_t e, uint32_t& row, uint32_t& col) {
+            row = row_w + 4 * (lane >> 5) + 8 * (e / 4) + (e & 3);
+            col = col0 + j * 32 + (lane & 31);
+          });
+      bad |= unsafe ? 1u : 0u;
     } else {
 #pragma unroll
       for (int j = 0; j < kNT; ++j) acc[j] = f32x16{};

@@ -228,7 +228,9 @@ enum { HB_MAX_PIECES = 16, HB_MAX_EP_OPS = 8, HB_MAX_GROUP = 4 };
  *   w[l]    device, DDR words [n/8][kb_total] x 144 B (PackWbuf) per plane
  *   modes[l] 0 FP4 (E2M1), 1 W8_HI, 2 W8_LO; a W8 layer is 2 planes {1, 2}
  *   c       device, fp32 row-major [m][n]; read if onto, always written
+ *           (4-byte aligned)
  *   q_out   device or NULL, MXINT8 DDR words [ceil(m/4)][n/32] x 144 B
+ *           (4-byte aligned)
  *   tbuf    device, 1024 TBUF entries (needed for HB_EP_ACT*)
  * n % 8 == 0 (n % 32 == 0 with q_out); rows of the last quad beyond m are
  * computed from A's rows as given but not stored in c. */

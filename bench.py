@@ -962,8 +962,9 @@ def time_chain(torch, ctx, work, steps=10, graph=True):
 def time_expert_step(hb, torch, ctx, batch, mode, steps=10):
     """Milliseconds per SmolVLA action-expert step (eager and graph), with
     its roofline over the best of the two."""
-    work = ExpertStep(hb, torch, batch, mode)
-    out = {"batch": batch, **time_chain(torch, ctx, work, steps)}
+    work = ExpertStep(hb, torch, batch, mode, panels=mode == hb.FAST)
+    out = {"batch": batch, "weights": "panels" if mode == hb.FAST else "DDR words",
+           **time_chain(torch, ctx, work, steps)}
     best = min(out["eager_ms"], out.get("graph_ms", out["eager_ms"]))
     out["tops"], out["roofline"] = chain_summary(
         work, best, "fp6_fp4", f"expert_b{batch}" if mode == hb.FAST else None)
@@ -1121,8 +1122,8 @@ def bench_lines(hb, torch, ctx):
                      wl(128, n, kb, False, 256, F, seed=5, panels=True, a_fp8=True)),
         "fp8_m1024": ("MXFP8 x MXFP4 M=1024 K=2560 N=960 x64 layers, fast, weights in panels",
                       wl(1024, n, kb, False, 64, F, seed=5, panels=True, a_fp8=True)),
-        "w8_fast": ("W8 M=64 K=960 N=2560 + MULP + ADDP x128 layers, fast",
-                    wl(64, 2560, 30, True, 128, F, epilogue=True, seed=4)),
+        "w8_fast": ("W8 M=64 K=960 N=2560 + MULP + ADDP x128 layers, fast, planes in panels",
+                    wl(64, 2560, 30, True, 128, F, epilogue=True, seed=4, panels=True)),
         "w8_exact": ("W8 M=64 K=960 N=2560 + MULP + ADDP x128 layers, exact",
                      wl(64, 2560, 30, True, 128, E, epilogue=True, seed=4)),
         "siglip_fast": ("SigLIP-style W8 set, 12 layers x 4 GEMMs, M=2048, fast, W8 panels",
@@ -1130,15 +1131,15 @@ def bench_lines(hb, torch, ctx):
         "siglip_exact": ("SigLIP-style W8 set, 12 layers x 4 GEMMs, M=2048, exact, DDR words",
                          lambda: ChainLine(SiglipSet(hb, torch, E))),
         "sparsedrive_fast": ("SparseDrive-S stage-1 im2col M=67584 K=576 N=64, MXFP4, fast",
-                             lambda: ChainLine(SparseDriveConv(hb, torch, F))),
+                             lambda: ChainLine(SparseDriveConv(hb, torch, F, panels=True))),
         "sparsedrive_exact": ("SparseDrive-S stage-1 im2col M=67584 K=576 N=64, MXFP4, exact",
                               lambda: ChainLine(SparseDriveConv(hb, torch, E))),
         "sparsedrive_head_f1": ("SparseDrive-S det head GEMMs, 6 blocks, 928 anchor rows (1 "
                                 "frame), W8 attention + MXFP4 FFN, fast",
-                                lambda: ChainLine(SparseDriveHead(hb, torch, 1, F))),
+                                lambda: ChainLine(SparseDriveHead(hb, torch, 1, F, panels=True))),
         "sparsedrive_head_f16": ("SparseDrive-S det head GEMMs, 6 blocks, 16 frames (14848 "
                                  "anchor rows), W8 attention + MXFP4 FFN, fast",
-                                 lambda: ChainLine(SparseDriveHead(hb, torch, 16, F))),
+                                 lambda: ChainLine(SparseDriveHead(hb, torch, 16, F, panels=True))),
         "backbone_f1": ("SparseDrive-S ResNet-50 backbone GEMM chain (stem + 16 bottlenecks, "
                         "49 GEMMs), 6 cameras, 1 frame, fast, weights in panels",
                         lambda: ChainLine(SparseDriveBackbone(hb, torch, 1, F))),
@@ -1146,13 +1147,13 @@ def bench_lines(hb, torch, ctx):
                          "49 GEMMs), 6 cameras, 16 frames, fast, weights in panels",
                          lambda: ChainLine(SparseDriveBackbone(hb, torch, 16, F))),
         "expert_b1": ("SmolVLA action-expert step GEMM chain, B=1 (M=50), fast, grouped",
-                      lambda: ChainLine(ExpertStep(hb, torch, 1, F))),
+                      lambda: ChainLine(ExpertStep(hb, torch, 1, F, panels=True))),
         "expert_b32": ("SmolVLA action-expert step GEMM chain, B=32 (M=1600), fast, grouped",
-                       lambda: ChainLine(ExpertStep(hb, torch, 32, F))),
+                       lambda: ChainLine(ExpertStep(hb, torch, 32, F, panels=True))),
         "prefix_b1": ("SmolVLA LM prefix GEMM chain, B=1 (M=141), fast, grouped",
-                      lambda: ChainLine(PrefixStep(hb, torch, 1, F))),
+                      lambda: ChainLine(PrefixStep(hb, torch, 1, F, panels=True))),
         "prefix_b32": ("SmolVLA LM prefix GEMM chain, B=32 (M=4512), fast, grouped",
-                       lambda: ChainLine(PrefixStep(hb, torch, 32, F))),
+                       lambda: ChainLine(PrefixStep(hb, torch, 32, F, panels=True))),
     }
 
 
@@ -1472,9 +1473,11 @@ def main():
         out["mxfp8_fast_m_sweep"] = sweep8
         # W8 layer with per-channel scale and bias, fast and exact
         L8 = 128
-        w8 = {"workload": f"W8 linear M=64 K=960 N=2560 + MULP + ADDP, {L8} layers per step"}
+        w8 = {"workload": f"W8 linear M=64 K=960 N=2560 + MULP + ADDP, {L8} layers per step; "
+                          "fast: each weight plane in panels, exact: DDR words"}
         for name, md, cls in (("fast", hb.FAST, "int8"), ("exact", hb.EXACT, "bf16")):
-            wk = Workload(hb, torch, ctx, 64, 2560, 30, True, L8, md, epilogue=True, seed=4)
+            wk = Workload(hb, torch, ctx, 64, 2560, 30, True, L8, md, epilogue=True, seed=4,
+                          panels=md == hb.FAST)
             ms8 = time_steps(hb, torch, ctx, stream, wk, extra_steps, extra_warm, settle_s=0.2)
             t8, r8 = summarize(wk, ms8, cls, f"w8_{name}")
             w8[name] = {"value": round(t8, 3), "unit": "TOPS", "ms_per_step": round(ms8, 4),
@@ -1493,14 +1496,16 @@ def main():
                  lambda md: SiglipSet(hb, torch, md, w8_panels=md == hb.FAST)),
                 ("sparsedrive_stage1_conv_mxfp4", "sparsedrive", "MXFP4 im2col GEMM M=67584 K=576 N=64 "
                  "(SparseDrive-S stage-1 3x3 conv, 6 cameras)", "fp6_fp4",
-                 lambda md: SparseDriveConv(hb, torch, md))):
+                 lambda md: SparseDriveConv(hb, torch, md, panels=md == hb.FAST))):
             rec = {}
             for name, md, cls in (("fast", hb.FAST, cls_fast), ("exact", hb.EXACT, "bf16")):
                 wk = make(md)
                 t = time_chain(torch, ctx, wk, steps=5, graph=False)
                 tops, roof = chain_summary(wk, t["eager_ms"], cls, f"{short}_{name}")
                 rec[name] = {"value": tops, "unit": "TOPS", "ms_per_pass": t["eager_ms"],
-                             "gemms": t["gemms"], "m": t["m"], "roofline": roof}
+                             "gemms": t["gemms"], "m": t["m"],
+                             "weights": ("W8 panels" if key == "siglip_w8_set" else "panels")
+                             if md == hb.FAST else "DDR words", "roofline": roof}
                 del wk
             if key == "siglip_w8_set":  # the fast set over DDR words, for comparison
                 wk = SiglipSet(hb, torch, hb.FAST)
@@ -1520,7 +1525,7 @@ def main():
         for frames, modes in ((1, (("fast", hb.FAST, "fp6_fp4"), ("exact", hb.EXACT, "bf16"))),
                               (16, (("fast", hb.FAST, "fp6_fp4"),))):
             for name, md, cls in modes:
-                wk = SparseDriveHead(hb, torch, frames, md)
+                wk = SparseDriveHead(hb, torch, frames, md, panels=md == hb.FAST)
                 t = time_chain(torch, ctx, wk, steps=5, graph=False)
                 tops, roof = chain_summary(wk, t["eager_ms"], cls,
                                            f"sparsedrive_head_f{frames}" if md == hb.FAST else None)
@@ -1528,6 +1533,8 @@ def main():
                 head[f"frames={frames}"][name] = {"value": tops, "unit": "TOPS",
                                                   "ms_per_pass": t["eager_ms"],
                                                   "gemms": t["gemms"], "m": t["m"],
+                                                  "weights": "panels" if md == hb.FAST
+                                                  else "DDR words",
                                                   "roofline": roof}
                 del wk
         out["sparsedrive_head"] = head
@@ -1563,11 +1570,12 @@ def main():
                               "(requantize), o 960 (+residual), up 2560, gate 2560 (ACT_MUL, "
                               "requantize), down 960 (+residual)}, MXFP4, 141 tokens per element"}
         for b in (1, 32):
-            wk = PrefixStep(hb, torch, b, mode)
+            wk = PrefixStep(hb, torch, b, mode, panels=fast)
             t = time_chain(torch, ctx, wk, steps=5)
             best = min(t["eager_ms"], t.get("graph_ms", t["eager_ms"]))
             tops, roof = chain_summary(wk, best, "fp6_fp4", f"prefix_b{b}" if fast else None)
-            prefix[f"B={b}"] = {**t, "tops": tops, "roofline": roof}
+            prefix[f"B={b}"] = {**t, "weights": "panels" if fast else "DDR words", "tops": tops,
+                                "roofline": roof}
             del wk
         ctx.set_stream(stream.cuda_stream)
         out["smolvla_prefix_ms"] = prefix

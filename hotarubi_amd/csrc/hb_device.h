@@ -404,4 +404,13 @@ __device__ __forceinline__ bool AccFromC(Acc (&acc)[kT], const uint32_t* c, uint
   return unsafe;
 }
 
+// The lane's index within its wave, read afresh where it is called: the
+// asm is opaque to the compiler, so lane-derived addresses computed from it
+// are not hoisted out of a loop to stay live (and spill) across its body.
+__device__ __forceinline__ uint32_t LaneNow() {
+  uint32_t l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 }  // namespace hb

@@ -395,7 +395,9 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
     const uint32_t nrt = min((uint32_t)kMT, (rows4 - min(row0, rows4) + 31) / 32);
     const uint32_t nct = min((uint32_t)(kBN / 32), (g.n - min(col0, g.n) + 31) / 32);
     const uint32_t units = nrt * nct * 2;
-    const uint32_t rr = l >> 3, cc = 4 * (l & 7);
+    (void)l;
+    const uint32_t ln = LaneNow();  // (held from the kernel's start, lane addresses spilled)
+    const uint32_t rr = ln >> 3, cc = 4 * (ln & 7);
     const bool c16 = (reinterpret_cast<uintptr_t>(c) & 15u) == 0;  // uniform
     for (uint32_t u = wv; u < units; u += kWaves) {
       const uint32_t half = u & 1, ct = (u >> 1) % nct, rt = (u >> 1) / nct;
@@ -481,8 +483,8 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
           for (int k = 0; k < 4; ++k)
             codes |= (uint32_t)QuantizeElementHw(__float_as_uint(y[i][k]), e) << (8 * k);
           *reinterpret_cast<uint32_t*>(word + (row & 3) * 32 + cc) = codes;  // (q_out 4-aligned)
-          if ((l & 7) == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(e);
-          if ((l & 7) == 1 && (row & 3) == 0) {  // bytes 132 .. 143 of the word are zero
+          if ((ln & 7) == 0) word[128 + (row & 3)] = (uint8_t)ScaleByteOf(e);
+          if ((ln & 7) == 1 && (row & 3) == 0) {  // bytes 132 .. 143 of the word are zero
             uint32_t* pad = reinterpret_cast<uint32_t*>(word + 132);
             pad[0] = pad[1] = pad[2] = 0u;
           }

@@ -426,9 +426,12 @@ __global__ __launch_bounds__(512) void Fp4Kernel(GemmArgs g) {
     // 4 (l % 8) .. of physical row l / 8 + 8 q.  LDS accesses of one wave
     // execute in order, so a wave-scope fence orders the lanes' accesses.
     // Adding +0 maps -0 to +0 (and a denormal sum, in the kernel's
-    // flush-to-zero mode, to +0).
+    // flush-to-zero mode, to +0).  (The lane index is read again here: held
+    // over the K loop, its addresses spilled.)
+    const uint32_t ln = LaneNow();
     Unroll<8>([&](auto jj) {
       constexpr int kJ = decltype(jj)::value;
+      const uint32_t lane = ln;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const uint32_t row = 8 * (r / 4) + 4 * (lane >> 5) + (r & 3);

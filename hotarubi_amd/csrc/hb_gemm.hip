@@ -805,12 +805,18 @@ hipError_t LaunchLinear(const GemmArgs& in, uint32_t batch, bool fast, Workspace
     return LaunchSplitLinear(args, stream);
   }
   args.fast_ep = fastk ? 1u : 0u;
-  // Over panels the streaming kernel takes plain layers.  Layers with ops
-  // or the requantize stay on the tile kernel: its epilogue runs on 16
-  // waves per CU, the streaming kernel's on 4 (measured on the SparseDrive
-  // backbone's layers, e.g. 67,584 x 256 x 128 with bias, ReLU and the
-  // requantize: 55 against 139 us).
-  if (fastk && !small && StreamEligible(args)) return LaunchStream(args, batch, stream);
+  // Over panels the streaming kernel takes plain batched layers (and
+  // MXFP8); a plain single layer takes the panel kernel, whose 8 waves per
+  // CU hide more latency where a workgroup has one or two tiles (measured,
+  // one layer per launch: 1,600 x 2,048 x 736 24.0 -> 16.9 us, 4,512 x
+  // 2,560 x 960 48.7 -> 36.2 us, 14,848 x 256 x 1,024 26.6 -> 18.6 us,
+  // 67,584 x 64 x 576 47.5 -> 40.9 us).  Layers with ops or the requantize
+  // stay on the tile kernel: its epilogue runs on 16 waves per CU, the
+  // streaming kernel's on 4 (measured on the SparseDrive backbone's layers,
+  // e.g. 67,584 x 256 x 128 with bias, ReLU and the requantize: 55 against
+  // 139 us).
+  if (fastk && !small && StreamEligible(args) && (batch > 1 || args.a_fp8))
+    return LaunchStream(args, batch, stream);
   if (fastk && !small && PanelEligible(args)) return LaunchPanel(args, batch, stream);
   if (small && fastk) {
     // as many splits as fit in one round of kTargetWorkgroups workgroups

@@ -380,9 +380,12 @@ __global__ __launch_bounds__(512) void PanelKernel(GemmArgs g) {
     }
     // Each MFMA tile through the wave's LDS block, stored as 16-byte rows
     // of 4 columns (rows at row ^ ((row >> 2) & 1): conflict-free writes and
-    // reads); +0 maps -0 (and a flushed denormal) to +0.
+    // reads); +0 maps -0 (and a flushed denormal) to +0.  (The lane index is
+    // read again here: held over the K loop, its addresses spilled.)
+    const uint32_t ln = LaneNow();
     Unroll<8>([&](auto jj) {
       constexpr int kJ = decltype(jj)::value;
+      const uint32_t lane = ln;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const uint32_t row = 8 * (r / 4) + 4 * (lane >> 5) + (r & 3);

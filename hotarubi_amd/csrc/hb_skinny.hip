@@ -37,16 +37,17 @@ constexpr uint32_t kSafeLo = 70, kSafeHi = 179;
 
 // Columns per workgroup: 16 * kNT, with the accumulators (kMT * kNT * 4) and
 // two chunks of raw loads within the registers of a wave.  MXFP4 at 16 rows
-// keeps to 128 registers (WavesPerSimd 4), so two workgroups share a CU and
-// one's reduction and epilogue overlap the other's loads; the others take up
-// to 256 (one workgroup per CU).
+// of one piece keeps to 128 registers (WavesPerSimd 4), so two workgroups
+// share a CU and one's reduction and epilogue overlap the other's loads; the
+// others take up to 256 (one workgroup per CU: several pieces' block lookup
+// spilled to scratch at 128).
 template <int kMT, bool kW8>
 constexpr int NTiles() {
   return kW8 ? (kMT == 4 ? 2 : 4) : 4;
 }
-template <int kMT, bool kW8>
+template <int kMT, bool kW8, bool kMulti>
 constexpr int WavesPerSimd() {
-  return kMT == 1 && !kW8 ? 4 : 2;
+  return kMT == 1 && !kW8 && !kMulti ? 4 : 2;
 }
 
 template <bool kMulti>
@@ -138,7 +139,7 @@ struct RawS {
 };
 
 template <int kMT, bool kW8, bool kMulti, bool kPanels>
-__global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8>())) void SkinnyKernel(GemmArgs g) {
+__global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8, kMulti>())) void SkinnyKernel(GemmArgs g) {
   constexpr int kNT = NTiles<kMT, kW8>(), kCols = 16 * kNT, kWP = kW8 ? 2 : 1;
   constexpr int kRows = 16 * kMT, kOut = kRows * kCols;
   __shared__ float lds_part[kWaves][kOut];  // the waves' partial sums

@@ -988,7 +988,7 @@ int hb_linear_group_async(hb_ctx* ctx, const hb_linear_desc* d, uint32_t count) 
   uint32_t cap1 = hb::kMaxSplitWaves, cap2 = hb::kMaxSplitWaves / 2, waves = 1, end = 0;
   const uint64_t cus = (uint64_t)hb::DeviceCus();
   for (;;) {
-    waves = 1;
+    waves = hb::kSplitFinishWaves;
     end = 0;
     for (uint32_t i = 0; i < count; ++i) {
       if (second[i]) continue;

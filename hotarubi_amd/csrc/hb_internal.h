@@ -306,6 +306,10 @@ bool SplitEligible(const GemmArgs& args, uint32_t batch);
 // splits of at least 4 steps, at most max_splits, one wave each) and the
 // workspace bytes it needs past the counters (0: no partials).
 constexpr uint32_t kMaxSplitWaves = 8;
+// Waves a split workgroup has at least: the epilogue's 4 row groups of a
+// 32 x 32 tile go to 4 finishers, one each, also where K has fewer splits
+// (the waves past the splits fold nothing).
+constexpr uint32_t kSplitFinishWaves = 4;
 size_t SplitPlan(GemmArgs& args, uint32_t max_splits = kMaxSplitWaves);
 hipError_t LaunchSplitLinear(const GemmArgs& args, hipStream_t stream);
 // Up to kMaxGroup single-launch split layers (args from SplitPlan, one

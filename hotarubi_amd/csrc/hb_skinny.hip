@@ -17,6 +17,7 @@
 // byte is converted twice in a workgroup.  The waves' partial sums are then
 // added in wave order through LDS, and the epilogue (ops in FP32 hardware
 // arithmetic, C, requantize) runs over the workgroup's outputs.
+#include <algorithm>
 #include <utility>
 
 #include "hb_device.h"
@@ -794,7 +795,7 @@ size_t SplitPlan(GemmArgs& args, uint32_t max_splits) {
 }
 
 hipError_t LaunchSplitLinear(const GemmArgs& args, hipStream_t stream) {
-  const dim3 grid(args.gx * args.gy), block(64 * args.splits);
+  const dim3 grid(args.gx * args.gy), block(64 * std::max(args.splits, kSplitFinishWaves));
   const bool w8 = args.n_planes == 2, multi = args.n_pieces > 1;
   if (w8) {
     if (multi) hipLaunchKernelGGL((SplitKernel<true, true>), grid, block, 0, stream, args);

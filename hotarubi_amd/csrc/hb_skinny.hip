@@ -600,23 +600,39 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
   bool slow = __builtin_amdgcn_ballot_w64(unsafe) != 0;
   f32x16 sum = acc;
   if (blockDim.x > 64) {  // the partials meet in LDS; each finisher adds its groups' in split order
+    // A split's partials as [group j][lane] 16-byte slots (values 4 j ..
+    // 4 j + 3): one conflict-free access per group.  A finisher reads every
+    // split's slot of its group at once (splits past the layer's read the
+    // last one's, not added), then adds them in split order.
+    f32x4_t* const part = reinterpret_cast<f32x4_t*>(&lds_part[0][0]);
     if (split < g.splits) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) lds_part[split][e * 64 + lane] = acc[e];
+      for (int j = 0; j < 4; ++j)
+        part[(split * 4 + j) * 64 + lane] =
+            f32x4_t{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]};
       if (lane == 0) lds_flag[split] = slow ? 1u : 0u;
     }
     __syncthreads();
     if (own) {
+      slow = false;
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        if (owns(e)) sum[e] = lds_part[0][e * 64 + lane];
-      slow = lds_flag[0] != 0;
-      for (uint32_t s = 1; s < g.splits; ++s) {
+      for (uint32_t s = 0; s < kMaxSplitWaves; ++s)
+        slow |= s < g.splits && lds_flag[min(s, g.splits - 1)] != 0;
+      UnrollS([&](auto j_c) {
+        constexpr int j = decltype(j_c)::value;
+        if ((own >> j) & 1u) {  // uniform
+          f32x4_t p[kMaxSplitWaves];
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if (owns(e)) sum[e] += lds_part[s][e * 64 + lane];
-        slow |= lds_flag[s] != 0;
-      }
+          for (uint32_t s = 0; s < kMaxSplitWaves; ++s)
+            p[s] = part[(min(s, g.splits - 1) * 4 + j) * 64 + lane];
+          f32x4_t t = p[0];
+#pragma unroll
+          for (uint32_t s = 1; s < kMaxSplitWaves; ++s)
+            if (s < g.splits) t += p[s];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sum[4 * j + i] = t[i];
+        }
+      }, std::make_integer_sequence<int, 4>{});
     }
   }
   const uint64_t* act = g.tbuf != nullptr ? g.tbuf + 512 : nullptr;
@@ -709,7 +725,7 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
 
 template <bool kW8, bool kMulti, bool kA8 = false>
 __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
-  __shared__ float lds_part[kMaxSplitWaves][16 * 64];
+  __shared__ __attribute__((aligned(16))) float lds_part[kMaxSplitWaves][16 * 64];
   __shared__ uint32_t lds_flag[kMaxSplitWaves];
   TouchArgs(&g, sizeof g);
   SplitTile<kW8, kMulti, kA8>(g, XcdLogical(blockIdx.x, gridDim.x),
@@ -725,7 +741,7 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
 // first's values reach the second's finisher through LDS.
 template <bool kW8, bool kMulti>
 __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitGroupKernel(SplitGroup grp) {
-  __shared__ float lds_part[kMaxSplitWaves][16 * 64];
+  __shared__ __attribute__((aligned(16))) float lds_part[kMaxSplitWaves][16 * 64];
   __shared__ float lds_y[16 * 64];
   __shared__ uint32_t lds_flag[kMaxSplitWaves];
   TouchArgs(&grp.units, sizeof grp - offsetof(SplitGroup, units));

@@ -618,19 +618,24 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
   const uint32_t* sa_base = &lds.sa[0][wm][lane];
   const uint32_t* sw_base = &lds.sw[0][wn][lane];
   constexpr int kSaStage = kMT / kTM * 64, kSwStage = 8 / kTN * 64;  // in dwords
-  auto read = [&](int st, Operands& op) {
+  // A plane p of stage st into slot q of every m-tile
+  auto read_a = [&](int st, int p, int q, Operands& op) __attribute__((always_inline)) {
 #pragma unroll
-    for (int mi = 0; mi < kTM; ++mi)
+    for (int mi = 0; mi < kTM; ++mi) {
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-          const uint2 v = a_base[st * kAStage + p * kAPlane + (mi * 3 + i) * 64];
-          op.a[mi][p][2 * i] = (int)v.x;
-          op.a[mi][p][2 * i + 1] = (int)v.y;
-        }
-        op.a[mi][p][6] = op.a[mi][p][7] = 0;
+      for (int i = 0; i < 3; ++i) {
+        const uint2 v = a_base[st * kAStage + p * kAPlane + (mi * 3 + i) * 64];
+        op.a[mi][q][2 * i] = (int)v.x;
+        op.a[mi][q][2 * i + 1] = (int)v.y;
       }
+      op.a[mi][q][6] = op.a[mi][q][7] = 0;
+    }
+  };
+  // A (both planes, or for W8 plane 0 only: plane 1 follows mid-step), W
+  // and the scales of stage st
+  auto read = [&](int st, Operands& op) {
+    read_a(st, 0, 0, op);
+    if constexpr (!kW8) read_a(st, 1, 1, op);
     op.sa = (int)sa_base[st * kSaStage];
     op.sb = (int)sw_base[st * kSwStage];
     if constexpr (kW8) {
@@ -671,16 +676,28 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
           op.a[kMi][kPa], op.b[kNj][kPb], acc[kJ], 2, F::kBFormat, kMi * 2 + kPa, op.sa,
           kNj * kWP + kPb, op.sb);
     };
-    if constexpr (kW8) {  // the four plane products, each over the 4 tiles
-      Unroll<2>([&](auto pa) {
-        Unroll<2>([&](auto pb) { Unroll<4>([&](auto j) { mfma(j, pa, pb); }); });
-      });
+    (void)mfma;
+    if constexpr (kW8) {  // (W8 issues its two A planes' products separately, below)
     } else {
       Unroll<4>([&](auto j) {
         mfma(j, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
         mfma(j, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
       });
     }
+  };
+  // W8: the products of A plane kPa (held in slot 0) with both W planes,
+  // each over the 4 tiles; the scale byte still picks plane kPa's
+  auto w8_plane = [&](const Operands& op, auto pa) __attribute__((always_inline)) {
+    constexpr int kPa = decltype(pa)::value;
+    Unroll<2>([&](auto pb) {
+      Unroll<4>([&](auto j) {
+        constexpr int kJ = decltype(j)::value, kPb = decltype(pb)::value;
+        constexpr int kMi = kJ / kTN, kNj = kJ % kTN;
+        acc[kJ] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            op.a[kMi][0], op.b[kNj][kPb], acc[kJ], 2, F::kBFormat, kMi * 2 + kPa, op.sa,
+            kNj * kWP + kPb, op.sb);
+      });
+    });
   };
   Operands ops;
   __syncthreads();  // steps 0 and 1 staged
@@ -689,7 +706,20 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < kU; ++i) {  // iteration step + i
       if (step + i >= steps) break;  // uniform; the producers stop at the same step
-      matrix(ops);
+      if constexpr (kW8) {
+        // A plane 0's products, then plane 1 read into the same registers
+        // (its LDS latency under plane 0's MFMAs), then plane 1's products:
+        // one A plane live at a time keeps the consumer within its 128
+        // registers (holding both spilled in the K loop)
+        w8_plane(ops, std::integral_constant<int, 0>{});
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(acc[j]));
+        __builtin_amdgcn_sched_barrier(0);
+        read_a(i % kU, 1, 0, ops);
+        w8_plane(ops, std::integral_constant<int, 1>{});
+      } else {
+        matrix(ops);
+      }
       // Anchor the step's matrix work here (the empty asm emits nothing):
       // left free, the compiler sinks the pure MFMA calls past later
       // barriers and keeps every step's operands live.  The fence keeps

@@ -405,8 +405,28 @@ typedef float f32x16s __attribute__((ext_vector_type(16)));
 // and after a second barrier the second layer's finishers read them from
 // x2_lds as op x2_op's [m][n] operand.  Every wave of the workgroup calls
 // this once (barriers).
+// What a wave needs to issue its first operand loads.  The single-layer
+// launch passes these as its leading kernel arguments, which the hardware
+// preloads into SGPRs (this file is compiled with kernel-argument preload),
+// so the loads go out before the argument block's round trip; a group
+// launch takes them from its GemmArgs.
+struct SplitHot {
+  const uint8_t* a;
+  const uint8_t* w0;
+  const uint8_t* w1;
+  uint32_t gy, quads, a_row, piece0, nblocks, split_steps, splits, w_row, groups, panels;
+};
+__device__ __forceinline__ SplitHot HotOf(const GemmArgs& g) {
+  uint32_t nblocks = 0;
+  for (uint32_t p = 0; p < g.n_pieces; ++p) nblocks += g.piece_kb[p];
+  return SplitHot{g.a, g.w[0], g.w[1], g.gy, g.quads, g.a_row, g.piece_off[0], nblocks,
+                  g.split_steps, g.splits, g.w_panels ? g.w_steps : g.kb_total, g.groups,
+                  g.w_panels};
+}
+
 template <bool kW8, bool kMulti, bool kA8 = false>
-__device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint32_t split,
+__device__ __forceinline__ void SplitTile(const GemmArgs& g, const SplitHot& h, bool touch,
+                                          uint32_t tile, uint32_t split,
                                           uint32_t nwaves, float (*lds_part)[16 * 64],
                                           uint32_t* lds_flag,
                                           bool pair, float* y_lds, const float* x2_lds,
@@ -416,28 +436,45 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
   const uint32_t lane = threadIdx.x & 63;
   // logical tiles run row tiles fastest: the workgroups of one column tile
   // (which read the same weights) are neighbours, on one XCD
-  const uint32_t col0 = (tile / g.gy) * 32, row0 = (tile % g.gy) * 32;
+  const uint32_t col0 = (tile / h.gy) * 32, row0 = (tile % h.gy) * 32;
   const uint32_t r32 = lane & 31, hb = lane >> 5;
-  const uint8_t* a = g.a;
-  const uint8_t* w0 = g.w[0];
-  const uint8_t* w1 = kW8 ? g.w[1] : w0;
+  const uint8_t* a = h.a;
+  const uint8_t* w0 = h.w0;
+  const uint8_t* w1 = kW8 ? h.w1 : w0;
 
-  uint32_t nblocks = 0;
-  for (uint32_t p = 0; p < g.n_pieces; ++p) nblocks += g.piece_kb[p];
+  const uint32_t nblocks = h.nblocks;
   const uint32_t steps = (nblocks + 1) / 2;
-  const uint32_t s_begin = split < g.splits ? split * g.split_steps : steps;
-  const uint32_t s_end = min(s_begin + g.split_steps, steps);
+  const uint32_t s_begin = split < h.splits ? split * h.split_steps : steps;
+  const uint32_t s_end = min(s_begin + h.split_steps, steps);
+  // a K block's word: one piece from piece0 on, or the piece list's
+  auto block_of = [&](uint32_t idx) {
+    return kMulti ? SkinnyBlockOf<true>(g, idx) : h.piece0 + idx;
+  };
 
   // the lane's A row and W column (a row or column past the layer reads
   // the last one's bytes; its outputs are not stored)
-  const uint32_t quad = min((row0 + r32) >> 2, g.quads - 1);
-  const uint32_t a_off = quad * g.a_row * kDdrWord + (r32 & 3) * 32;
+  const uint32_t quad = min((row0 + r32) >> 2, h.quads - 1);
+  const uint32_t a_off = quad * h.a_row * kDdrWord + (r32 & 3) * 32;
   const uint32_t ashift = 8 * (r32 & 3), as_delta = 128 - (r32 & 3) * 32;
-  const WLaneOff wo = WLane(g, min((col0 + r32) >> 3, g.groups - 1) * 8 + (r32 & 7));
+  WLaneOff wo;
+  {
+    const uint32_t col = min((col0 + r32) >> 3, h.groups - 1) * 8 + (r32 & 7);
+    if (h.panels) {  // (WLane with w_row = the panel's steps, or the DDR words' blocks)
+      const uint32_t base = (col / kPanelCols) * h.w_row * kPanelChunk, c = col % kPanelCols;
+      wo.codes = base + c * 16;
+      wo.scale = base + kPanelScales + 4 * ((c % 32) / 2);
+      wo.shift = 8 * (2 * (c % 2) + c / 32);
+    } else {
+      const uint32_t base = (col / 8) * h.w_row * kDdrWord, cl = col % 8;
+      wo.codes = base + cl * 16;
+      wo.scale = base + 128 + (cl & 4);
+      wo.shift = 8 * (cl & 3);
+    }
+  }
 
   auto load = [&](RawSplit<kW8>& rw, uint32_t st) __attribute__((always_inline)) {
     const uint32_t idx = 2 * st + hb;
-    const uint32_t ublk = SkinnyBlockOf<kMulti>(g, min(idx, nblocks - 1));
+    const uint32_t ublk = block_of(min(idx, nblocks - 1));
     const uint8_t* p = a + (size_t)ublk * kDdrWord + a_off;
     if constexpr (kA8) {
       // 8-bit A operands take K in 16-wide halves per lane: registers 0-3
@@ -447,8 +484,8 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
       // step (block 2 st in 0-3, 2 st + 1 in 4-7) and the scale of block
       // 2 st + h.  nib: bit 0 / 1 set when block 2 st / 2 st + 1 is in range.
       rw.nib = (st < s_end ? 1u : 0u) | ((st < s_end && 2 * st + 1 < nblocks) ? 2u : 0u);
-      const uint32_t b0 = SkinnyBlockOf<kMulti>(g, min(2 * st, nblocks - 1));
-      const uint32_t b1 = SkinnyBlockOf<kMulti>(g, min(2 * st + 1, nblocks - 1));
+      const uint32_t b0 = block_of(min(2 * st, nblocks - 1));
+      const uint32_t b1 = block_of(min(2 * st + 1, nblocks - 1));
       const u32x4 v0 = *reinterpret_cast<const u32x4*>(a + (size_t)b0 * kDdrWord + a_off + 16 * hb);
       const u32x4 v1 = *reinterpret_cast<const u32x4*>(a + (size_t)b1 * kDdrWord + a_off + 16 * hb);
 #pragma unroll
@@ -467,7 +504,8 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
       }
     }
     rw.sa = *reinterpret_cast<const uint32_t*>(p + as_delta);
-    const uint32_t wbc = WBlockCodes(g, ublk), wbs = WBlockScale(g, ublk);
+    const uint32_t wbc = WBlockCodes(g, ublk, h.panels != 0),
+                   wbs = WBlockScale(g, ublk, h.panels != 0);
 #pragma unroll
     for (int pl = 0; pl < kWP; ++pl) {
       const uint8_t* wp = pl ? w1 : w0;
@@ -545,6 +583,17 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
   const uint32_t col = col0 + r32;
   const bool col_in = col < g.n;
   auto row_of = [&](int e) { return row0 + 8 * (e / 4) + 4 * hb + (e & 3); };
+  // K loop: kAhead steps' loads in flight (a split of a small layer has
+  // about that many, so they all go out at once, first of all the wave's
+  // loads); steps past the range are neither loaded nor computed.
+  constexpr int kAhead = 4;
+  RawSplit<kW8> ring[kAhead];
+#pragma unroll
+  for (int i = 0; i < kAhead; ++i)
+    if (s_begin + i < s_end) load(ring[i], s_begin + i);
+  // the rest of the arguments (one scalar load per 64-byte line, one wait)
+  if (touch) TouchArgs(&g, sizeof g);
+
   // The epilogue is shared: the tile's 16 elements per lane form 4 groups
   // of 4 rows (e / 4), group j finished by the layer's wave j % min(4,
   // nwaves) (`own`: this wave's groups).  Each finisher loads its groups'
@@ -582,14 +631,6 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
     }
   }
 
-  // K loop: kAhead steps' loads in flight (a split of a small layer has
-  // about that many, so they all go out at once); steps past the range are
-  // neither loaded nor computed.
-  constexpr int kAhead = 4;
-  RawSplit<kW8> ring[kAhead];
-#pragma unroll
-  for (int i = 0; i < kAhead; ++i)
-    if (s_begin + i < s_end) load(ring[i], s_begin + i);
   for (uint32_t st = s_begin; st < s_end; st += kAhead) {
 #pragma unroll
     for (int i = 0; i < kAhead; ++i) {
@@ -723,12 +764,19 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, uint32_t tile, uint
   }
 }
 
+// The leading arguments (SplitHot's, 13 dwords, preloaded into SGPRs):
+// gy_panels = gy | panels << 31, steps_splits = split_steps | splits << 24;
+// w1 (W8 only) and the GemmArgs follow in memory.
 template <bool kW8, bool kMulti, bool kA8 = false>
-__global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(GemmArgs g) {
+__global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(
+    const uint8_t* a, const uint8_t* w0, uint32_t tiles, uint32_t gy_panels, uint32_t quads,
+    uint32_t a_row, uint32_t piece0, uint32_t nblocks, uint32_t steps_splits, uint32_t w_row,
+    uint32_t groups, const uint8_t* w1, GemmArgs g) {
   __shared__ __attribute__((aligned(16))) float lds_part[kMaxSplitWaves][16 * 64];
   __shared__ uint32_t lds_flag[kMaxSplitWaves];
-  TouchArgs(&g, sizeof g);
-  SplitTile<kW8, kMulti, kA8>(g, XcdLogical(blockIdx.x, gridDim.x),
+  const SplitHot h{a, w0, w1, gy_panels & 0x7FFFFFFFu, quads, a_row, piece0, nblocks,
+                   steps_splits & 0xFFFFFFu, steps_splits >> 24, w_row, groups, gy_panels >> 31};
+  SplitTile<kW8, kMulti, kA8>(g, h, true, XcdLogical(blockIdx.x, tiles),
                          __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
                          blockDim.x / 64, lds_part, lds_flag, false, nullptr, nullptr, 0);
 }
@@ -758,7 +806,7 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitGroupKernel(SplitGro
   const uint32_t waves = blockDim.x / 64;
   const GemmArgs& g = grp.g[in2 ? second : grp.first[u]];
   TouchArgs(&g, sizeof g);
-  SplitTile<kW8, kMulti>(g, tile, wave - base,
+  SplitTile<kW8, kMulti>(g, HotOf(g), false, tile, wave - base,
                          in2 ? waves - s1 : min(s1, waves), lds_part + base, lds_flag + base, pair,
                          pair && !in2 ? lds_y : nullptr, in2 ? lds_y : nullptr, grp.x2_op[u]);
 }
@@ -811,18 +859,31 @@ size_t SplitPlan(GemmArgs& args, uint32_t max_splits) {
 }
 
 hipError_t LaunchSplitLinear(const GemmArgs& args, hipStream_t stream) {
-  const dim3 grid(args.gx * args.gy), block(64 * std::max(args.splits, kSplitFinishWaves));
+  const uint32_t tiles = args.gx * args.gy;
+  const dim3 grid(tiles), block(64 * std::max(args.splits, kSplitFinishWaves));
   const bool w8 = args.n_planes == 2, multi = args.n_pieces > 1;
+  uint32_t nblocks = 0;
+  for (uint32_t p = 0; p < args.n_pieces; ++p) nblocks += args.piece_kb[p];
+  // the packed fields' ranges (steps below 2^24: W spans at most 4 GiB)
+  if (args.gy >= (1u << 31) || args.split_steps >= (1u << 24) || args.splits > 255)
+    return hipErrorInvalidValue;
+  const uint32_t gy_panels = args.gy | (args.w_panels ? 1u << 31 : 0u);
+  const uint32_t steps_splits = args.split_steps | args.splits << 24;
+  const uint32_t w_row = args.w_panels ? args.w_steps : args.kb_total;
+  const uint8_t* w1 = w8 ? args.w[1] : args.w[0];
+#define HB_SPLIT_ARGS args.a, args.w[0], tiles, gy_panels, args.quads, args.a_row, \
+    args.piece_off[0], nblocks, steps_splits, w_row, args.groups, w1, args
   if (w8) {
-    if (multi) hipLaunchKernelGGL((SplitKernel<true, true>), grid, block, 0, stream, args);
-    else hipLaunchKernelGGL((SplitKernel<true, false>), grid, block, 0, stream, args);
+    if (multi) hipLaunchKernelGGL((SplitKernel<true, true>), grid, block, 0, stream, HB_SPLIT_ARGS);
+    else hipLaunchKernelGGL((SplitKernel<true, false>), grid, block, 0, stream, HB_SPLIT_ARGS);
   } else if (args.a_fp8) {
-    if (multi) hipLaunchKernelGGL((SplitKernel<false, true, true>), grid, block, 0, stream, args);
-    else hipLaunchKernelGGL((SplitKernel<false, false, true>), grid, block, 0, stream, args);
+    if (multi) hipLaunchKernelGGL((SplitKernel<false, true, true>), grid, block, 0, stream, HB_SPLIT_ARGS);
+    else hipLaunchKernelGGL((SplitKernel<false, false, true>), grid, block, 0, stream, HB_SPLIT_ARGS);
   } else {
-    if (multi) hipLaunchKernelGGL((SplitKernel<false, true>), grid, block, 0, stream, args);
-    else hipLaunchKernelGGL((SplitKernel<false, false>), grid, block, 0, stream, args);
+    if (multi) hipLaunchKernelGGL((SplitKernel<false, true>), grid, block, 0, stream, HB_SPLIT_ARGS);
+    else hipLaunchKernelGGL((SplitKernel<false, false>), grid, block, 0, stream, HB_SPLIT_ARGS);
   }
+#undef HB_SPLIT_ARGS
   return hipGetLastError();
 }
 

@@ -424,8 +424,10 @@ __device__ __forceinline__ SplitHot HotOf(const GemmArgs& g) {
                   g.w_panels};
 }
 
-template <bool kW8, bool kMulti, bool kA8 = false>
-__device__ __forceinline__ void SplitTile(const GemmArgs& g, const SplitHot& h, bool touch,
+// kSingle: the single-layer launch (its arguments untouched until its
+// loads are out; the epilogue's scalars pinned in SGPRs), else a group's.
+template <bool kW8, bool kMulti, bool kA8 = false, bool kSingle = false>
+__device__ __forceinline__ void SplitTile(const GemmArgs& g, const SplitHot& h,
                                           uint32_t tile, uint32_t split,
                                           uint32_t nwaves, float (*lds_part)[16 * 64],
                                           uint32_t* lds_flag,
@@ -592,7 +594,23 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, const SplitHot& h, 
   for (int i = 0; i < kAhead; ++i)
     if (s_begin + i < s_end) load(ring[i], s_begin + i);
   // the rest of the arguments (one scalar load per 64-byte line, one wait)
-  if (touch) TouchArgs(&g, sizeof g);
+  if constexpr (kSingle) TouchArgs(&g, sizeof g);
+  // The epilogue's sizes and pointers.  A single layer reads them now and
+  // holds them in SGPRs (the empty asm makes them opaque): read after the K
+  // loop, they came one scalar round trip at a time.  (In the group kernel
+  // the pinned values cost more registers than they save.)
+  uint32_t p_m = 0, p_n = 0, p_quads = 0, p_ops = 0;
+  uint32_t* p_c = nullptr;
+  uint8_t* p_q = nullptr;
+  const uint64_t* p_t = nullptr;
+  if constexpr (kSingle) {
+    p_m = g.m, p_n = g.n, p_quads = g.quads, p_ops = g.n_ops;
+    p_c = g.c;
+    p_q = g.q_out;
+    p_t = g.tbuf;
+    asm volatile("" : "+s"(p_m), "+s"(p_n), "+s"(p_quads), "+s"(p_ops), "+s"(p_c), "+s"(p_q),
+                 "+s"(p_t));
+  }
 
   // The epilogue is shared: the tile's 16 elements per lane form 4 groups
   // of 4 rows (e / 4), group j finished by the layer's wave j % min(4,
@@ -638,6 +656,14 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, const SplitHot& h, 
       if (st + kAhead + i < s_end) load(ring[i], st + kAhead + i);
     }
   }
+  // (read where used in a group's tile, as loads the compiler may repeat)
+  auto e_m = [&] { return kSingle ? p_m : g.m; };
+  auto e_n = [&] { return kSingle ? p_n : g.n; };
+  auto e_quads = [&] { return kSingle ? p_quads : g.quads; };
+  auto e_ops = [&] { return kSingle ? p_ops : g.n_ops; };
+  auto e_c = [&] { return kSingle ? p_c : g.c; };
+  auto e_q = [&] { return kSingle ? p_q : g.q_out; };
+  auto e_t = [&] { return kSingle ? p_t : g.tbuf; };
   bool slow = __builtin_amdgcn_ballot_w64(unsafe) != 0;
   f32x16 sum = acc;
   if (blockDim.x > 64) {  // the partials meet in LDS; each finisher adds its groups' in split order
@@ -676,7 +702,7 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, const SplitHot& h, 
       }, std::make_integer_sequence<int, 4>{});
     }
   }
-  const uint64_t* act = g.tbuf != nullptr ? g.tbuf + 512 : nullptr;
+  const uint64_t* act = e_t() != nullptr ? e_t() + 512 : nullptr;
   // group j's rows: ops, C, the requantize, and (a pair's first layer) the
   // values the second reads
   auto finish_group = [&](auto j_c) __attribute__((always_inline)) {
@@ -686,59 +712,59 @@ __device__ __forceinline__ void SplitTile(const GemmArgs& g, const SplitHot& h, 
     for (int i = 0; i < 4; ++i) {
       const int e = 4 * j + i;
       const uint32_t row = row_of(e);
-      const float init = row < g.m ? pre_init[e] : 0.0f;
+      const float init = row < e_m() ? pre_init[e] : 0.0f;
       y[i] = init + sum[e] + 0.0f;
-      if (slow && col_in && (row >> 2) < g.quads) {  // a scale byte left the window: exactly
+      if (slow && col_in && (row >> 2) < e_quads()) {  // a scale byte left the window: exactly
         y[i] = __uint_as_float(kA8 ? SlowLinearFp8(g, a, w0, __float_as_uint(init), row, col)
                                    : SlowLinear(g, a, w0, w1, __float_as_uint(init), row, col));
       }
     }
-    for (uint32_t op = 0; op < g.n_ops; ++op) {
+    for (uint32_t op = 0; op < e_ops(); ++op) {
       const uint32_t kind = g.op_kind[op];
       float pv = 0.0f;
       f32x4_t x2 = {};
       if (x2_lds && op == x2_op) {  // rows past m read zeros, as from memory
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          x2[i] = row_of(4 * j + i) < g.m && col_in ? x2_lds[(4 * j + i) * 64 + lane] : 0.0f;
+          x2[i] = row_of(4 * j + i) < e_m() && col_in ? x2_lds[(4 * j + i) * 64 + lane] : 0.0f;
       } else if (op < (uint32_t)kPreOps) {
 #pragma unroll
         for (int o = 0; o < kPreOps; ++o)
           if (op == (uint32_t)o) {
             pv = pre_v[o];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x2[i] = row_of(4 * j + i) < g.m ? pre_x2[o][4 * j + i] : 0.0f;
+            for (int i = 0; i < 4; ++i) x2[i] = row_of(4 * j + i) < e_m() ? pre_x2[o][4 * j + i] : 0.0f;
           }
       } else if (col_in) {
         if (kind == kEpAddP || kind == kEpMulP) pv = __uint_as_float(g.op_vec[op][col]);
         if (kind == kEpAdd || kind == kEpActMul) {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (row_of(4 * j + i) < g.m)
-              x2[i] = __uint_as_float(g.op_x2[op][(size_t)row_of(4 * j + i) * g.n + col]);
+            if (row_of(4 * j + i) < e_m())
+              x2[i] = __uint_as_float(g.op_x2[op][(size_t)row_of(4 * j + i) * e_n() + col]);
         }
       }
       EpApplyFastN<false>(kind, g.op_imm[op], y, x2, pv, act);
     }
-    if (col_in && g.c != nullptr) {
+    if (col_in && e_c() != nullptr) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t row = row_of(4 * j + i);
-        if (row < g.m) g.c[(size_t)row * g.n + col] = __float_as_uint(y[i]);
+        if (row < e_m()) e_c()[(size_t)row * e_n() + col] = __float_as_uint(y[i]);
       }
     }
-    if (g.q_out != nullptr) {
+    if (e_q() != nullptr) {
       // one MXINT8 block: the row's 32 columns are the 32 lanes of this half
       uint32_t ex[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        ex[i] = HalfMax32((row_of(4 * j + i) >> 2) < g.quads && col_in
+        ex[i] = HalfMax32((row_of(4 * j + i) >> 2) < e_quads() && col_in
                               ? ExpField(__float_as_uint(y[i])) : 0u);
       // the 4 values are rows 0..3 of one quad: one DDR word; lanes 0..15
       // then write its bytes 128..143 (4 scale bytes, 12 zeros) in one store
       const uint32_t quad = row_of(4 * j) >> 2;
-      if (quad < g.quads && col_in) {
-        uint8_t* word = g.q_out + ((size_t)quad * (g.n >> 5) + (col >> 5)) * kDdrWord;
+      if (quad < e_quads() && col_in) {
+        uint8_t* word = e_q() + ((size_t)quad * (e_n() >> 5) + (col >> 5)) * kDdrWord;
 #pragma unroll
         for (int i = 0; i < 4; ++i) word[i * 32 + r32] = QuantizeElementHw(__float_as_uint(y[i]), ex[i]);
         const uint32_t sb = ScaleByteOf(ex[0]) | ScaleByteOf(ex[1]) << 8 |
@@ -776,7 +802,7 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitKernel(
   __shared__ uint32_t lds_flag[kMaxSplitWaves];
   const SplitHot h{a, w0, w1, gy_panels & 0x7FFFFFFFu, quads, a_row, piece0, nblocks,
                    steps_splits & 0xFFFFFFu, steps_splits >> 24, w_row, groups, gy_panels >> 31};
-  SplitTile<kW8, kMulti, kA8>(g, h, true, XcdLogical(blockIdx.x, tiles),
+  SplitTile<kW8, kMulti, kA8, true>(g, h, XcdLogical(blockIdx.x, tiles),
                          __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
                          blockDim.x / 64, lds_part, lds_flag, false, nullptr, nullptr, 0);
 }
@@ -806,7 +832,7 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitGroupKernel(SplitGro
   const uint32_t waves = blockDim.x / 64;
   const GemmArgs& g = grp.g[in2 ? second : grp.first[u]];
   TouchArgs(&g, sizeof g);
-  SplitTile<kW8, kMulti>(g, HotOf(g), false, tile, wave - base,
+  SplitTile<kW8, kMulti>(g, HotOf(g), tile, wave - base,
                          in2 ? waves - s1 : min(s1, waves), lds_part + base, lds_flag + base, pair,
                          pair && !in2 ? lds_y : nullptr, in2 ? lds_y : nullptr, grp.x2_op[u]);
 }

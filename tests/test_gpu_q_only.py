@@ -5,7 +5,8 @@ stores only the ABUF words of the requantize (tools/iss/vec_engine.cpp:
 can requantize, the words equal those of the same layer with C given, bit
 for bit, and those equal the oracle's (bitwise in exact mode, within the
 fast-mode bound otherwise).  The API rejects C = NULL without q_out, with
-`onto`, and for pieces at different A offsets (their launches meet in C)."""
+`onto`, and for pieces at different A offsets (their launches meet in C),
+and C or q_out not 4-byte aligned."""
 from __future__ import annotations
 
 import numpy as np
@@ -128,7 +129,9 @@ def test_rejections(gpu):
     c = torch.zeros((16, 32), dtype=torch.float32, device=DEV)
     q = torch.zeros((4, 144), dtype=torch.uint8, device=DEV)
     for kw in (dict(c=None), dict(c=None, q_out=q, onto=True),
-               dict(c=None, q_out=q, a_stride=4, pieces=[(0, 1, 0), (1, 1, 3)])):
+               dict(c=None, q_out=q, a_stride=4, pieces=[(0, 1, 0), (1, 1, 3)]),
+               dict(q_out=q.data_ptr() + 2),  # q_out not 4-byte aligned
+               dict(c=c.data_ptr() + 2)):  # C not 4-byte aligned
         args = dict(m=16, n=32, kb_total=2, a=a, planes=[w], modes=[0], c=c)
         args.update(kw)
         with pytest.raises(hb.HbError) as err:

@@ -373,16 +373,17 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8, kMulti>())) vo
 
 // ---------------------------------------------------------------------------
 // One small layer in one launch (HB_LINEAR_FAST, a single layer of at most
-// kSplitMaxRows rows).  A workgroup is one wave and computes a 32 x 32
-// output tile over a range of K steps (64 K values: two blocks per step)
-// with v_mfma_scale_f32_32x32x64_f8f6f4: lane l's A operand is 32 values of
-// row l % 32 and block l / 32 of the step, its B operand 32 values of
-// column l % 32 and the same block (formats and scale bytes as above).
-// The K ranges ("splits") of a tile are the waves of its workgroup (up to
-// kMaxSplitWaves): each wave folds its range, the partial sums meet in LDS,
-// and wave 0 adds them in split order, so the sum does not depend on which
-// wave finishes first, then runs the epilogue and the requantize and stores
-// C.  Per split about 3.4 KB of operands per step (MXFP4), so a workgroup
+// kSplitMaxRows rows).  A workgroup computes a 32 x 32 output tile with
+// v_mfma_scale_f32_32x32x64_f8f6f4 over K steps (64 K values: two blocks
+// per step): lane l's A operand is 32 values of row l % 32 and block l / 32
+// of the step, its B operand 32 values of column l % 32 and the same block
+// (formats and scale bytes as above).  The K ranges ("splits") of a tile
+// are the waves of its workgroup (up to kMaxSplitWaves; at least
+// kSplitFinishWaves waves, the ones past the splits folding nothing): each
+// wave folds its range, the partial sums meet in LDS, and each of 4
+// finishers adds its row group's sums in split order, so the sum does not
+// depend on which wave finishes first, then runs the epilogue and the
+// requantize and stores C.  Per split about 3.4 KB of operands per step (MXFP4), so a workgroup
 // moves a few 10 KB: small layers are latency-bound, and the splits put
 // every tile's loads in flight at once with one round trip to memory,
 // finishing in the same workgroup.
@@ -398,8 +399,9 @@ typedef float f32x16s __attribute__((ext_vector_type(16)));
 // One layer's tile of a split launch, called by the waves of the workgroup
 // that fold it (`split`: the wave's K range; a wave past the layer's splits
 // folds nothing; nwaves: the layer's waves in the workgroup).  The
-// partials meet in part / flag (LDS, [split][e][lane]) and up to 4 of the
-// layer's waves finish the tile, 4 of each lane's 16 rows apiece.  A fused
+// partials meet in part / flag (LDS, [split][row group][lane] 16-byte
+// slots) and up to 4 of the layer's waves finish the tile, 4 of each lane's
+// 16 rows apiece.  A fused
 // pair (`pair`) is two layers of one tile whose waves fold at the same
 // time: the first layer's finishers leave its values in y_lds ([e][lane]),
 // and after a second barrier the second layer's finishers read them from

@@ -175,22 +175,26 @@ void W8Kernel(GemmArgs g) {
     // last load the last one again, so every wave issues kOps loads per
     // step, all in bounds.
     uint32_t ds = 0, dslot = 0;
+    // load k of the step at s into the slot at LDS byte `slot`
+    auto issue_op = [&](int k, uint32_t s, uint32_t slot) __attribute__((always_inline)) {
+      if (k < kALoads) {
+        const uint32_t i = kALoads * w + k;  // uniform
+        const uint32_t h = i < kACodes / 1024 ? i / 4 : i % 2;
+        Dma16(a + min(2 * s + h, nblocks - 1) * kDdrWord, voff[k], slot + i * 1024);
+      } else {
+        Dma16(wp + s * kW8Chunk, voff[k], slot + kSlotW + (kWaves * (k - kALoads) + w) * 1024);
+      }
+    };
+    auto issue_advance = [&]() __attribute__((always_inline)) {
+      ++ds;
+      dslot = dslot + 1 == kD ? 0u : dslot + 1;
+    };
     auto issue_next = [&]() __attribute__((always_inline)) {
       const uint32_t s = min(ds, steps - 1);
       const uint32_t slot = ring_base + dslot * kSlot;
 #pragma unroll
-      for (int k = 0; k < kOps; ++k) {
-        if (k < kALoads) {
-          const uint32_t i = kALoads * w + k;  // uniform
-          const uint32_t h = i < kACodes / 1024 ? i / 4 : i % 2;
-          Dma16(a + min(2 * s + h, nblocks - 1) * kDdrWord, voff[k], slot + i * 1024);
-        } else {
-          Dma16(wp + s * kW8Chunk, voff[k],
-                slot + kSlotW + (kWaves * (k - kALoads) + w) * 1024);
-        }
-      }
-      ++ds;
-      dslot = dslot + 1 == kD ? 0u : dslot + 1;
+      for (int k = 0; k < kOps; ++k) issue_op(k, s, slot);
+      issue_advance();
     };
 
     // Reads from ring slot `slot`: W's B operands and scale dwords; this
@@ -255,7 +259,9 @@ void W8Kernel(GemmArgs g) {
       WaitVm<(kD - 3) * kOps>();
       WaitLds();
       __syncthreads();
-      issue_next();
+      // the refill's loads go out between the step's MFMAs (one after every
+      // kEvery), not in a burst ahead of them
+      const uint32_t is_s = min(ds, steps - 1), is_slot = ring_base + dslot * kSlot;
       const uint32_t s1 = slot + 1 == kD ? 0u : slot + 1;
       const uint32_t s2 = s1 + 1 == kD ? 0u : s1 + 1;
       read_w(oth, s1);
@@ -269,25 +275,28 @@ void W8Kernel(GemmArgs g) {
                         (int)use.r[4], (int)use.r[5], 0, 0};
       // product (A plane pa, W plane pl) over the n-tiles, for each of the
       // four products (n-tiles past the layer compute outputs not stored)
+      constexpr int kM = 4 * kNT, kEvery = (kM + kOps - 1) / kOps;
       Unroll<4>([&](auto pc) {
         constexpr int kPa = decltype(pc)::value / 2, kPl = decltype(pc)::value % 2;
         Unroll<kNT>([&](auto tc) {
           constexpr int kT = decltype(tc)::value;
+          constexpr int kI = decltype(pc)::value * kNT + kT;  // MFMA index in the step
           const u32x6& bv = use.b[2 * kT + kPl];
           const i32x8 bt = {(int)bv[0], (int)bv[1], (int)bv[2], (int)bv[3], (int)bv[4], (int)bv[5],
                             0, 0};
           acc[kT] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
               kPa ? ar : ah, bt, acc[kT], 2, 2, kPa, use.sa, 2 * (kT % 2) + kPl,
               (int)use.sw[kT / 2]);
+          if constexpr ((kI + 1) % kEvery == 0 && (kI + 1) / kEvery <= kOps) {
+            // (the empty asm takes this MFMA's result: the MFMA issues first)
+            asm volatile("" ::"a"(acc[kT]));
+            issue_op((kI + 1) / kEvery - 1, is_s, is_slot);
+          }
         });
       });
-      // issue order: the LDS reads, then each MFMA followed by a share of the
-      // step's vector ALU work
-      __builtin_amdgcn_sched_group_barrier(0x100, 9 * kTP + 3, 0);
-      Unroll<4 * kNT>([&](auto) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-      });
+#pragma unroll
+      for (int k = kM / kEvery; k < kOps; ++k) issue_op(k, is_s, is_slot);
+      issue_advance();
 #pragma unroll
       for (int t = 0; t < kNT; ++t) asm volatile("" : "+a"(acc[t]));
       asm volatile("" : "+v"(oth.h), "+v"(oth.r), "+v"(oth.sa), "+v"(oth.abad));

@@ -165,10 +165,10 @@ uint64_t hb_gemm_cycles(const hb_gemm_cmd* cmd, uint32_t fixed_cycles);
  * RELU, ACT, ACT_MUL) or the row programs 12 SOFTMAX, 22 LAYERNORM, 34
  * RMSNORM (tools/compiler/vec_rom.cpp:133-212, 239-272), with or without
  * quantize.  The engine's failures return HB_EBADCMD with its texts.  A row
- * program whose quads touch the same FBUF or ABUF words returns
- * HB_EUNSUPPORTED (its result depends on the engine's pass interleaving,
- * which this backend does not reproduce); HB_EUNSUPPORTED also for other
- * entries (10 ROPE and the transposes). */
+ * program whose quads touch FBUF or ABUF words that other quads write runs
+ * in the engine's pass order (pairs of quads pass by pass, vec_rom.cpp:
+ * 84-131) in one workgroup; other row programs run one workgroup per quad.
+ * HB_EUNSUPPORTED for other entries (10 ROPE and the transposes). */
 int hb_vec_exec(hb_ctx* ctx, const hb_vec_cmd* cmd, hb_onchip* onchip);
 
 /* ---------------------------------------------------- linear level -- */

@@ -718,7 +718,13 @@ int hb_ctx_create(int device, hb_ctx** out) {
   ctx->device = device;
   hipError_t err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (err == hipSuccess) err = hipMalloc(&ctx->d_flag, sizeof(uint32_t));
+  // the workspace starts at the no-allocation path's size, so a layer whose
+  // K splits fit in it never allocates after the context is created
+  if (err == hipSuccess) err = hb::GrowWorkspace(ctx->ws, HB_NOALLOC_SCRATCH_BYTES, ctx->stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
   if (err != hipSuccess) {
+    hb::FreeWorkspace(ctx->ws);
+    if (ctx->d_flag) (void)hipFree(ctx->d_flag);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return HipFail(err, "context create");

@@ -287,9 +287,10 @@ typedef struct hb_linear_desc {
   uint32_t a_stride;
 } hb_linear_desc;
 
-/* A single small layer (fewer than 128 output tiles) may grow the context's
- * workspace on its first call of a larger shape (a hipMalloc, with no stream
- * synchronization).  A workspace buffer is never freed before
+/* A single small layer (fewer than 128 output tiles) splits its K range
+ * over workgroups in the context's workspace, which hb_ctx_create sizes to
+ * HB_NOALLOC_SCRATCH_BYTES; a layer that needs more grows it on its first
+ * call of that shape (a hipMalloc, with no stream synchronization).  A workspace buffer is never freed before
  * hb_ctx_destroy, so work already queued and HIP graphs captured earlier
  * stay valid when a later call grows it; a graph is valid until its context
  * is destroyed.  Warm a shape up before capturing it in a graph (the

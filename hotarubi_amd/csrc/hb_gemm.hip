@@ -722,6 +722,12 @@ hipError_t LaunchFp8Linear(const GemmArgs& in, uint32_t batch, bool fast, hipStr
     args.fast_ep = 1u;
     return LaunchSplitLinear(args, stream);
   }
+  // batches of layers of up to 16 rows: the skinny kernel (the streaming
+  // kernel's 128-row tiles would be mostly padding)
+  if (fast && args.quads * 4 <= 16) {
+    args.fast_ep = 1u;
+    return LaunchLinearSkinny(args, batch, stream);
+  }
   // batches and larger layers over weight panels (ops and the requantize
   // included): the streaming kernel, not the per-output exact fold below
   if (fast && StreamEligible(args)) {

@@ -139,8 +139,16 @@ struct RawS {
   uint32_t nib;  // 0x0F0F0F0F, or 0 for a block past the end (adds zero)
 };
 
-template <int kMT, bool kW8, bool kMulti, bool kPanels>
+// kA8 (MXFP8 activations, kMT 1, MXFP4 W): the code bytes are the MFMA's
+// FP8 operand, which takes K in 16-wide chunks: lane group q = l / 16
+// holds K [16 q, 16 q + 16) of the 128-deep chunk in registers 0-3 and K
+// [64 + 16 q, + 16) in registers 4-7, i.e. bytes [16 (q % 2), + 16) of its
+// row in blocks q / 2 and 2 + q / 2, while its scale byte is still block
+// q's.  Each chunk's codes go through two MFMAs, split by exponent
+// (fp8::Split), as in the other MXFP8 kernels.
+template <int kMT, bool kW8, bool kMulti, bool kPanels, bool kA8 = false>
 __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8, kMulti>())) void SkinnyKernel(GemmArgs g) {
+  static_assert(!kA8 || (kMT == 1 && !kW8), "MXFP8 activations: 16 rows, MXFP4 W");
   constexpr int kNT = NTiles<kMT, kW8>(), kCols = 16 * kNT, kWP = kW8 ? 2 : 1;
   constexpr int kRows = 16 * kMT, kOut = kRows * kCols;
   __shared__ float lds_part[kWaves][kOut];  // the waves' partial sums
@@ -214,8 +222,23 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8, kMulti>())) vo
     const uint32_t blk = ublk * kDdrWord;
     const uint32_t wbc = kPanels ? WBlockCodes(g, ublk) : blk;
     const uint32_t wbs = kPanels ? WBlockScale(g, ublk) : blk;
+    if constexpr (kA8) {  // the two 16-byte chunks (blocks 4 ch + q / 2 and + 2); nib bit i: chunk i live
+      const uint32_t i0 = 4 * ch + (kq >> 1), i1 = i0 + 2;
+      rw.nib = (ch < c_end && i0 < nblocks ? 1u : 0u) | (ch < c_end && i1 < nblocks ? 2u : 0u);
+      const uint32_t b0 = SkinnyBlockOf<kMulti>(g, min(i0, nblocks - 1)) * kDdrWord;
+      const uint32_t b1 = SkinnyBlockOf<kMulti>(g, min(i1, nblocks - 1)) * kDdrWord;
+      const uint32_t at = a_off[0] + 16 * (kq & 1);  // the row's codes, this half
+      const u32x4 v0 = *reinterpret_cast<const u32x4*>(a + b0 + at);
+      const u32x4 v1 = *reinterpret_cast<const u32x4*>(a + b1 + at);
 #pragma unroll
-    for (int mi = 0; mi < kMT; ++mi) {
+      for (int i = 0; i < 4; ++i) {
+        rw.a[0][i] = v0[i];
+        rw.a[0][4 + i] = v1[i];
+      }
+      rw.sa[0] = *reinterpret_cast<const uint32_t*>(a + blk + a_off[0] + as_delta);
+    }
+#pragma unroll
+    for (int mi = 0; mi < (kA8 ? 0 : kMT); ++mi) {
       const uint8_t* p = a + blk + a_off[mi];
       const u32x4 v0 = *reinterpret_cast<const u32x4*>(p);
       const u32x4 v1 = *reinterpret_cast<const u32x4*>(p + 16);
@@ -275,6 +298,30 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8, kMulti>())) vo
         for (int i = 0; i < 4; ++i) b[nj][0][i] = (int)rw.w[nj][0][i];
         b[nj][0][4] = b[nj][0][5] = b[nj][0][6] = b[nj][0][7] = 0;
       }
+    }
+    if constexpr (kA8) {
+      const uint32_t ea = __builtin_amdgcn_ubfe(rw.sa[0], ashift, 8);
+      unsafe |= ea - kSafeLo > kSafeHi - kSafeLo;
+      const uint32_t keep0 = (rw.nib & 1u) ? ~0u : 0u, keep1 = (rw.nib & 2u) ? ~0u : 0u;
+      i32x8 a_lo, a_hi;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint32_t lo, hi;
+        fp8::Split(rw.a[0][i] & (i < 4 ? keep0 : keep1), lo, hi);
+        a_lo[i] = (int)lo;
+        a_hi[i] = (int)hi;
+      }
+      UnrollS([&](auto nj_c) {
+        constexpr int nj = decltype(nj_c)::value;
+        acc[0][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a_lo, b[nj][0], acc[0][nj], 0, 4,
+                                                                       0, (int)ea, 0, (int)sb[nj]);
+      }, std::make_integer_sequence<int, kNT>{});
+      UnrollS([&](auto nj_c) {
+        constexpr int nj = decltype(nj_c)::value;
+        acc[0][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a_hi, b[nj][0], acc[0][nj], 0, 4,
+                                                                       0, (int)ea, 0, (int)sb[nj]);
+      }, std::make_integer_sequence<int, kNT>{});
+      return;
     }
 #pragma unroll
     for (int mi = 0; mi < kMT; ++mi) {
@@ -340,7 +387,8 @@ __global__ __launch_bounds__(kWaves * 64, (WavesPerSimd<kMT, kW8, kMulti>())) vo
     if (in) {
       const uint32_t init = (g.acc && row < g.m) ? c[(size_t)row * g.n + col] : 0u;
       if (slow) {
-        y = SlowLinear<kPanels ? 2 : 1>(g, a, w0, w1, init, row, col);
+        y = kA8 ? SlowLinearFp8(g, a, w0, init, row, col)
+                : SlowLinear<kPanels ? 2 : 1>(g, a, w0, w1, init, row, col);
       } else {
         float s = __uint_as_float(init);
 #pragma unroll
@@ -839,7 +887,7 @@ __global__ __launch_bounds__(64 * kMaxSplitWaves) void SplitGroupKernel(SplitGro
                          pair && !in2 ? lds_y : nullptr, in2 ? lds_y : nullptr, grp.x2_op[u]);
 }
 
-template <int kMT, bool kW8, bool kMulti>
+template <int kMT, bool kW8, bool kMulti, bool kA8 = false>
 void LaunchS(const GemmArgs& in, uint32_t batch, hipStream_t stream) {
   constexpr int kCols = 16 * NTiles<kMT, kW8>();
   GemmArgs args = in;
@@ -847,10 +895,10 @@ void LaunchS(const GemmArgs& in, uint32_t batch, hipStream_t stream) {
   args.gy = 1;
   args.gz = batch;
   if (args.w_panels)
-    hipLaunchKernelGGL((SkinnyKernel<kMT, kW8, kMulti, true>), dim3(args.gx * args.gz),
+    hipLaunchKernelGGL((SkinnyKernel<kMT, kW8, kMulti, true, kA8>), dim3(args.gx * args.gz),
                        dim3(kWaves * 64), 0, stream, args);
   else
-    hipLaunchKernelGGL((SkinnyKernel<kMT, kW8, kMulti, false>), dim3(args.gx * args.gz),
+    hipLaunchKernelGGL((SkinnyKernel<kMT, kW8, kMulti, false, kA8>), dim3(args.gx * args.gz),
                        dim3(kWaves * 64), 0, stream, args);
 }
 
@@ -933,6 +981,12 @@ hipError_t LaunchLinearSkinny(const GemmArgs& args, uint32_t batch, hipStream_t 
   // (layers of up to 16 rows in a batch; one layer of up to kSplitMaxRows
   // rows runs as a split launch instead)
   if (args.quads * 4 > 16) return hipErrorInvalidValue;
+  if (args.a_fp8) {  // one MXFP4 plane
+    if (args.n_planes != 1 || args.modes[0] != kModeFp4) return hipErrorInvalidValue;
+    if (args.n_pieces > 1) LaunchS<1, false, true, true>(args, batch, stream);
+    else LaunchS<1, false, false, true>(args, batch, stream);
+    return hipGetLastError();
+  }
   LaunchRowsS<1>(args, batch, stream);
   return hipGetLastError();
 }

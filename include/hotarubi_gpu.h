@@ -276,10 +276,12 @@ typedef struct hb_linear_desc {
    * codes go to the FP8 x FP4 matrix cores as two planes split by
    * exponent, so every instruction sums its products without loss): one
    * layer of up to 1,024 rows (ops, requantize, pieces, DDR words or
-   * panels); batches and larger layers of one piece with the weights in
-   * panels (ops and the requantize included).  Other fast MXFP8 layers
-   * (batches or more than 1,024 rows over DDR words, or with several
-   * pieces) fold exactly per output (correct, slower). */
+   * panels); batches of layers of up to 16 rows (the same); batches and
+   * larger layers of one piece with the weights in panels (ops and the
+   * requantize included).  Other fast MXFP8 layers
+   * (batches of more than 16 rows or layers of more than 1,024 rows over
+   * DDR words or with several pieces) fold exactly per output (correct,
+   * slower). */
   uint32_t flags;
   /* 0: A is [ceil(m/4)][kb_total] words.  Otherwise A words per quad, and
    * each piece's blocks start at its a_word (see hb_piece); every A word a

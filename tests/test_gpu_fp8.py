@@ -11,7 +11,9 @@ pinned in test_oracle_fp8.py):
     exponent planes) within the fast-mode bound of the MXINT8 path
     (check_fp8_fast) at config 1's sweep M in {1, 16, 128, 1024} (K = 2560,
     N = 960) one layer per launch and batched (the streaming kernel, more
-    tiles than CUs, from C, a partial panel, a mid-stream exact recompute),
+    tiles than CUs, from C, a partial panel, a mid-stream exact recompute;
+    the skinny kernel for up to 16 rows: ragged rows, partial panels, DDR
+    words, pieces, an out-of-window scale),
     and M = 141, with ops and requantize, and with scale bytes outside the
     fast window (those tiles are computed exactly, bitwise);
   * the descriptor rule (one MXFP4 plane).
@@ -201,13 +203,15 @@ def test_fp8_needs_one_mxfp4_plane(gpu):
 
 # ---- batches over weight panels: the streaming kernel ----
 
-def fp8_batch(gpu, m, n, kb, layers, sets, onto=False, bad=None, seed=0):
-    """`layers` MXFP8 x MXFP4 layers (weights in panels) in one fast batched
-    launch; layer i holds data set i % sets.  The oracle computes each set
-    once and every layer holding it must equal it bit for bit.  bad =
-    (layer, word): that layer's weights get one scale byte outside the
-    fast window in DDR word `word` (the tile holding it is recomputed by
-    the exact fold, bitwise, in the middle of the workgroup's stream)."""
+def fp8_batch(gpu, m, n, kb, layers, sets, onto=False, bad=None, seed=0, panels=True,
+              pieces=None, tile_cols=320):
+    """`layers` MXFP8 x MXFP4 layers (weights in panels, or DDR words) in
+    one fast batched launch; layer i holds data set i % sets.  The oracle
+    computes each set once and every layer holding it must equal it bit for
+    bit.  bad = (layer, word): that layer's weights get one scale byte
+    outside the fast window in DDR word `word` (the tile_cols-wide column
+    tile holding it is recomputed by the exact fold, bitwise, in the middle
+    of the workgroup's stream)."""
     rng = np.random.default_rng(seed)
     a_sets, w_sets, c_sets = [], [], []
     for _ in range(sets):
@@ -224,16 +228,22 @@ def fp8_batch(gpu, m, n, kb, layers, sets, onto=False, bad=None, seed=0):
     w_p = torch.empty((layers, pb), dtype=torch.uint8, device=DEV)
     c_d = torch.zeros((layers, m, n), dtype=torch.float32, device=DEV)
     w_dev = [dev(w) for w in w_sets]
+    if not panels:
+        w_p = torch.empty((layers,) + w_sets[0].shape, dtype=torch.uint8, device=DEV)
     for i in range(layers):
         a_d[i].copy_(dev(a_sets[set_of[i]]))
         src = dev(w_bad) if bad is not None and i == bad[0] else w_dev[set_of[i]]
-        hb.pack_weights(src, n, kb, w_p[i], ctx=gpu)
+        if panels:
+            hb.pack_weights(src, n, kb, w_p[i], ctx=gpu)
+        else:
+            w_p[i].copy_(src)
         if onto:
             c_d[i].copy_(dev(c_sets[set_of[i]].view(np.float32)))
-    descs = [hb.linear_desc(m, n, kb, a_d[i], [w_p[i]], [0], c_d[i], mode=hb.FAST, panels=True,
-                            onto=onto, a_fp8=True) for i in range(layers)]
+    descs = [hb.linear_desc(m, n, kb, a_d[i], [w_p[i]], [0], c_d[i], mode=hb.FAST, panels=panels,
+                            onto=onto, a_fp8=True, pieces=pieces) for i in range(layers)]
     torch.cuda.synchronize()
-    say("fp8 batch", dict(m=m, n=n, kb=kb, layers=layers, sets=sets, onto=onto, bad=bad))
+    say("fp8 batch", dict(m=m, n=n, kb=kb, layers=layers, sets=sets, onto=onto, bad=bad,
+                          panels=panels, pieces=pieces))
     hb.linear_batched(descs, gpu)
     got = host(c_d).view(np.uint32)
     rep = {}
@@ -246,7 +256,7 @@ def fp8_batch(gpu, m, n, kb, layers, sets, onto=False, bad=None, seed=0):
             rep[set_of[i]] = i
     for s in range(sets):
         want, _ = helpers.oracle_linear_mt(m, n, kb, a_sets[s], [w_sets[s]], [0], onto=c_sets[s],
-                                           a_fp8=True)
+                                           a_fp8=True, pieces=pieces)
         if onto:
             g, w = got[rep[s]].view(np.float32).astype(np.float64), want.view(np.float32)
             row = np.abs(w.astype(np.float64)).max(axis=1, keepdims=True)
@@ -257,9 +267,9 @@ def fp8_batch(gpu, m, n, kb, layers, sets, onto=False, bad=None, seed=0):
         layer, word = bad
         s = set_of[layer]
         want, _ = helpers.oracle_linear_mt(m, n, kb, a_sets[s], [w_bad], [0], onto=c_sets[s],
-                                           a_fp8=True)
-        c0 = (word // kb) * 8 // 320 * 320
-        cols = slice(c0, min(c0 + 320, n))
+                                           a_fp8=True, pieces=pieces)
+        c0 = (word // kb) * 8 // tile_cols * tile_cols
+        cols = slice(c0, min(c0 + tile_cols, n))
         assert np.array_equal(got[layer][:, cols], want[:, cols])
         others = np.setdiff1d(np.arange(n), np.arange(n)[cols])
         assert np.array_equal(got[layer][:, others], got[rep[s]][:, others])
@@ -282,3 +292,25 @@ def test_fast_batched_exact_recompute_mid_stream(gpu):
     """One weight scale byte outside the window in layer 150's middle column
     tile: that tile is folded exactly, the rest of the stream is fast."""
     fp8_batch(gpu, 128, 960, 80, 256, 11, bad=(150, 50 * 80 + 41), seed=811)
+
+
+# ---- batches of layers of up to 16 rows: the skinny kernel ----
+
+@pytest.mark.parametrize("m,n,kb,panels,onto", [(5, 200, 7, True, True), (16, 256, 13, False, False),
+                                                (1, 64, 1, True, False), (11, 960, 80, False, True)])
+def test_skinny_batched(gpu, m, n, kb, panels, onto):
+    """Ragged rows, a partial last panel, odd and single block counts (a
+    K chunk's blocks past the end), over panels and DDR words, from C."""
+    fp8_batch(gpu, m, n, kb, 24, 3, onto=onto, panels=panels, seed=820 + m)
+
+
+@pytest.mark.parametrize("panels", [True, False])
+def test_skinny_pieces(gpu, panels):
+    """Two pieces, W blocks [9, 23) then [0, 9), over panels and DDR words."""
+    fp8_batch(gpu, 16, 320, 23, 12, 2, panels=panels, pieces=[(9, 14), (0, 9)], seed=830)
+
+
+def test_skinny_out_of_window_scale(gpu):
+    """One weight scale byte outside the window: that workgroup's 64 columns
+    are folded exactly (bitwise), every other one is fast."""
+    fp8_batch(gpu, 16, 960, 80, 64, 5, bad=(40, 7 * 80 + 33), seed=831, tile_cols=64)

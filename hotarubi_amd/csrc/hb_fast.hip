@@ -356,6 +356,10 @@ __global__ __launch_bounds__(512 + kBM * 4) void FastKernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) float lds_vec[kMaxOps][kBN];  // tile's op columns
   __shared__ uint32_t lds_unsafe;
 
+  // every line of the arguments into the scalar cache at once: the epilogue
+  // reads many of them (sizes, pointers, op kinds), each otherwise a round
+  // trip to memory in turn after the K loop
+  TouchArgs(&g, sizeof g);
   const TileId tile = LogicalTile(g.gx, g.gy, g.gz);
   // z: the layer of a batched launch, or the K split of a split one layer
   const uint32_t split = g.splits > 1 ? tile.z : 0u;

@@ -303,7 +303,7 @@ hipError_t LaunchLinearSkinny(const GemmArgs& args, uint32_t batch, hipStream_t 
 constexpr uint32_t kSplitMaxRows = 160;
 bool SplitEligible(const GemmArgs& args, uint32_t batch);
 // Grid and K split of a split launch (sets gx, gy, splits, split_steps:
-// splits of at least 4 steps, at most max_splits, one wave each) and the
+// splits of at least 2 steps, at most max_splits, one wave each) and the
 // workspace bytes it needs past the counters (0: no partials).
 constexpr uint32_t kMaxSplitWaves = 8;
 // Waves a split workgroup has at least: the epilogue's 4 row groups of a

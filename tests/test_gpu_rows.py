@@ -3,7 +3,13 @@ MI355X against the oracle's hb_vec_exec of the same rows laid out as FBUF
 words, bitwise: RMSNorm + quantize at the SmolVLA LM width (960, 141 rows
 and 4512 rows), LayerNorm at the SigLIP width (768), softmax over 141 of 192
 keys, fp32 and MXINT8 outputs, a last quad with fewer than 4 rows, and the
-argument checks.  The MXINT8 words feed hb_linear as its A."""
+argument checks.  The MXINT8 words feed hb_linear as its A.
+
+Both forms of the kernel run: with the source rows kept in LDS (the smaller
+cases) and read again by each pass that takes them, which the library picks
+when that lets the quads fit in one round of the CUs (on a 256-CU MI355X:
+RMSNorm 4512 x 960, 1,128 quads, 4 resident per CU with the rows kept and 6
+without; LayerNorm 6000 x 768, 1,500 quads, 5 and 7)."""
 from __future__ import annotations
 
 import sys
@@ -95,7 +101,8 @@ def activations(rng, rows, cols, scale=1.0):
     return (rng.standard_normal((rows, cols)) * scale).astype(np.float32).view(np.uint32)
 
 
-@pytest.mark.parametrize("rows,quantize", [(141, True), (141, False), (4512, True), (3, True)])
+@pytest.mark.parametrize("rows,quantize", [(141, True), (141, False), (4512, True), (4512, False),
+                                          (3, True)])
 def test_rmsnorm_smolvla_width(gpu, rows, quantize):
     rng = np.random.default_rng(rows + quantize)
     cols = 960
@@ -105,7 +112,8 @@ def test_rmsnorm_smolvla_width(gpu, rows, quantize):
     check(got, oracle_rows(34, x, cols, EPS, gamma=gamma, quantize=quantize))
 
 
-@pytest.mark.parametrize("rows,quantize", [(64, False), (2048, True), (50, True)])
+@pytest.mark.parametrize("rows,quantize", [(64, False), (2048, True), (50, True), (6000, True),
+                                          (5999, False)])
 def test_layernorm_siglip_width(gpu, rows, quantize):
     rng = np.random.default_rng(100 + rows)
     cols = 768

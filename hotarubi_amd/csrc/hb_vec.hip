@@ -341,7 +341,7 @@ __host__ __device__ constexpr size_t RowLdsBytes(uint32_t n8, bool ddr, bool cac
 // keeps them in `xs` for the later passes that read the source; otherwise
 // every such pass reads them again (the host picks the form, see
 // RowsCacheSource).
-template <bool kDdr, bool kCache = false>
+template <bool kDdr, bool kCache = false, uint32_t kT = 256>
 __device__ __forceinline__ void RowQuadPass(const VecRowArgs& a, const RowPass& p, bool first,
                                             uint32_t quad, const VecRowDdr& d, uint8_t* abuf,
                                             uint32_t* fbuf, const uint32_t* pbuf,
@@ -352,7 +352,7 @@ __device__ __forceinline__ void RowQuadPass(const VecRowArgs& a, const RowPass& 
   // The pass's operands in device memory (the DDR form's source rows, read
   // by every pass that takes the source; the FBUF and PBUF words) are copied
   // into LDS first, up to kStage requests in flight per thread: element
-  // e = tid + 256 i belongs to the same thread in both loops, so no barrier
+  // e = tid + kT i belongs to the same thread in both loops, so no barrier
   // is needed between them, and a thread waits for one round trip per kStage
   // elements instead of one per element.  The x operand lands in `out`: a
   // pass that reads the source does not read the previous pass's outputs,
@@ -361,12 +361,12 @@ __device__ __forceinline__ void RowQuadPass(const VecRowArgs& a, const RowPass& 
   const bool stage_x = kDdr ? !kCache && p.from_x != 0 : true;
   const bool stage_p = !kDdr && p.pb != ~0u;
   if (stage_x || stage_p) {
-    for (uint32_t b0 = 0; b0 < total; b0 += 256 * kStage) {
+    for (uint32_t b0 = 0; b0 < total; b0 += kT * kStage) {
       uint32_t xv[kStage], pv[kStage];
 #pragma unroll
       for (uint32_t i = 0; i < kStage; ++i) {
-        if (b0 + 256 * i >= total) break;  // the same for the whole workgroup
-        const uint32_t e = b0 + 256 * i + tid;
+        if (b0 + kT * i >= total) break;  // the same for the whole workgroup
+        const uint32_t e = b0 + kT * i + tid;
         const uint32_t w = e >> 5, t = (e >> 3) & 3u, l = e & 7u;
         xv[i] = pv[i] = 0u;
         if (e < total) {
@@ -382,8 +382,8 @@ __device__ __forceinline__ void RowQuadPass(const VecRowArgs& a, const RowPass& 
       }
 #pragma unroll
       for (uint32_t i = 0; i < kStage; ++i) {
-        if (b0 + 256 * i >= total) break;
-        const uint32_t e = b0 + 256 * i + tid;
+        if (b0 + kT * i >= total) break;
+        const uint32_t e = b0 + kT * i + tid;
         if (e < total) {
           if (stage_x) out[e] = xv[i];
           if (stage_p) sp[e] = pv[i];
@@ -391,7 +391,7 @@ __device__ __forceinline__ void RowQuadPass(const VecRowArgs& a, const RowPass& 
       }
     }
   }
-  for (uint32_t e = tid; e < total; e += 256) {
+  for (uint32_t e = tid; e < total; e += kT) {
     const uint32_t w = e >> 5, t = (e >> 3) & 3u, l = e & 7u;
     uint32_t x;
     if (kDdr && kCache && p.from_x && first) {
@@ -421,7 +421,7 @@ __device__ __forceinline__ void RowQuadPass(const VecRowArgs& a, const RowPass& 
   }
   __syncthreads();
   if (p.red != kRedNone) {
-    for (uint32_t i2 = tid; i2 < n8 * 4; i2 += 256) {
+    for (uint32_t i2 = tid; i2 < n8 * 4; i2 += kT) {
       const uint32_t* v = &out[(i2 >> 2) * 32 + (i2 & 3u) * 8];
       tree[i2] = p.red == kRedSum
                      ? FAdd(FAdd(FAdd(v[0], v[1]), FAdd(v[2], v[3])), FAdd(FAdd(v[4], v[5]), FAdd(v[6], v[7])))
@@ -466,7 +466,7 @@ __device__ __forceinline__ void RowQuadPass(const VecRowArgs& a, const RowPass& 
     }
   }
   if (kDdr && p.wr == kWrFinal && !a.quantize) {
-    for (uint32_t e = tid; e < n8 * 32; e += 256) {
+    for (uint32_t e = tid; e < n8 * 32; e += kT) {
       const uint32_t row = quad * 4 + ((e >> 3) & 3u);
       if (row < d.rows) d.y[(size_t)row * d.cols + (e >> 5) * 8 + (e & 7u)] = out[e];
     }
@@ -478,7 +478,7 @@ __device__ __forceinline__ void RowQuadPass(const VecRowArgs& a, const RowPass& 
     // dwords; qw 0 the token's scale byte; token 0's qw 0..2 the 12 zero
     // bytes 132..143.
     const uint32_t nb = n8 / 4;
-    for (uint32_t i2 = tid; i2 < n8 * 4; i2 += 256) {
+    for (uint32_t i2 = tid; i2 < n8 * 4; i2 += kT) {
       const uint32_t b = i2 >> 4, t = (i2 >> 2) & 3u, qw = i2 & 3u;
       const uint32_t* v = &out[(4 * b + qw) * 32 + t * 8];
       uint32_t emax = 0;
@@ -500,10 +500,10 @@ __device__ __forceinline__ void RowQuadPass(const VecRowArgs& a, const RowPass& 
   } else if (kDdr) {
     // the scratch region stays in LDS
   } else if (p.wr == kWrFbuf || (p.wr == kWrFinal && !a.quantize)) {
-    for (uint32_t e = tid; e < n8 * 32; e += 256)
+    for (uint32_t e = tid; e < n8 * 32; e += kT)
       fbuf[(size_t)((p.dst + (e >> 5)) & (kFbufDepth - 1)) * 32 + (e & 31u)] = out[e];
   } else if (p.wr == kWrFinal) {  // QuantizeBlock per 4 words (lane.cpp:406-424)
-    for (uint32_t i2 = tid; i2 < n8; i2 += 256) {
+    for (uint32_t i2 = tid; i2 < n8; i2 += kT) {
       const uint32_t b = i2 >> 2, t = i2 & 3u;
       uint32_t emax = 0;
       for (uint32_t qw = 0; qw < 4; ++qw)
@@ -522,8 +522,8 @@ __device__ __forceinline__ void RowQuadPass(const VecRowArgs& a, const RowPass& 
 // the scratch region kept in LDS (each pass that reads it is the next one
 // to use the previous pass's outputs, element by element), the row vectors
 // from gamma / beta, the result to y or to MXINT8 DDR words.
-template <uint32_t kEntry, bool kDdr, bool kCache>
-__global__ __launch_bounds__(256) void VecRowKernel(VecRowArgs args, VecRowDdr d, uint8_t* abuf,
+template <uint32_t kEntry, bool kDdr, bool kCache, uint32_t kT>
+__global__ __launch_bounds__(kT) void VecRowKernel(VecRowArgs args, VecRowDdr d, uint8_t* abuf,
                                                     uint32_t* fbuf, const uint32_t* pbuf,
                                                     const uint64_t* tbuf) {
   // LDS sized to the row: the pass outputs (n8 x 32), in DDR mode the
@@ -543,7 +543,7 @@ __global__ __launch_bounds__(256) void VecRowKernel(VecRowArgs args, VecRowDdr d
   if constexpr (kDdr && kEntry != kRowSoftmax) {
     // the row vectors, read by every quad's later passes, once into LDS
     const uint32_t cols = n8 * 8;
-    for (uint32_t c = threadIdx.x; c < cols; c += 256) {
+    for (uint32_t c = threadIdx.x; c < cols; c += kT) {
       sp[c] = d.gamma[c];
       if (kEntry == kRowLayerNorm) sp[cols + c] = d.beta[c];
     }
@@ -551,8 +551,8 @@ __global__ __launch_bounds__(256) void VecRowKernel(VecRowArgs args, VecRowDdr d
   }
   ring::Unroll<kPasses>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
-    RowQuadPass<kDdr, kCache>(a, RowPassOf(a, quad, i), i == 0, quad, d, abuf, fbuf, pbuf, tbuf,
-                              out, sp, sp, xs, tree, acc, rs0, rs1);
+    RowQuadPass<kDdr, kCache, kT>(a, RowPassOf(a, quad, i), i == 0, quad, d, abuf, fbuf, pbuf,
+                                  tbuf, out, sp, sp, xs, tree, acc, rs0, rs1);
   });
 }
 
@@ -628,47 +628,74 @@ int RowProgramSpans(const VecRowArgs& a, uint32_t quad, RowPassSpan* out) {
   return n;
 }
 
-template <bool kDdr, bool kCache>
+template <bool kDdr, bool kCache, uint32_t kT>
 const void* RowKernelFn(uint32_t entry) {
-  return entry == kRowSoftmax     ? (const void*)VecRowKernel<kRowSoftmax, kDdr, kCache>
-         : entry == kRowLayerNorm ? (const void*)VecRowKernel<kRowLayerNorm, kDdr, kCache>
-         : entry == kRowRmsNorm   ? (const void*)VecRowKernel<kRowRmsNorm, kDdr, kCache>
+  return entry == kRowSoftmax     ? (const void*)VecRowKernel<kRowSoftmax, kDdr, kCache, kT>
+         : entry == kRowLayerNorm ? (const void*)VecRowKernel<kRowLayerNorm, kDdr, kCache, kT>
+         : entry == kRowRmsNorm   ? (const void*)VecRowKernel<kRowRmsNorm, kDdr, kCache, kT>
                                   : nullptr;
 }
 
-// Workgroups of `fn` resident per CU at `lds` bytes of LDS (0 if unknown).
-int RowResident(const void* fn, size_t lds) {
+// Form f of the parallel row kernel: bit 0 keeps the DDR form's source rows
+// in LDS, bit 1 selects 1,024 threads per workgroup (else 256).
+template <bool kDdr>
+const void* RowFormFn(uint32_t entry, int f) {
+  if constexpr (kDdr) {
+    switch (f) {
+      case 0: return RowKernelFn<true, false, 256>(entry);
+      case 1: return RowKernelFn<true, true, 256>(entry);
+      case 2: return RowKernelFn<true, false, 1024>(entry);
+      default: return RowKernelFn<true, true, 1024>(entry);
+    }
+  } else {
+    return f & 2 ? RowKernelFn<false, false, 1024>(entry) : RowKernelFn<false, false, 256>(entry);
+  }
+}
+
+// Workgroups of `fn` resident per CU at `threads` and `lds` bytes (0 if unknown).
+int RowResident(const void* fn, int threads, size_t lds) {
   int n = 0;
   if (lds > 65536 &&
       hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 256, lds) != hipSuccess) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess) return 0;
   return n;
 }
 
-// The DDR form keeps the source rows in LDS (one read of them from HBM)
-// unless that LDS leaves the quads more than one round of the CUs and
-// without it they fit in one (measured, 4512 x 960 RMSNorm: 1,128 quads,
-// 4 resident per CU with the rows kept, 6 without: 36.7 -> 27.5 us; a quad
-// that reads its rows again pays a memory round trip per pass, which costs
-// more where the rounds do not change: LayerNorm 2048 x 768 24.5 -> 26.9 us,
-// softmax 24,960 x 192 37.4 -> 46.4 us).
-bool RowsCacheSource(uint32_t entry, uint32_t n8, uint32_t quads) {
-  static std::atomic<int> memo[3][kRowMaxWords + 1][2];  // residency + 1, 0: not yet known
+// The form a launch of `quads` workgroups runs in: the fewest rounds of the
+// CUs (from each form's residency, remembered per program and width); at
+// equal rounds the source rows kept in LDS (one read of them), then the
+// wider workgroup (more waves on each quad's chains).  Measured at model
+// shapes: RMSNorm 4512 x 960 (1,128 quads) has 4 workgroups per CU with the
+// rows kept and 6 without, and re-reading them went 36.7 -> 27.5 us; where
+// the rounds do not change a quad that reads its rows again pays a memory
+// round trip per pass (LayerNorm 2048 x 768 24.5 -> 26.9 us, softmax
+// 24,960 x 192 37.4 -> 46.4 us when forced).
+template <bool kDdr>
+int RowForm(uint32_t entry, uint32_t n8, uint32_t quads) {
+  static std::atomic<int> memo[2][3][kRowMaxWords + 1][4];  // residency + 1, 0: not yet known
   const int k = entry == kRowSoftmax ? 0 : entry == kRowLayerNorm ? 1 : 2;
-  int res[2];
-  for (int c = 0; c < 2; ++c) {
-    int v = memo[k][n8][c].load(std::memory_order_relaxed);
-    if (v == 0) {
-      const void* fn = c ? RowKernelFn<true, true>(entry) : RowKernelFn<true, false>(entry);
-      v = RowResident(fn, RowLdsBytes(n8, true, c != 0)) + 1;
-      memo[k][n8][c].store(v, std::memory_order_relaxed);
-    }
-    res[c] = v - 1;
-  }
   const uint64_t cus = (uint64_t)DeviceCus();
-  if (res[1] == 0 || res[0] == 0) return res[1] != 0;
-  return !(quads > cus * (uint64_t)res[1] && quads <= cus * (uint64_t)res[0]);
+  int best = -1;
+  uint64_t best_rounds = 0;
+  for (int f : {3, 1, 2, 0}) {  // the preference order at equal rounds
+    if (!kDdr && (f & 1)) continue;
+    std::atomic<int>& m = memo[kDdr][k][n8][f];
+    int v = m.load(std::memory_order_relaxed);
+    if (v == 0) {
+      v = RowResident(RowFormFn<kDdr>(entry, f), f & 2 ? 1024 : 256,
+                      RowLdsBytes(n8, kDdr, (f & 1) != 0)) + 1;
+      m.store(v, std::memory_order_relaxed);
+    }
+    if (v == 1) continue;
+    const uint64_t slots = cus * (uint64_t)(v - 1);
+    const uint64_t rounds = (quads + slots - 1) / slots;
+    if (best < 0 || rounds < best_rounds) {
+      best = f;
+      best_rounds = rounds;
+    }
+  }
+  return best < 0 ? (kDdr ? 1 : 0) : best;
 }
 
 template <bool kDdr>
@@ -677,18 +704,17 @@ hipError_t LaunchRowKernel(const VecRowArgs& a, const VecRowDdr& d, uint8_t* abu
                            bool serial = false) {
   if (a.rows_q == 0 || a.n8 == 0 || a.n8 > kRowMaxWords || (kDdr && serial))
     return hipErrorInvalidValue;
-  const bool cache = kDdr && RowsCacheSource(a.entry, a.n8, a.rows_q);
-  const size_t lds = RowLdsBytes(a.n8, kDdr, cache);
+  const int form = serial ? 0 : RowForm<kDdr>(a.entry, a.n8, a.rows_q);
+  const size_t lds = RowLdsBytes(a.n8, kDdr, (form & 1) != 0);
+  const uint32_t threads = form & 2 ? 1024 : 256;
   const void* fn;
   if (serial)
     fn = a.entry == kRowSoftmax     ? (const void*)VecRowSerialKernel<kRowSoftmax>
          : a.entry == kRowLayerNorm ? (const void*)VecRowSerialKernel<kRowLayerNorm>
          : a.entry == kRowRmsNorm   ? (const void*)VecRowSerialKernel<kRowRmsNorm>
                                     : nullptr;
-  else if constexpr (kDdr)
-    fn = cache ? RowKernelFn<true, true>(a.entry) : RowKernelFn<true, false>(a.entry);
   else
-    fn = RowKernelFn<false, false>(a.entry);
+    fn = RowFormFn<kDdr>(a.entry, form);
   if (fn == nullptr) return hipErrorInvalidValue;
   if (lds > 65536) {  // rows of more than about 1900 columns
     const hipError_t err =
@@ -700,7 +726,7 @@ hipError_t LaunchRowKernel(const VecRowArgs& a, const VecRowDdr& d, uint8_t* abu
     return hipLaunchKernel(fn, dim3(1), dim3(256), params, lds, stream);
   }
   void* params[] = {(void*)&a, (void*)&d, (void*)&abuf, (void*)&fbuf, (void*)&pbuf, (void*)&tbuf};
-  return hipLaunchKernel(fn, dim3(a.rows_q), dim3(256), params, lds, stream);
+  return hipLaunchKernel(fn, dim3(a.rows_q), dim3(threads), params, lds, stream);
 }
 
 hipError_t LaunchVecRows(const VecRowArgs& a, uint8_t* abuf, uint32_t* fbuf, const uint32_t* pbuf,

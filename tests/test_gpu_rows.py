@@ -5,11 +5,14 @@ and 4512 rows), LayerNorm at the SigLIP width (768), softmax over 141 of 192
 keys, fp32 and MXINT8 outputs, a last quad with fewer than 4 rows, and the
 argument checks.  The MXINT8 words feed hb_linear as its A.
 
-Both forms of the kernel run: with the source rows kept in LDS (the smaller
-cases) and read again by each pass that takes them, which the library picks
-when that lets the quads fit in one round of the CUs (on a 256-CU MI355X:
-RMSNorm 4512 x 960, 1,128 quads, 4 resident per CU with the rows kept and 6
-without; LayerNorm 6000 x 768, 1,500 quads, 5 and 7)."""
+Every form of the kernel runs.  The library picks, per launch, the form
+with the fewest rounds of the CUs: the source rows kept in LDS or read again
+by each pass that takes them, 256 or 1,024 threads per quad.  On a 256-CU
+MI355X: up to 512 quads (two per CU) run 1,024 threads with the rows kept
+(most cases here); RMSNorm 3001 x 960 (751 quads) and softmax 24,960 x 192
+run 256 threads with the rows kept; RMSNorm 4512 x 960 (1,128 quads, 4
+resident per CU with the rows kept and 6 without) and LayerNorm 6000 x 768
+(1,500 quads, 5 and 7) run 256 threads reading the rows again."""
 from __future__ import annotations
 
 import sys
@@ -102,7 +105,7 @@ def activations(rng, rows, cols, scale=1.0):
 
 
 @pytest.mark.parametrize("rows,quantize", [(141, True), (141, False), (4512, True), (4512, False),
-                                          (3, True)])
+                                          (3001, False), (3, True)])
 def test_rmsnorm_smolvla_width(gpu, rows, quantize):
     rng = np.random.default_rng(rows + quantize)
     cols = 960
@@ -125,7 +128,8 @@ def test_layernorm_siglip_width(gpu, rows, quantize):
 
 
 @pytest.mark.parametrize("rows,cols,valid,quantize", [(50, 192, 141, False), (50, 192, 141, True),
-                                                      (241, 544, 544, True), (7, 64, 0, False)])
+                                                      (241, 544, 544, True), (7, 64, 0, False),
+                                                      (24960, 192, 192, True)])
 def test_softmax_attention_rows(gpu, rows, cols, valid, quantize):
     rng = np.random.default_rng(200 + rows + valid)
     x = activations(rng, rows, cols, 4.0)

@@ -652,13 +652,26 @@ const void* RowFormFn(uint32_t entry, int f) {
   }
 }
 
-// Workgroups of `fn` resident per CU at `threads` and `lds` bytes (0 if unknown).
+// Workgroups of `fn` resident per CU at `threads` and `lds` bytes (0 if the
+// form cannot run).  A form past the device's LDS per workgroup is not
+// asked about, and a failed query's error is cleared, so that it does not
+// surface at the caller's next HIP call.
 int RowResident(const void* fn, int threads, size_t lds) {
-  int n = 0;
-  if (lds > 65536 &&
-      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  int dev = 0, max_lds = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) !=
+          hipSuccess) {
+    (void)hipGetLastError();
     return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess) return 0;
+  }
+  if (lds > (size_t)max_lds) return 0;
+  int n = 0;
+  if ((lds > 65536 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)lds) != hipSuccess) ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
   return n;
 }
 

@@ -636,8 +636,14 @@ const void* RowKernelFn(uint32_t entry) {
                                   : nullptr;
 }
 
-// Form f of the parallel row kernel: bit 0 keeps the DDR form's source rows
-// in LDS, bit 1 selects 1,024 threads per workgroup (else 256).
+// Form f of the parallel row kernel, f = 2 * shape + kept: kept (DDR form
+// only) keeps the source rows in LDS; shape 0, 1, 2 is 256, 1,024 or 128
+// threads per quad (one quad per workgroup).
+constexpr int kRowForms = 6;
+constexpr uint32_t RowFormThreads(int f) {
+  return f >> 1 == 1 ? 1024u : f >> 1 == 2 ? 128u : 256u;
+}
+
 template <bool kDdr>
 const void* RowFormFn(uint32_t entry, int f) {
   if constexpr (kDdr) {
@@ -645,10 +651,16 @@ const void* RowFormFn(uint32_t entry, int f) {
       case 0: return RowKernelFn<true, false, 256>(entry);
       case 1: return RowKernelFn<true, true, 256>(entry);
       case 2: return RowKernelFn<true, false, 1024>(entry);
-      default: return RowKernelFn<true, true, 1024>(entry);
+      case 3: return RowKernelFn<true, true, 1024>(entry);
+      case 4: return RowKernelFn<true, false, 128>(entry);
+      default: return RowKernelFn<true, true, 128>(entry);
     }
   } else {
-    return f & 2 ? RowKernelFn<false, false, 1024>(entry) : RowKernelFn<false, false, 256>(entry);
+    switch (f >> 1) {
+      case 0: return RowKernelFn<false, false, 256>(entry);
+      case 1: return RowKernelFn<false, false, 1024>(entry);
+      default: return RowKernelFn<false, false, 128>(entry);
+    }
   }
 }
 
@@ -677,35 +689,46 @@ int RowResident(const void* fn, int threads, size_t lds) {
 
 // The form a launch of `quads` workgroups runs in: the fewest rounds of the
 // CUs (from each form's residency, remembered per program and width); at
-// equal rounds the source rows kept in LDS (one read of them), then the
-// wider workgroup (more waves on each quad's chains).  Measured at model
-// shapes: RMSNorm 4512 x 960 (1,128 quads) has 4 workgroups per CU with the
-// rows kept and 6 without, and re-reading them went 36.7 -> 27.5 us; where
-// the rounds do not change a quad that reads its rows again pays a memory
-// round trip per pass (LayerNorm 2048 x 768 24.5 -> 26.9 us, softmax
-// 24,960 x 192 37.4 -> 46.4 us when forced).
+// equal rounds the most waves the launch places on a CU, then the source
+// rows kept in LDS (one read of them), then more threads per quad.
+// Measured at model shapes: RMSNorm 4512 x 960 (1,128 quads) has 4
+// workgroups per CU with the rows kept and 6 without, and re-reading them
+// went 36.7 -> 27.5 us; where the rounds do not change a quad that reads its
+// rows again pays a memory round trip per pass (LayerNorm 2048 x 768 24.5 ->
+// 26.9 us, softmax 24,960 x 192 37.4 -> 46.4 us when forced); launches of up
+// to two quads per CU take 1,024 threads (LayerNorm 2048 x 768 24.1 -> 15.3
+// us, RMSNorm 141 x 960 17.4 -> 9.3 us).
 template <bool kDdr>
 int RowForm(uint32_t entry, uint32_t n8, uint32_t quads) {
-  static std::atomic<int> memo[2][3][kRowMaxWords + 1][4];  // residency + 1, 0: not yet known
+  static std::atomic<int> memo[2][3][kRowMaxWords + 1][kRowForms];  // residency + 1; 0: unknown
   const int k = entry == kRowSoftmax ? 0 : entry == kRowLayerNorm ? 1 : 2;
   const uint64_t cus = (uint64_t)DeviceCus();
   int best = -1;
-  uint64_t best_rounds = 0;
-  for (int f : {3, 1, 2, 0}) {  // the preference order at equal rounds
+  uint64_t best_rounds = 0, best_waves = 0;
+  for (int f = 0; f < kRowForms; ++f) {
     if (!kDdr && (f & 1)) continue;
     std::atomic<int>& m = memo[kDdr][k][n8][f];
     int v = m.load(std::memory_order_relaxed);
     if (v == 0) {
-      v = RowResident(RowFormFn<kDdr>(entry, f), f & 2 ? 1024 : 256,
+      v = RowResident(RowFormFn<kDdr>(entry, f), RowFormThreads(f),
                       RowLdsBytes(n8, kDdr, (f & 1) != 0)) + 1;
       m.store(v, std::memory_order_relaxed);
     }
     if (v == 1) continue;
     const uint64_t slots = cus * (uint64_t)(v - 1);
     const uint64_t rounds = (quads + slots - 1) / slots;
-    if (best < 0 || rounds < best_rounds) {
+    // waves the launch places on a CU at once
+    const uint64_t per_cu = std::min<uint64_t>((uint64_t)(v - 1), (quads + cus - 1) / cus);
+    const uint64_t waves = per_cu * RowFormThreads(f) / 64;
+    // at equal rounds and waves: the rows kept, then more threads per quad
+    const bool tie = rounds == best_rounds && waves == best_waves;
+    const bool pref = tie && ((f & 1) != (best & 1) ? (f & 1) != 0
+                                                    : RowFormThreads(f) > RowFormThreads(best));
+    if (best < 0 || rounds < best_rounds || (rounds == best_rounds && waves > best_waves) ||
+        pref) {
       best = f;
       best_rounds = rounds;
+      best_waves = waves;
     }
   }
   return best < 0 ? (kDdr ? 1 : 0) : best;
@@ -719,7 +742,7 @@ hipError_t LaunchRowKernel(const VecRowArgs& a, const VecRowDdr& d, uint8_t* abu
     return hipErrorInvalidValue;
   const int form = serial ? 0 : RowForm<kDdr>(a.entry, a.n8, a.rows_q);
   const size_t lds = RowLdsBytes(a.n8, kDdr, (form & 1) != 0);
-  const uint32_t threads = form & 2 ? 1024 : 256;
+  const uint32_t threads = RowFormThreads(form);
   const void* fn;
   if (serial)
     fn = a.entry == kRowSoftmax     ? (const void*)VecRowSerialKernel<kRowSoftmax>

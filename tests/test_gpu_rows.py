@@ -7,10 +7,10 @@ argument checks.  The MXINT8 words feed hb_linear as its A.
 
 Every form of the kernel runs.  The library picks, per launch, the form
 with the fewest rounds of the CUs: the source rows kept in LDS or read again
-by each pass that takes them, 256 or 1,024 threads per quad.  On a 256-CU
+by each pass that takes them, 128, 256 or 1,024 threads per quad.  On a 256-CU
 MI355X: up to 512 quads (two per CU) run 1,024 threads with the rows kept
-(most cases here); RMSNorm 3001 x 960 (751 quads) and softmax 24,960 x 192
-run 256 threads with the rows kept; RMSNorm 4512 x 960 (1,128 quads, 4
+(most cases here); RMSNorm 3001 x 960 (751 quads) runs 256 threads and
+softmax 24,960 x 192 128 threads with the rows kept; RMSNorm 4512 x 960 (1,128 quads, 4
 resident per CU with the rows kept and 6 without) and LayerNorm 6000 x 768
 (1,500 quads, 5 and 7) run 256 threads reading the rows again."""
 from __future__ import annotations

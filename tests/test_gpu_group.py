@@ -192,3 +192,51 @@ def test_group_rejections(gpu):
         with pytest.raises(hb.HbError) as err:
             hb.linear_group(descs, gpu)
         assert err.value.code == hb.HB_EINVAL
+
+
+def test_group_sparsedrive_head_qkv(gpu):
+    """The SparseDrive-S head's temporal attention projections as one group
+    (tools/compiler/sparsedrive_head.cpp:800-886): q over the 928 anchor
+    rows, k and v over 608 temporal rows with their own A, each 512 -> 512
+    W8 with both planes packed as weight panels, bias (ADDP) and the
+    requantize.  Each layer of the group meets the oracle at the fast-mode
+    tolerance, and so do the same layers launched one by one."""
+    rng = np.random.default_rng(520)
+    n, kb = 512, 16
+    layers = []
+    for m in (928, 608, 608):
+        a = helpers.activations(rng, m, kb * 32)[1]
+        planes, modes = w8_planes(rng, n, kb)
+        bias = helpers.random_fp32_words(rng, (n,), 118, 126)
+        pan, src = [], [dev(p) for p in planes]  # src stays alive until the packers ran
+        for p in src:
+            t = torch.empty((hb.panel_bytes(n, kb),), dtype=torch.uint8, device=DEV)
+            hb.pack_weights(p, n, kb, t, ctx=gpu)
+            pan.append(t)
+        layers.append(dict(m=m, a=a, a_d=dev(a), planes=planes, modes=modes, bias=bias,
+                           bias_d=dev(bias.view(np.float32)), pan=pan, src=src))
+    gpu.synchronize()
+
+    def outputs():
+        return [(torch.zeros((ly["m"], n), dtype=torch.float32, device=DEV),
+                 torch.zeros(((ly["m"] + 3) // 4 * (n // 32), 144), dtype=torch.uint8, device=DEV))
+                for ly in layers]
+
+    def descs(outs):
+        return [hb.linear_desc(ly["m"], n, kb, ly["a_d"], ly["pan"], ly["modes"], c,
+                               ops=[(hb.EP_ADDP, ly["bias_d"])], q_out=q, mode=hb.FAST,
+                               panels=True)
+                for ly, (c, q) in zip(layers, outs)]
+
+    say("group head q/k/v", dict(m=(928, 608, 608), n=n, kb=kb))
+    sep = outputs()
+    for d in descs(sep):
+        hb.launch(d, gpu)
+    grp = outputs()
+    hb.linear_group(descs(grp), gpu)
+    torch.cuda.synchronize()
+    for ly, (c1, q1), (c2, q2) in zip(layers, sep, grp):
+        want, wq = helpers.oracle_linear_mt(ly["m"], n, kb, ly["a"], ly["planes"], ly["modes"],
+                                            ops=[(hb.EP_ADDP, ly["bias"])], quantize=True)
+        for c, q in ((c1, q1), (c2, q2)):
+            helpers.check_fast(host(c).view(np.uint32).copy(), want, host(q).copy(), wq)
